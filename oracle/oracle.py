@@ -1,0 +1,219 @@
+"""ctypes wrapper over oracle/liboracle.so — TEST INFRASTRUCTURE ONLY.
+
+Used by tests/, by __graft_entry__.smoke() as the checker, and by bench.py's
+cpu_baseline leg. The product (phyz_amd) never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libphyz_ref_host.so")
+
+_lib = None
+
+dp = C.POINTER(C.c_double)
+fp = C.POINTER(C.c_float)
+u64p = C.POINTER(C.c_uint64)
+
+
+def build(quiet: bool = True) -> None:
+    """Compile the oracle (and oracle/_ref where the reference tree exists)."""
+    out = subprocess.run(["make", "-C", HERE, "all"], capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
+    if not quiet:
+        print(out.stdout)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.orc_model_create.restype = C.c_void_p
+        L.orc_model_create.argtypes = [dp, C.c_int, C.c_int, C.c_int, dp, C.c_double, C.c_char_p, C.c_int]
+        L.orc_model_destroy.argtypes = [C.c_void_p]
+        L.orc_set_contact.argtypes = [C.c_void_p, dp, C.c_double, C.c_double]
+        L.orc_set_pd.argtypes = [C.c_void_p, dp, C.c_int]
+        L.orc_set_noise.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_double, C.c_double, C.POINTER(C.c_int), C.c_int]
+        L.orc_aba.argtypes = [C.c_void_p, dp, dp, dp, dp, dp, C.c_int]
+        L.orc_aba_f32.argtypes = [C.c_void_p, fp, fp, fp, fp, fp]
+        L.orc_rnea.argtypes = [C.c_void_p, dp, dp, dp, dp, dp]
+        L.orc_qdd_f32.argtypes = [C.c_void_p, fp, fp, fp, fp]
+        L.orc_crba.argtypes = [C.c_void_p, dp, dp]
+        L.orc_generalized_forces.argtypes = [C.c_void_p, dp, dp, dp, dp]
+        L.orc_fk.argtypes = [C.c_void_p, dp, dp, dp]
+        L.orc_contact.argtypes = [C.c_void_p, dp, dp, dp, dp]
+        L.orc_integrate.argtypes = [C.c_void_p, dp, dp, dp]
+        L.orc_world_seed.restype = C.c_uint64
+        L.orc_world_seed.argtypes = [C.c_uint64, C.c_uint64]
+        L.orc_quat_exp_log.argtypes = [dp, dp, dp]
+        L.orc_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, dp, dp, dp, u64p, dp, dp, C.c_int, C.c_int]
+        L.orc_count_ops.argtypes = [C.c_void_p, dp, dp, dp, dp, C.c_uint64, C.c_int, u64p]
+        _lib = L
+    return _lib
+
+
+def _d(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float64 and a.flags.c_contiguous
+    return a.ctypes.data_as(dp)
+
+
+PHASES = ("noise", "pd", "contact", "aba", "integrate")
+COUNTERS = ("add", "mul", "div", "sqrt", "trans", "other")
+
+
+class Oracle:
+    """f64 CPU restatement of one model's step (see oracle/phz_oracle.hpp)."""
+
+    def __init__(self, model, contact=None, pd=None, noise=None):
+        from phyz_amd.model import pack_bodies
+        L = lib()
+        self.model = model
+        self.nb, self.nq, self.nv = model.nbodies, model.nq, model.nv
+        table = np.ascontiguousarray(pack_bodies(model))
+        g = np.ascontiguousarray(model.gravity, dtype=np.float64)
+        err = C.create_string_buffer(256)
+        h = L.orc_model_create(_d(table), self.nb, self.nq, self.nv, _d(g), float(model.dt), err, 256)
+        if not h:
+            raise ValueError(err.value.decode())
+        self._h = C.c_void_p(h)
+        self.n_pd = 0
+        self.noise = None
+        if contact is not None:
+            geom, ground_h, mu = contact
+            L.orc_set_contact(self._h, _d(np.ascontiguousarray(geom, dtype=np.float64)), float(ground_h), float(mu))
+        if pd is not None:
+            t = np.ascontiguousarray(pd, dtype=np.float64)
+            self.n_pd = t.shape[0]
+            L.orc_set_pd(self._h, _d(t), self.n_pd)
+        if noise is not None:
+            seed, dist, a, b, dofs = noise
+            arr = (C.c_int * len(dofs))(*dofs)
+            L.orc_set_noise(self._h, int(seed), int(dist), float(a), float(b), arr, len(dofs))
+            self.noise = noise
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            _lib.orc_model_destroy(self._h)
+            self._h = None
+
+    # ── single-world calls ──
+    def aba(self, q, v, ctrl, ext=None, dense=False):
+        out = np.zeros(self.nv)
+        lib().orc_aba(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)),
+                      _d(np.ascontiguousarray(ctrl, dtype=np.float64)),
+                      _d(None if ext is None else np.ascontiguousarray(ext, dtype=np.float64)), _d(out), 1 if dense else 0)
+        return out
+
+    def aba_f32(self, q, v, ctrl, ext=None):
+        f = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+        out = np.zeros(self.nv, dtype=np.float32)
+        qq, vv, cc = f(q), f(v), f(ctrl)
+        ee = None if ext is None else f(ext)
+        lib().orc_aba_f32(self._h, qq.ctypes.data_as(fp), vv.ctypes.data_as(fp), cc.ctypes.data_as(fp),
+                          None if ee is None else ee.ctypes.data_as(fp), out.ctypes.data_as(fp))
+        return out
+
+    def qdd_f32(self, q, v, ctrl):
+        """One step's qdd (with contact when enabled) computed in f32 arithmetic."""
+        f = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+        out = np.zeros(self.nv, dtype=np.float32)
+        qq, vv, cc = f(q), f(v), f(ctrl)
+        lib().orc_qdd_f32(self._h, qq.ctypes.data_as(fp), vv.ctypes.data_as(fp), cc.ctypes.data_as(fp),
+                          out.ctypes.data_as(fp))
+        return out.astype(np.float64)
+
+    def rnea(self, q, v, qdd, ext=None):
+        out = np.zeros(self.nv)
+        lib().orc_rnea(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)),
+                       _d(np.ascontiguousarray(qdd, dtype=np.float64)),
+                       _d(None if ext is None else np.ascontiguousarray(ext, dtype=np.float64)), _d(out))
+        return out
+
+    def crba(self, q):
+        out = np.zeros((self.nv, self.nv))
+        lib().orc_crba(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(out))
+        return out
+
+    def generalized_forces(self, q, v, ctrl):
+        out = np.zeros(self.nv)
+        lib().orc_generalized_forces(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)),
+                                     _d(np.ascontiguousarray(v, dtype=np.float64)),
+                                     _d(np.ascontiguousarray(ctrl, dtype=np.float64)), _d(out))
+        return out
+
+    def fk(self, q, v):
+        out = np.zeros((self.nb, 18))
+        lib().orc_fk(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)), _d(out))
+        return out
+
+    def contact(self, q, v):
+        ext = np.zeros((self.nb, 6))
+        rows = np.zeros((self.nb, 8))
+        rc = lib().orc_contact(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)),
+                               _d(np.ascontiguousarray(v, dtype=np.float64)), _d(ext), _d(rows))
+        if rc != 0:
+            raise RuntimeError("contact not enabled on this oracle")
+        return ext, rows
+
+    def integrate(self, q, v, qdd):
+        q = np.array(q, dtype=np.float64)
+        v = np.array(v, dtype=np.float64)
+        lib().orc_integrate(self._h, _d(q), _d(v), _d(np.ascontiguousarray(qdd, dtype=np.float64)))
+        return q, v
+
+    # ── batch stepping ──
+    def rng_states(self, nworld: int) -> np.ndarray:
+        if self.noise is None:
+            return None
+        seed = int(self.noise[0])
+        return np.array([lib().orc_world_seed(seed, w) for w in range(nworld)], dtype=np.uint64)
+
+    def step_batch(self, q, v, ctrl, nsteps, targets=None, rng=None, threads=1, dense=False, want_contacts=False):
+        """Advance world-major (q, v, ctrl) in place by nsteps. Returns (qdd_last, contact_rows|None)."""
+        nworld = q.shape[0]
+        assert q.dtype == np.float64 and q.flags.c_contiguous
+        qdd = np.zeros((nworld, self.nv))
+        rows = np.zeros((nworld, self.nb, 8)) if want_contacts else None
+        tg = None
+        if self.n_pd:
+            tg = np.ascontiguousarray(targets, dtype=np.float64)
+        rp = None
+        if rng is not None:
+            assert rng.dtype == np.uint64 and rng.flags.c_contiguous
+            rp = rng.ctypes.data_as(u64p)
+        lib().orc_step_batch(self._h, nworld, int(nsteps), _d(q), _d(v), _d(ctrl), _d(tg), rp, _d(qdd),
+                             _d(rows), int(threads), 1 if dense else 0)
+        return qdd, rows
+
+    def count_ops(self, q, v, ctrl, targets=None, rng_state=1, dense=False):
+        """Per-phase operation counts of one world-step: {phase: {counter: n}}."""
+        c = np.zeros(len(PHASES) * len(COUNTERS), dtype=np.uint64)
+        tg = np.ascontiguousarray(targets if targets is not None else np.zeros(max(self.n_pd, 1)), dtype=np.float64)
+        lib().orc_count_ops(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)),
+                            _d(np.ascontiguousarray(ctrl, dtype=np.float64)), _d(tg), int(rng_state), 1 if dense else 0,
+                            c.ctypes.data_as(u64p))
+        c = c.reshape(len(PHASES), len(COUNTERS))
+        return {p: {k: int(c[i, j]) for j, k in enumerate(COUNTERS)} for i, p in enumerate(PHASES)}
+
+
+def world_seed(seed: int, world: int) -> int:
+    return int(lib().orc_world_seed(int(seed), int(world)))
+
+
+def quat_exp_log(w):
+    q = np.zeros(4)
+    l = np.zeros(3)
+    lib().orc_quat_exp_log(_d(np.ascontiguousarray(w, dtype=np.float64)), _d(q), _d(l))
+    return q, l

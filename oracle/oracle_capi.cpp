@@ -1,0 +1,218 @@
+// oracle_capi.cpp — C ABI over phz_oracle.hpp for the Python test harness.
+//
+// TEST INFRASTRUCTURE ONLY (see phz_oracle.hpp). Loaded by tests/ and by the
+// cpu_baseline leg of bench.py through oracle/oracle.py; never by the product.
+//
+// Arrays are world-major, matching the reference wire format
+// (crates/phyz-gpu/src/layout.rs:340-356): q[w * nq + j], v[w * nv + j].
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "phz_oracle.hpp"
+
+using namespace phzo;
+
+struct orc_model {
+  Model m;
+};
+
+static void set_err(char* err, int len, const char* msg) {
+  if (err && len > 0) { std::snprintf(err, (size_t)len, "%s", msg); }
+}
+
+extern "C" {
+
+orc_model* orc_model_create(const double* bodies, int nb, int nq, int nv, const double* g, double dt, char* err,
+                            int errlen) {
+  auto* o = new orc_model();
+  const char* e = model_from_table(o->m, bodies, nb, nq, nv, g, dt);
+  if (e[0]) { set_err(err, errlen, e); delete o; return nullptr; }
+  return o;
+}
+void orc_model_destroy(orc_model* o) { delete o; }
+
+int orc_set_contact(orc_model* o, const double* geom, double ground_h, double mu) {
+  geoms_from_table(o->m, geom);
+  o->m.contact = true;
+  o->m.ground_h = ground_h;
+  o->m.mu = mu;
+  return 0;
+}
+int orc_set_pd(orc_model* o, const double* dofs, int n) {
+  o->m.pd.clear();
+  for (int i = 0; i < n; i++) {
+    const double* r = dofs + i * PD_STRIDE;
+    o->m.pd.push_back(PdDof{(int)r[0], (int)r[1], r[2], r[3], r[4]});
+  }
+  return 0;
+}
+int orc_set_noise(orc_model* o, uint64_t seed, int dist, double a, double b, const int* vidx, int n) {
+  o->m.noise = n > 0;
+  o->m.noise_seed = seed;
+  o->m.noise_dist = dist;
+  o->m.noise_a = a;
+  o->m.noise_b = b;
+  o->m.noise_dofs.assign(vidx, vidx + n);
+  return 0;
+}
+
+static std::vector<SV<double>> ext_from(const Model& m, const double* ext) {
+  std::vector<SV<double>> e(m.nb);
+  for (int i = 0; i < m.nb; i++)
+    for (int k = 0; k < 6; k++) e[i].set(k, ext[i * 6 + k]);
+  return e;
+}
+
+// qdd = ABA(q, v, ctrl, ext). mode 0: aba_struct, 1: aba_dense.
+int orc_aba(orc_model* o, const double* q, const double* v, const double* ctrl, const double* ext, double* qdd, int mode) {
+  std::vector<SV<double>> e;
+  if (ext) e = ext_from(o->m, ext);
+  if (mode == 1) aba_dense<double>(o->m, q, v, ctrl, ext ? e.data() : nullptr, qdd);
+  else aba_struct<double>(o->m, q, v, ctrl, ext ? e.data() : nullptr, qdd);
+  return 0;
+}
+// f32 arithmetic through the same restatement (diagnostics: f32 rounding floor).
+int orc_aba_f32(orc_model* o, const float* q, const float* v, const float* ctrl, const float* ext, float* qdd) {
+  std::vector<SV<float>> e(o->m.nb);
+  if (ext) for (int i = 0; i < o->m.nb; i++) for (int k = 0; k < 6; k++) e[i].set(k, ext[i * 6 + k]);
+  aba_struct<float>(o->m, q, v, ctrl, ext ? e.data() : nullptr, qdd);
+  return 0;
+}
+// FK + contact + ABA entirely in f32 arithmetic (diagnostic: the f32 rounding
+// floor of one step's qdd for a given state and control).
+int orc_qdd_f32(orc_model* o, const float* q, const float* v, const float* ctrl, float* qdd) {
+  const Model& m = o->m;
+  std::vector<SV<float>> ext(m.nb);
+  if (m.contact) {
+    std::vector<FK<float>> fk(m.nb);
+    forward_kinematics<float>(m, q, v, fk.data());
+    ground_contact<float>(m, fk.data(), ext.data(), nullptr);
+  }
+  aba_struct<float>(m, q, v, ctrl, m.contact ? ext.data() : nullptr, qdd);
+  return 0;
+}
+// tau = RNEA(q, v, qdd, ext): pure rigid-body inverse dynamics, no passive terms.
+int orc_rnea(orc_model* o, const double* q, const double* v, const double* qdd, const double* ext, double* tau) {
+  std::vector<SV<double>> e;
+  if (ext) e = ext_from(o->m, ext);
+  rnea<double>(o->m, q, v, qdd, ext ? e.data() : nullptr, tau);
+  return 0;
+}
+// Joint-space inertia, armature and dt*damping on the diagonal (nv x nv).
+int orc_crba(orc_model* o, const double* q, double* M) {
+  crba<double>(o->m, q, M);
+  return 0;
+}
+// Passive + ctrl generalized force (actuation.rs:18-39 subset).
+int orc_generalized_forces(orc_model* o, const double* q, const double* v, const double* ctrl, double* qfrc) {
+  generalized_forces<double>(o->m, q, v, ctrl, qfrc);
+  return 0;
+}
+// FK rows per body: w_rot (body->world, row-major 9), w_pos (3), body-frame
+// spatial velocity (6) — 18 doubles.
+int orc_fk(orc_model* o, const double* q, const double* v, double* out) {
+  std::vector<FK<double>> fk(o->m.nb);
+  forward_kinematics<double>(o->m, q, v, fk.data());
+  for (int i = 0; i < o->m.nb; i++) {
+    double* r = out + i * 18;
+    for (int a = 0; a < 3; a++) for (int b = 0; b < 3; b++) r[a * 3 + b] = fk[i].w_rot.m[a][b];
+    for (int k = 0; k < 3; k++) r[9 + k] = fk[i].w_pos[k];
+    for (int k = 0; k < 6; k++) r[12 + k] = fk[i].vel.get(k);
+  }
+  return 0;
+}
+int orc_contact(orc_model* o, const double* q, const double* v, double* ext_out, double* rows_out) {
+  if (!o->m.contact) return 1;
+  std::vector<FK<double>> fk(o->m.nb);
+  std::vector<SV<double>> ext(o->m.nb);
+  forward_kinematics<double>(o->m, q, v, fk.data());
+  ground_contact<double>(o->m, fk.data(), ext.data(), rows_out);
+  for (int i = 0; i < o->m.nb; i++) for (int k = 0; k < 6; k++) ext_out[i * 6 + k] = ext[i].get(k);
+  return 0;
+}
+int orc_integrate(orc_model* o, double* q, double* v, const double* qdd) {
+  integrate<double>(o->m, q, v, qdd);
+  return 0;
+}
+uint64_t orc_world_seed(uint64_t seed, uint64_t world) { return world_seed(seed, world); }
+
+int orc_quat_exp_log(const double* w, double* quat_out, double* log_out) {
+  Q<double> qq = quat_exp(V3<double>{w[0], w[1], w[2]});
+  quat_out[0] = qq.w; quat_out[1] = qq.x; quat_out[2] = qq.y; quat_out[3] = qq.z;
+  V3<double> l = quat_log(qq);
+  log_out[0] = l.x; log_out[1] = l.y; log_out[2] = l.z;
+  return 0;
+}
+
+// Step nworld worlds nsteps times, in place. rng: per-world xorshift state
+// (nullable when noise is off). targets: [nworld][n_pd]. qdd_last:
+// [nworld][nv] (nullable). contact_rows: [nworld][nb][8] of the last step
+// (nullable). threads <= 0 uses hardware concurrency. mode 0 struct, 1 dense.
+int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, double* ctrl, const double* targets,
+                   uint64_t* rng, double* qdd_last, double* contact_rows, int threads, int mode) {
+  const Model& m = o->m;
+  if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+  threads = std::min(threads, std::max(1, nworld));
+  const int npd = (int)m.pd.size();
+  auto work = [&](int w0, int w1) {
+    WorldScratch<double> ws;
+    std::vector<double> rows(m.nb * CONTACT_ROW);
+    for (int w = w0; w < w1; w++) {
+      double* qw = q + (size_t)w * m.nq;
+      double* vw = v + (size_t)w * m.nv;
+      double* cw = ctrl + (size_t)w * m.nv;
+      const double* tw = npd ? targets + (size_t)w * npd : nullptr;
+      uint64_t* rw = rng ? rng + w : nullptr;
+      for (int s = 0; s < nsteps; s++) {
+        double* cr = (contact_rows && s == nsteps - 1) ? contact_rows + (size_t)w * m.nb * CONTACT_ROW : nullptr;
+        step_world<double>(m, qw, vw, cw, tw, rw, ws, cr, mode == 1);
+      }
+      if (qdd_last && nsteps > 0) std::memcpy(qdd_last + (size_t)w * m.nv, ws.qdd.data(), sizeof(double) * m.nv);
+    }
+  };
+  if (threads == 1) { work(0, nworld); return 0; }
+  std::vector<std::thread> pool;
+  int chunk = (nworld + threads - 1) / threads;
+  for (int t = 0; t < threads; t++) {
+    int w0 = t * chunk, w1 = std::min(nworld, w0 + chunk);
+    if (w0 >= w1) break;
+    pool.emplace_back(work, w0, w1);
+  }
+  for (auto& th : pool) th.join();
+  return 0;
+}
+
+// Count operations of one world-step at the given state (struct formulation
+// when mode 0, dense when mode 1). counts: 5 phases x 6 counters
+// (add, mul, div, sqrt, trans, other), phases: noise, pd, contact, aba, integrate.
+int orc_count_ops(orc_model* o, const double* q0, const double* v0, const double* ctrl0, const double* targets0,
+                  uint64_t rng_state, int mode, uint64_t* counts) {
+  const Model& m = o->m;
+  std::vector<OpScalar> q(m.nq), v(m.nv), ctrl(m.nv), tg(m.pd.size());
+  for (int j = 0; j < m.nq; j++) q[j] = OpScalar::state(q0[j]);
+  for (int j = 0; j < m.nv; j++) { v[j] = OpScalar::state(v0[j]); ctrl[j] = OpScalar::state(ctrl0[j]); }
+  for (size_t d = 0; d < m.pd.size(); d++) tg[d] = OpScalar::state(targets0[d]);
+  OpCount c;
+  OpCount* prev = op_counter();
+  op_counter() = &c;
+  OpCount last;
+  auto hook = [&](int phase) {
+    uint64_t* out = counts + phase * 6;
+    out[0] = c.add - last.add; out[1] = c.mul - last.mul; out[2] = c.div - last.div;
+    out[3] = c.sqrt - last.sqrt; out[4] = c.trans - last.trans; out[5] = c.other - last.other;
+    last = c;
+  };
+  WorldScratch<OpScalar> ws;
+  std::vector<OpScalar> rows(m.nb * CONTACT_ROW);
+  uint64_t r = rng_state;
+  step_world<OpScalar>(m, q.data(), v.data(), ctrl.data(), tg.data(), m.noise ? &r : nullptr, ws, nullptr, mode == 1,
+                       hook);
+  op_counter() = prev;
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+"""ctypes binding of libphyz_amd.so (the C ABI in include/phyz_amd.h).
+
+The library must be built in-tree (python -m phyz_amd.build); loading fails
+loudly when it is missing — there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libphyz_amd.so")
+
+_lib = None
+
+dp = C.POINTER(C.c_double)
+u32p = C.POINTER(C.c_uint32)
+u64p = C.POINTER(C.c_uint64)
+i64p = C.POINTER(C.c_int64)
+SIM = C.c_void_p
+
+# name -> (restype, argtypes); every symbol declared in include/phyz_amd.h.
+SIGNATURES = {
+    "phz_sim_create": (C.c_int, [dp, C.c_uint32, C.c_uint32, C.c_uint32, dp, C.c_double, C.c_uint32, C.c_int, C.c_int,
+                                 C.POINTER(C.c_void_p)]),
+    "phz_sim_destroy": (None, [SIM]),
+    "phz_last_error": (C.c_char_p, [SIM]),
+    "phz_set_model": (C.c_int, [SIM, dp, C.c_uint32, C.c_uint32, C.c_uint32, dp, C.c_double]),
+    "phz_enable_ground_contact": (C.c_int, [SIM, C.c_double, C.c_double, C.c_double, C.c_double, dp, u32p]),
+    "phz_enable_ground_contact_per_body": (C.c_int, [SIM, C.c_double, C.c_double, dp, dp, u32p]),
+    "phz_enable_pd_control": (C.c_int, [SIM, dp, C.c_uint32]),
+    "phz_set_position_targets": (C.c_int, [SIM, dp]),
+    "phz_enable_control_noise": (C.c_int, [SIM, C.c_uint64, C.c_int, C.c_double, C.c_double, u32p, C.c_uint32]),
+    "phz_load_states": (C.c_int, [SIM, dp, dp, dp]),
+    "phz_set_controls": (C.c_int, [SIM, dp]),
+    "phz_step": (C.c_int, [SIM]),
+    "phz_step_many": (C.c_int, [SIM, C.c_uint32]),
+    "phz_set_graphs_enabled": (C.c_int, [SIM, C.c_int]),
+    "phz_graphs_enabled": (C.c_int, [SIM]),
+    "phz_synchronize": (C.c_int, [SIM]),
+    "phz_readback_states": (C.c_int, [SIM, dp, dp]),
+    "phz_readback_contacts": (C.c_int, [SIM, dp]),
+    "phz_readback_controls": (C.c_int, [SIM, dp]),
+    "phz_readback_qdd": (C.c_int, [SIM, dp]),
+    "phz_readback_rng": (C.c_int, [SIM, u64p]),
+    "phz_load_rng": (C.c_int, [SIM, u64p]),
+    "phz_collidable_bodies": (C.c_int, [SIM]),
+    "phz_compile": (C.c_int, [SIM]),
+    "phz_time_step_many": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp]),
+    "phz_kernel_info": (C.c_int, [SIM, i64p]),
+}
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run `python -m phyz_amd.build` (hipcc, gfx950)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib

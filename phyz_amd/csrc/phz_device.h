@@ -1,0 +1,734 @@
+// phz_device.h — fused per-step device code for gfx950 (CDNA4).
+//
+// One lane advances one world. A launch runs `nsteps` steps with the world's
+// q, v and ctrl held in registers and touches HBM only to load the state at
+// the start and store it at the end. Each step is, in the reference's order
+// (crates/phyz-gpu/src/cuda/mod.rs:879-945):
+//   control noise -> PD servo -> FK + ground penalty contact -> ABA -> integrate
+//
+// The model is not read from memory: the host emits a `struct Model` of
+// constexpr tables (body tree, joint types, inertias, transforms, geometry,
+// gains) and compiles this header against it with hiprtc. Every loop over
+// bodies is unrolled at compile time (sfor/rfor below), so per-body state lives
+// in registers and zero / unit entries of axes, transforms and inertias fold
+// away (the kernel is built with -ffinite-math-only -fno-signed-zeros so that
+// x*0 and x+0 fold).
+//
+// Formulation (same equations as crates/phyz-rigid/src/aba.rs:117-368 and the
+// reference kernels crates/phyz-gpu/cuda/phyz_kernels.cu:1175-1421, structure
+// exploited):
+//   pass 1  X_i = X_J(q) X_ptj, v_i = X_i v_p + S qd, c_i = v_i x S qd,
+//           p_i = v_i x* (I_i v_i) - f_ext_i   (contact computed here, FK shared)
+//   pass 2  U = I_A S, D = S^T U + armature + dt damping, u = tau - S^T p_A;
+//           I_a = I_A - U D^-1 U^T, p_a = p_A + I_a c + U D^-1 u;
+//           I_A[p] += X^T I_a X (rotation then translation, symmetric blocks),
+//           p_A[p] += X^T p_a
+//   pass 3  a' = X a_p + c, qdd = D^-1 (u - U^T a'), a = a' + S qdd
+//   integrate  v += dt qdd; hinge/slide q += dt v; ball/free quaternion
+//              compose-and-relog (crates/phyz-rigid/src/integrate.rs:41-92)
+#pragma once
+
+#if !defined(__HIPCC_RTC__)
+#include <hip/hip_runtime.h>
+#endif
+
+namespace phz {
+
+typedef unsigned long long u64;
+
+template <int V> struct ic { static constexpr int value = V; };
+template <int I, int N, class F> __device__ __forceinline__ void sfor(F&& f) {
+  if constexpr (I < N) { f(ic<I>{}); sfor<I + 1, N>(f); }
+}
+template <int N, class F> __device__ __forceinline__ void rfor(F&& f) {
+  if constexpr (N > 0) { f(ic<N - 1>{}); rfor<N - 1>(f); }
+}
+
+enum { J_REV = 0, J_PRIS = 1, J_FIXED = 2, J_BALL = 3, J_FREE = 4 };
+enum { G_NONE = 0, G_SPHERE = 1, G_BOX = 2, G_CAPSULE = 3, G_CYLINDER = 4, G_MESH = 5 };
+constexpr int ndof_of(int jt) { return jt == J_FIXED ? 0 : (jt == J_BALL ? 3 : (jt == J_FREE ? 6 : 1)); }
+
+// ── math ─────────────────────────────────────────────────────────────────────
+__device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
+__device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
+__device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
+__device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
+__device__ __forceinline__ double dlog(double x) { return log(x); }
+__device__ __forceinline__ float dlog(float x) { return logf(x); }
+__device__ __forceinline__ double datan2(double y, double x) { return atan2(y, x); }
+__device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x); }
+template <class T> __device__ __forceinline__ T dmax(T a, T b) { return a > b ? a : b; }
+template <class T> __device__ __forceinline__ T dmin(T a, T b) { return a < b ? a : b; }
+template <class T> __device__ __forceinline__ T dabs(T a) { return a < T(0) ? -a : a; }
+template <class T> __device__ __forceinline__ T dsign(T a) { return a > T(0) ? T(1) : (a < T(0) ? T(-1) : T(0)); }
+// Small-angle thresholds of quat exp/log: f64::EPSILON on the f64 path
+// (crates/phyz-math/src/lib.rs:48, 67), 1e-6 on the f32 path
+// (crates/phyz-gpu/cuda/phyz_kernels.cu:250, 282).
+template <class T> struct Eps;
+template <> struct Eps<double> { static constexpr double v = 2.220446049250313e-16; };
+template <> struct Eps<float> { static constexpr float v = 1e-6f; };
+
+template <class T> struct V3 { T x, y, z; };
+template <class T> __device__ __forceinline__ V3<T> v3(T x, T y, T z) { return V3<T>{x, y, z}; }
+template <class T> __device__ __forceinline__ V3<T> operator+(V3<T> a, V3<T> b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
+template <class T> __device__ __forceinline__ V3<T> operator-(V3<T> a, V3<T> b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
+template <class T> __device__ __forceinline__ V3<T> operator*(V3<T> a, T s) { return {a.x * s, a.y * s, a.z * s}; }
+template <class T> __device__ __forceinline__ T dot(V3<T> a, V3<T> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+template <class T> __device__ __forceinline__ V3<T> cross(V3<T> a, V3<T> b) {
+  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+template <class T> struct SV { V3<T> a, l; };  // [angular; linear]
+template <class T> __device__ __forceinline__ SV<T> operator+(SV<T> x, SV<T> y) { return {x.a + y.a, x.l + y.l}; }
+template <class T> __device__ __forceinline__ SV<T> operator-(SV<T> x, SV<T> y) { return {x.a - y.a, x.l - y.l}; }
+template <class T> __device__ __forceinline__ SV<T> operator*(SV<T> x, T s) { return {x.a * s, x.l * s}; }
+template <class T> __device__ __forceinline__ T sv_get(const SV<T>& s, int k) {
+  return k == 0 ? s.a.x : k == 1 ? s.a.y : k == 2 ? s.a.z : k == 3 ? s.l.x : k == 4 ? s.l.y : s.l.z;
+}
+template <class T> __device__ __forceinline__ void sv_set(SV<T>& s, int k, T v) {
+  if (k == 0) s.a.x = v; else if (k == 1) s.a.y = v; else if (k == 2) s.a.z = v;
+  else if (k == 3) s.l.x = v; else if (k == 4) s.l.y = v; else s.l.z = v;
+}
+template <class T> __device__ __forceinline__ T dot(const SV<T>& x, const SV<T>& y) { return dot(x.a, y.a) + dot(x.l, y.l); }
+template <class T> __device__ __forceinline__ SV<T> cross_motion(const SV<T>& v, const SV<T>& m) {
+  return {cross(v.a, m.a), cross(v.a, m.l) + cross(v.l, m.a)};
+}
+template <class T> __device__ __forceinline__ SV<T> cross_force(const SV<T>& v, const SV<T>& f) {
+  return {cross(v.a, f.a) + cross(v.l, f.l), cross(v.a, f.l)};
+}
+
+// Row-major 3x3.
+template <class T> struct R3 { T m[9]; };
+template <class T> __device__ __forceinline__ V3<T> mul(const R3<T>& r, V3<T> v) {
+  return {r.m[0] * v.x + r.m[1] * v.y + r.m[2] * v.z, r.m[3] * v.x + r.m[4] * v.y + r.m[5] * v.z,
+          r.m[6] * v.x + r.m[7] * v.y + r.m[8] * v.z};
+}
+template <class T> __device__ __forceinline__ V3<T> tmul(const R3<T>& r, V3<T> v) {
+  return {r.m[0] * v.x + r.m[3] * v.y + r.m[6] * v.z, r.m[1] * v.x + r.m[4] * v.y + r.m[7] * v.z,
+          r.m[2] * v.x + r.m[5] * v.y + r.m[8] * v.z};
+}
+template <class T> __device__ __forceinline__ R3<T> mul(const R3<T>& a, const R3<T>& b) {
+  R3<T> r;
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) r.m[i * 3 + j] = a.m[i * 3] * b.m[j] + a.m[i * 3 + 1] * b.m[3 + j] + a.m[i * 3 + 2] * b.m[6 + j];
+  return r;
+}
+template <class T> __device__ __forceinline__ R3<T> mul_bt(const R3<T>& a, const R3<T>& b) {  // a b^T
+  R3<T> r;
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+      r.m[i * 3 + j] = a.m[i * 3] * b.m[j * 3] + a.m[i * 3 + 1] * b.m[j * 3 + 1] + a.m[i * 3 + 2] * b.m[j * 3 + 2];
+  return r;
+}
+template <class T> __device__ __forceinline__ R3<T> transpose(const R3<T>& a) {
+  return R3<T>{{a.m[0], a.m[3], a.m[6], a.m[1], a.m[4], a.m[7], a.m[2], a.m[5], a.m[8]}};
+}
+
+// Plucker transform: X v = [E w; E (v - r x w)], X^T f = [E^T t + r x E^T f; E^T f].
+template <class T> struct Xf { R3<T> E; V3<T> r; };
+template <class T> __device__ __forceinline__ SV<T> apply_motion(const Xf<T>& x, const SV<T>& v) {
+  return {mul(x.E, v.a), mul(x.E, v.l - cross(x.r, v.a))};
+}
+template <class T> __device__ __forceinline__ SV<T> inv_apply_force(const Xf<T>& x, const SV<T>& f) {
+  V3<T> rf = tmul(x.E, f.l);
+  return {tmul(x.E, f.a) + cross(x.r, rf), rf};
+}
+
+// Symmetric 6x6 as blocks [A B; B^T C]; A and C stored as upper triangles
+// (00 01 02 11 12 22), B full row-major.
+template <class T> struct Sym { T a[6]; T b[9]; T c[6]; };
+__device__ __forceinline__ constexpr int sx(int i, int j) {
+  return i <= j ? (i == 0 ? j : (i == 1 ? 2 + j : 5)) : (j == 0 ? i : (j == 1 ? 2 + i : 5));
+}
+template <class T> __device__ __forceinline__ T sym_get(const Sym<T>& s, int i, int j) {
+  if (i < 3 && j < 3) return s.a[sx(i, j)];
+  if (i >= 3 && j >= 3) return s.c[sx(i - 3, j - 3)];
+  if (i < 3) return s.b[i * 3 + (j - 3)];
+  return s.b[j * 3 + (i - 3)];
+}
+template <class T> __device__ __forceinline__ SV<T> sym_mul(const Sym<T>& s, const SV<T>& v) {
+  SV<T> r;
+#pragma unroll
+  for (int i = 0; i < 6; i++) {
+    T acc = sym_get(s, i, 0) * sv_get(v, 0);
+#pragma unroll
+    for (int j = 1; j < 6; j++) acc = acc + sym_get(s, i, j) * sv_get(v, j);
+    sv_set(r, i, acc);
+  }
+  return r;
+}
+template <class T> __device__ __forceinline__ void sym_add(Sym<T>& d, const Sym<T>& s) {
+#pragma unroll
+  for (int k = 0; k < 6; k++) { d.a[k] = d.a[k] + s.a[k]; d.c[k] = d.c[k] + s.c[k]; }
+#pragma unroll
+  for (int k = 0; k < 9; k++) d.b[k] = d.b[k] + s.b[k];
+}
+// E^T M E for symmetric M (upper triangles).
+template <class T> __device__ __forceinline__ void sym_rot(const T* m, const R3<T>& E, T* out) {
+  T t[9];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) t[i * 3 + j] = m[sx(i, 0)] * E.m[j] + m[sx(i, 1)] * E.m[3 + j] + m[sx(i, 2)] * E.m[6 + j];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = i; j < 3; j++) out[sx(i, j)] = E.m[i] * t[j] + E.m[3 + i] * t[3 + j] + E.m[6 + i] * t[6 + j];
+}
+// X^T I X = T^T (Rot^T I Rot) T with T = [1 0; -r x 1]:
+//   A1 = E^T A E, B1 = E^T B E, C1 = E^T C E
+//   B2 = B1 + r x C1,  A2 = A1 - B1 r x + r x B2^T,  C2 = C1
+template <class T> __device__ __forceinline__ Sym<T> sym_xtix(const Sym<T>& I, const Xf<T>& X) {
+  const R3<T>& E = X.E;
+  Sym<T> o;
+  sym_rot(I.a, E, o.a);
+  sym_rot(I.c, E, o.c);
+  T t[9], b1[9];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) t[i * 3 + j] = I.b[i * 3] * E.m[j] + I.b[i * 3 + 1] * E.m[3 + j] + I.b[i * 3 + 2] * E.m[6 + j];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) b1[i * 3 + j] = E.m[i] * t[j] + E.m[3 + i] * t[3 + j] + E.m[6 + i] * t[6 + j];
+  const V3<T> r = X.r;
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    V3<T> rc = cross(r, v3(o.c[sx(0, j)], o.c[sx(1, j)], o.c[sx(2, j)]));
+    o.b[j] = b1[j] + rc.x;
+    o.b[3 + j] = b1[3 + j] + rc.y;
+    o.b[6 + j] = b1[6 + j] + rc.z;
+  }
+  V3<T> rb1[3], rb2[3];
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    rb1[i] = cross(r, v3(b1[i * 3], b1[i * 3 + 1], b1[i * 3 + 2]));
+    rb2[i] = cross(r, v3(o.b[i * 3], o.b[i * 3 + 1], o.b[i * 3 + 2]));
+  }
+  auto comp = [](const V3<T>& v, int k) { return k == 0 ? v.x : (k == 1 ? v.y : v.z); };
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = i; j < 3; j++) o.a[sx(i, j)] = o.a[sx(i, j)] + comp(rb1[i], j) + comp(rb2[j], i);
+  return o;
+}
+
+// Quaternions (w, x, y, z).
+template <class T> struct Q { T w, x, y, z; };
+template <class T> __device__ __forceinline__ Q<T> qmul(const Q<T>& a, const Q<T>& b) {
+  return {a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z, a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
+          a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x, a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
+}
+template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
+  T ang = dsqrt(dot(w, w));
+  T s, c;
+  dsincos(ang * T(0.5), &s, &c);
+  const bool small = ang < T(Eps<T>::v);
+  T f = small ? T(0.5) : s / ang;
+  return {small ? T(1) : c, w.x * f, w.y * f, w.z * f};
+}
+template <class T> __device__ __forceinline__ V3<T> quat_log(const Q<T>& q) {
+  V3<T> v = v3(q.x, q.y, q.z);
+  T n = dsqrt(dot(v, v));
+  const bool small = n < T(Eps<T>::v);
+  T f = small ? T(2) : T(2) * datan2(n, q.w) / n;
+  return v * f;
+}
+// Rotation matrix of unit q (active), row-major.
+template <class T> __device__ __forceinline__ R3<T> quat_mat(const Q<T>& q) {
+  T w = q.w, x = q.x, y = q.y, z = q.z;
+  return R3<T>{{T(1) - T(2) * (y * y + z * z), T(2) * (x * y - w * z), T(2) * (x * z + w * y),
+                T(2) * (x * y + w * z), T(1) - T(2) * (x * x + z * z), T(2) * (y * z - w * x),
+                T(2) * (x * z - w * y), T(2) * (y * z + w * x), T(1) - T(2) * (x * x + y * y)}};
+}
+template <class T> __device__ __forceinline__ V3<T> qrotate(const Q<T>& q, V3<T> p) {
+  V3<T> u = v3(q.x, q.y, q.z);
+  V3<T> t = cross(u, p) * T(2);
+  return p + t * q.w + cross(u, t);
+}
+
+// ── per-world RNG: SplitMix64 world seed + xorshift64 ───────────────────────
+// (crates/phyz-gpu/src/policy_pipeline.rs:417-456)
+__device__ __forceinline__ u64 xorshift64(u64& s) {
+  u64 x = s;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  s = x;
+  return x;
+}
+// Uniform on [0, 1): 53 bits on the f64 path, 24 bits on the f32 path (both exact).
+__device__ __forceinline__ double uniform01(u64& s, double) { return (double)(xorshift64(s) >> 11) * 0x1.0p-53; }
+__device__ __forceinline__ float uniform01(u64& s, float) { return (float)(unsigned)(xorshift64(s) >> 40) * 0x1.0p-24f; }
+
+// ── kernel arguments ─────────────────────────────────────────────────────────
+// Structure-of-arrays state: element (j, w) at j * stride + w.
+struct StepArgs {
+  void* q;             // [nq][stride]
+  void* v;             // [nv][stride]
+  void* ctrl;          // [nv][stride]
+  void* qdd;           // [nv][stride], last step's accelerations
+  const void* targets; // [npd][stride]
+  u64* rng;            // [stride]
+  void* contact_rows;  // [nb * 8][stride], last step's contact readback
+  int nworld;
+  int stride;
+  int nsteps;
+  int write_contacts;
+};
+
+// Model-derived constants evaluated in double on the host side of the
+// compiler, then rounded once to T.
+template <class M, int i> struct BodyK {
+  static constexpr int jt = M::jtype[i];
+  static constexpr int nd = ndof_of(jt);
+  static constexpr int parent = M::parent[i];
+};
+
+template <class M, class T, int i> __device__ __forceinline__ Sym<T> rigid_inertia() {
+  Sym<T> s;
+#pragma unroll
+  for (int k = 0; k < 6; k++) { s.a[k] = T(M::inA[i][k]); s.c[k] = T(M::inC[i][k]); }
+#pragma unroll
+  for (int k = 0; k < 9; k++) s.b[k] = T(M::inB[i][k]);
+  return s;
+}
+template <class M, class T, int i> __device__ __forceinline__ SV<T> subspace(int k) {
+  constexpr int jt = M::jtype[i];
+  SV<T> s = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  if constexpr (jt == J_REV) s.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2]));
+  else if constexpr (jt == J_PRIS) s.l = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2]));
+  else sv_set(s, k, T(1));
+  return s;
+}
+
+// Effective mass of body i at body-frame offset r along unit direction u
+// (crates/phyz-gpu/cuda/phyz_kernels.cu:545-571).
+template <class M, class T, int i> __device__ __forceinline__ T eff_mass(V3<T> r, V3<T> u) {
+  if constexpr (!(M::mass[i] > 0.0)) {
+    return T(1e30);
+  } else {
+    V3<T> rc = r - v3(T(M::com[i][0]), T(M::com[i][1]), T(M::com[i][2]));
+    V3<T> a = cross(rc, u);
+    // Cofactor inverse of the COM inertia, upper triangle (zeros if singular).
+    V3<T> ia = v3(T(M::iinv[i][0]) * a.x + T(M::iinv[i][1]) * a.y + T(M::iinv[i][2]) * a.z,
+                  T(M::iinv[i][1]) * a.x + T(M::iinv[i][3]) * a.y + T(M::iinv[i][4]) * a.z,
+                  T(M::iinv[i][2]) * a.x + T(M::iinv[i][4]) * a.y + T(M::iinv[i][5]) * a.z);
+    T ang = dmax(dot(a, ia), T(0));
+    return T(1) / (T(1.0 / M::mass[i]) + ang);
+  }
+}
+
+// Ground penalty contact of body i (crates/phyz-gpu/cuda/phyz_kernels.cu:804-980,
+// penalty branch 939-965). Rw: body->world rotation, pw: body origin in world,
+// vel: body-frame spatial velocity. Returns the body-frame spatial force. When
+// `write` is set, stores the readback row (touching, deepest penetration,
+// point (x, y, h), summed world force) at out[k * S], k = 8 i .. 8 i + 7.
+template <class M, class T, int i>
+__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, T* out, int S, bool write) {
+  constexpr int gt = M::gtype[i];
+  constexpr int npts = gt == G_BOX ? 8 : 1;
+  constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
+  const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
+  V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);  // world +Z in the body frame
+  SV<T> ext = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  V3<T> ftot = v3(T(0), T(0), T(0));
+  T deepest = T(0);
+  T dx = T(0), dy = T(0);
+  bool any = false;
+  const R3<T> oR = R3<T>{{T(M::gorot[i][0]), T(M::gorot[i][1]), T(M::gorot[i][2]), T(M::gorot[i][3]), T(M::gorot[i][4]),
+                          T(M::gorot[i][5]), T(M::gorot[i][6]), T(M::gorot[i][7]), T(M::gorot[i][8])}};
+  const V3<T> oP = v3(T(M::gopos[i][0]), T(M::gopos[i][1]), T(M::gopos[i][2]));
+#pragma unroll
+  for (int cp = 0; cp < npts; cp++) {
+    V3<T> sup;
+    if constexpr (gt == G_BOX) {
+      V3<T> corner = v3(T(M::gp[i][0] * ((cp & 1) ? 1.0 : -1.0)), T(M::gp[i][1] * ((cp & 2) ? 1.0 : -1.0)),
+                        T(M::gp[i][2] * ((cp & 4) ? 1.0 : -1.0)));
+      sup = oP + tmul(oR, corner);
+    } else {
+      V3<T> n = mul(oR, zb);
+      V3<T> s;
+      if constexpr (gt == G_SPHERE) {
+        s = n * T(-M::gp[i][0]);
+      } else if constexpr (gt == G_CAPSULE) {
+        s = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
+      } else if constexpr (gt == G_CYLINDER) {
+        T rl = dsqrt(n.x * n.x + n.y * n.y);
+        T f = rl > T(1e-6) ? T(M::gp[i][0]) / rl : T(0);
+        s = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
+      } else {  // mesh AABB
+        s = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
+               T(0.5 * (M::gp[i][1] + M::gp[i][4])) - T(0.5 * (M::gp[i][4] - M::gp[i][1])) * dsign(n.y),
+               T(0.5 * (M::gp[i][2] + M::gp[i][5])) - T(0.5 * (M::gp[i][5] - M::gp[i][2])) * dsign(n.z));
+      }
+      sup = oP + tmul(oR, s);
+    }
+    V3<T> supw = pw + mul(Rw, sup);
+    T pen = T(M::ground_h) - supw.z;
+    const bool in = pen > T(0);
+    V3<T> vpt = vel.l + cross(vel.a, sup);
+    T vn = dot(vpt, zb);
+    T mn = eff_mass<M, T, i>(sup, zb);
+    T kb = dmin(T(sc * M::gk[i]), T(4.0 / (dtc * dtc)) * mn);
+    T db = dmin(T(sc * M::gd[i]), T(1.0 / dtc) * mn);
+    T fn = dmax(kb * pen - db * vn, T(0));
+    V3<T> vt3 = vpt - zb * vn;
+    T vt = dsqrt(dot(vt3, vt3));
+    const bool slip = vt > T(1e-6);
+    T ivt = slip ? T(1) / vt : T(0);
+    V3<T> td = vt3 * ivt;
+    T coul = T(M::mu) * fn * dmin(T(1), vt * T(1e3));
+    T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i>(sup, td) * vt);
+    ft = slip ? ft : T(0);
+    V3<T> fb = zb * fn - td * ft;
+    fb = in ? fb : v3(T(0), T(0), T(0));
+    ext.a = ext.a + cross(sup, fb);
+    ext.l = ext.l + fb;
+    if (write) {
+      ftot = ftot + mul(Rw, fb);
+      const bool deeper = in && pen > deepest;
+      deepest = deeper ? pen : deepest;
+      dx = deeper ? supw.x : dx;
+      dy = deeper ? supw.y : dy;
+      any = any || in;
+    }
+  }
+  if (write) {
+    T* o = out + 8 * i * S;
+    o[0] = any ? T(1) : T(0);
+    o[S] = any ? deepest : T(0);
+    o[2 * S] = any ? dx : T(0);
+    o[3 * S] = any ? dy : T(0);
+    o[4 * S] = any ? T(M::ground_h) : T(0);
+    o[5 * S] = any ? ftot.x : T(0);
+    o[6 * S] = any ? ftot.y : T(0);
+    o[7 * S] = any ? ftot.z : T(0);
+  }
+  return ext;
+}
+
+// One full step of one world. State arrays are in registers.
+template <class M, class T>
+__device__ __forceinline__ void step_world(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+                                           const T* tgt, u64& rng, T* rows, int S, bool write_rows) {
+  constexpr int NB = M::NB;
+  // ── control noise (one draw per listed DOF, list order) ──
+  if constexpr (M::NNOISE > 0) {
+    if constexpr (M::noise_dist == 1) {
+      sfor<0, M::NNOISE>([&](auto K) {
+        constexpr int k = decltype(K)::value;
+        T u = uniform01(rng, T(0));
+        ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b - M::noise_a) * u;
+      });
+    } else {
+      sfor<0, (M::NNOISE + 1) / 2>([&](auto K) {
+        constexpr int k = 2 * decltype(K)::value;
+        T u1 = uniform01(rng, T(0));
+        T u2 = uniform01(rng, T(0));
+        T r = dsqrt(T(-2) * dlog(T(1) - u1));
+        T sn, cs;
+        dsincos(T(6.283185307179586) * u2, &sn, &cs);
+        ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
+        if constexpr (k + 1 < M::NNOISE) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
+      });
+    }
+  }
+  // ── PD servo (crates/phyz-gpu/cuda/phyz_kernels.cu:464-483) ──
+  sfor<0, M::NPD>([&](auto K) {
+    constexpr int d = decltype(K)::value;
+    T tau = T(M::pd_kp[d]) * (tgt[d] - q[M::pd_q[d]]) - T(M::pd_kd[d]) * v[M::pd_v[d]];
+    ctrl[M::pd_v[d]] = dmin(dmax(tau, T(-M::pd_max[d])), T(M::pd_max[d]));
+  });
+
+  Xf<T> X[NB];
+  SV<T> vel[NB], cb[NB], pA[NB];
+  R3<T> Rw[NB];
+  V3<T> Pw[NB];
+  // ── pass 1: transforms, velocities, bias forces, contact ──
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int jt = M::jtype[i];
+    constexpr int p = M::parent[i];
+    constexpr int qo = M::qoff[i], vo = M::voff[i];
+    const R3<T> Rp = R3<T>{{T(M::ptj_rot[i][0]), T(M::ptj_rot[i][1]), T(M::ptj_rot[i][2]), T(M::ptj_rot[i][3]),
+                            T(M::ptj_rot[i][4]), T(M::ptj_rot[i][5]), T(M::ptj_rot[i][6]), T(M::ptj_rot[i][7]),
+                            T(M::ptj_rot[i][8])}};
+    const V3<T> pp = v3(T(M::ptj_pos[i][0]), T(M::ptj_pos[i][1]), T(M::ptj_pos[i][2]));
+    SV<T> vj = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+    if constexpr (jt == J_REV) {
+      T s, c;
+      dsincos(-q[qo], &s, &c);
+      const T omc = T(1) - c;
+      R3<T> EJ;
+#pragma unroll
+      for (int k = 0; k < 9; k++) EJ.m[k] = T(k % 4 == 0 ? 1.0 : 0.0) + T(M::rev_k[i][k]) * s + T(M::rev_k2[i][k]) * omc;
+      X[i].E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+      X[i].r = pp;
+      vj.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+    } else if constexpr (jt == J_PRIS) {
+      X[i].E = Rp;
+      X[i].r = pp + tmul(Rp, v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * q[qo]);
+      vj.l = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+    } else if constexpr (jt == J_BALL || jt == J_FREE) {
+      R3<T> EJ = transpose(quat_mat(quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]))));
+      X[i].E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+      if constexpr (jt == J_FREE) {
+        X[i].r = pp + tmul(Rp, v3(q[qo + 3], q[qo + 4], q[qo + 5]));
+        vj.l = v3(v[vo + 3], v[vo + 4], v[vo + 5]);
+      } else {
+        X[i].r = pp;
+      }
+      vj.a = v3(v[vo], v[vo + 1], v[vo + 2]);
+    } else {
+      X[i].E = Rp;
+      X[i].r = pp;
+    }
+    if constexpr (p < 0) {
+      vel[i] = vj;
+      cb[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+    } else {
+      vel[i] = apply_motion(X[i], vel[p]) + vj;
+      cb[i] = cross_motion(vel[i], vj);
+    }
+    pA[i] = cross_force(vel[i], sym_mul(rigid_inertia<M, T, i>(), vel[i]));
+    if constexpr (M::need_world[i]) {
+      if constexpr (p < 0) {
+        Rw[i] = transpose(X[i].E);
+        Pw[i] = X[i].r;
+      } else {
+        Rw[i] = mul_bt(Rw[p], X[i].E);
+        Pw[i] = Pw[p] + mul(Rw[p], X[i].r);
+      }
+    }
+    if constexpr (M::gtype[i] != G_NONE) {
+      SV<T> f = contact_body<M, T, i>(Rw[i], Pw[i], vel[i], rows, S, write_rows);
+      pA[i] = pA[i] - f;
+    }
+  });
+
+  // ── pass 2: articulated inertias, leaves to root ──
+  Sym<T> IA[NB];
+  sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; IA[i] = rigid_inertia<M, T, i>(); });
+  constexpr int MAXD = M::MAXNDOF > 0 ? M::MAXNDOF : 1;
+  T U[NB][MAXD][6];
+  T Lm[NB][MAXD][MAXD];
+  T Dinv[NB][MAXD];
+  T uu[NB][MAXD];
+  bool ok[NB];
+  rfor<NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int jt = M::jtype[i];
+    constexpr int nd = ndof_of(jt);
+    constexpr int p = M::parent[i];
+    constexpr int vo = M::voff[i], qo = M::qoff[i];
+    ok[i] = true;
+    Sym<T> Ia = IA[i];
+    SV<T> pa = pA[i];
+    if constexpr (nd > 0) {
+#pragma unroll
+      for (int k = 0; k < nd; k++) {
+        SV<T> uk = sym_mul(IA[i], subspace<M, T, i>(k));
+        U[i][k][0] = uk.a.x; U[i][k][1] = uk.a.y; U[i][k][2] = uk.a.z;
+        U[i][k][3] = uk.l.x; U[i][k][4] = uk.l.y; U[i][k][5] = uk.l.z;
+        T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
+        if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
+        uu[i][k] = tau - dot(subspace<M, T, i>(k), pA[i]);
+      }
+      T D[MAXD][MAXD];
+#pragma unroll
+      for (int r = 0; r < nd; r++)
+#pragma unroll
+        for (int c = 0; c <= r; c++) {
+          SV<T> sr = subspace<M, T, i>(r);
+          SV<T> ucol = {v3(U[i][c][0], U[i][c][1], U[i][c][2]), v3(U[i][c][3], U[i][c][4], U[i][c][5])};
+          D[r][c] = dot(sr, ucol) + (r == c ? T(M::armature[i] + M::dt * M::damping[i]) : T(0));
+        }
+      // LDL^T with the pivots stored inverted (same singular test as aba.rs:210).
+      T E[MAXD][MAXD];
+#pragma unroll
+      for (int j = 0; j < nd; j++) {
+        T dj = D[j][j];
+#pragma unroll
+        for (int k = 0; k < j; k++) dj = dj - Lm[i][j][k] * E[j][k];
+        ok[i] = ok[i] && !(dabs(dj) < T(1e-20));
+        Dinv[i][j] = T(1) / dj;
+#pragma unroll
+        for (int r = j + 1; r < nd; r++) {
+          T e = D[r][j];
+#pragma unroll
+          for (int k = 0; k < j; k++) e = e - Lm[i][r][k] * E[j][k];
+          E[r][j] = e;
+          Lm[i][r][j] = e * Dinv[i][j];
+        }
+      }
+      if constexpr (p >= 0) {
+        // W = U D^-1, one row of U at a time.
+        T W[MAXD][6];
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+          T y[MAXD];
+#pragma unroll
+          for (int k = 0; k < nd; k++) {
+            y[k] = U[i][k][r];
+#pragma unroll
+            for (int t = 0; t < k; t++) y[k] = y[k] - Lm[i][k][t] * y[t];
+          }
+#pragma unroll
+          for (int k = 0; k < nd; k++) y[k] = y[k] * Dinv[i][k];
+#pragma unroll
+          for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+            for (int t = k + 1; t < nd; t++) y[k] = y[k] - Lm[i][t][k] * y[t];
+#pragma unroll
+          for (int k = 0; k < nd; k++) W[k][r] = y[k];
+        }
+#pragma unroll
+        for (int r = 0; r < 3; r++)
+#pragma unroll
+          for (int c = r; c < 3; c++) {
+            T s0 = W[0][r] * U[i][0][c], s1 = W[0][3 + r] * U[i][0][3 + c];
+#pragma unroll
+            for (int k = 1; k < nd; k++) { s0 = s0 + W[k][r] * U[i][k][c]; s1 = s1 + W[k][3 + r] * U[i][k][3 + c]; }
+            Ia.a[sx(r, c)] = Ia.a[sx(r, c)] - s0;
+            Ia.c[sx(r, c)] = Ia.c[sx(r, c)] - s1;
+          }
+#pragma unroll
+        for (int r = 0; r < 3; r++)
+#pragma unroll
+          for (int c = 0; c < 3; c++) {
+            T s0 = W[0][r] * U[i][0][3 + c];
+#pragma unroll
+            for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * U[i][k][3 + c];
+            Ia.b[r * 3 + c] = Ia.b[r * 3 + c] - s0;
+          }
+        SV<T> wu;
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+          T s0 = W[0][r] * uu[i][0];
+#pragma unroll
+          for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * uu[i][k];
+          sv_set(wu, r, s0);
+        }
+        pa = pa + sym_mul(Ia, cb[i]) + wu;
+        if (ok[i]) {
+          sym_add(IA[p], sym_xtix(Ia, X[i]));
+          pA[p] = pA[p] + inv_apply_force(X[i], pa);
+        }
+      }
+    } else if constexpr (p >= 0) {
+      sym_add(IA[p], sym_xtix(Ia, X[i]));
+      pA[p] = pA[p] + inv_apply_force(X[i], pa);
+    }
+  });
+
+  // ── pass 3: accelerations, root to leaves ──
+  SV<T> acc[NB];
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int jt = M::jtype[i];
+    constexpr int nd = ndof_of(jt);
+    constexpr int p = M::parent[i];
+    constexpr int vo = M::voff[i];
+    SV<T> ap;
+    if constexpr (p < 0) {
+      SV<T> a0 = {v3(T(0), T(0), T(0)), v3(T(-M::gravity[0]), T(-M::gravity[1]), T(-M::gravity[2]))};
+      ap = apply_motion(X[i], a0) + cb[i];
+    } else {
+      ap = apply_motion(X[i], acc[p]) + cb[i];
+    }
+    if constexpr (nd > 0) {
+      T y[MAXD];
+#pragma unroll
+      for (int k = 0; k < nd; k++) {
+        T uta = U[i][k][0] * ap.a.x + U[i][k][1] * ap.a.y + U[i][k][2] * ap.a.z + U[i][k][3] * ap.l.x +
+                U[i][k][4] * ap.l.y + U[i][k][5] * ap.l.z;
+        y[k] = uu[i][k] - uta;
+#pragma unroll
+        for (int t = 0; t < k; t++) y[k] = y[k] - Lm[i][k][t] * y[t];
+      }
+#pragma unroll
+      for (int k = 0; k < nd; k++) y[k] = y[k] * Dinv[i][k];
+#pragma unroll
+      for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+        for (int t = k + 1; t < nd; t++) y[k] = y[k] - Lm[i][t][k] * y[t];
+#pragma unroll
+      for (int k = 0; k < nd; k++) {
+        y[k] = ok[i] ? y[k] : T(0);
+        qdd[vo + k] = y[k];
+        ap = ap + subspace<M, T, i>(k) * y[k];
+      }
+    }
+    acc[i] = ap;
+  });
+
+  // ── semi-implicit Euler (crates/phyz-rigid/src/integrate.rs:83-92) ──
+  const T dt = T(M::dt);
+#pragma unroll
+  for (int j = 0; j < M::NV; j++) v[j] = v[j] + dt * qdd[j];
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int jt = M::jtype[i];
+    constexpr int qo = M::qoff[i], vo = M::voff[i];
+    if constexpr (jt == J_REV || jt == J_PRIS) {
+      q[qo] = q[qo] + dt * v[vo];
+    } else if constexpr (jt == J_BALL || jt == J_FREE) {
+      Q<T> cur = quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]));
+      if constexpr (jt == J_FREE) {
+        V3<T> wl = qrotate(cur, v3(v[vo + 3], v[vo + 4], v[vo + 5]));
+        q[qo + 3] = q[qo + 3] + dt * wl.x;
+        q[qo + 4] = q[qo + 4] + dt * wl.y;
+        q[qo + 5] = q[qo + 5] + dt * wl.z;
+      }
+      Q<T> nx = qmul(cur, quat_exp(v3(v[vo], v[vo + 1], v[vo + 2]) * dt));
+      T n = dsqrt(nx.w * nx.w + nx.x * nx.x + nx.y * nx.y + nx.z * nx.z);
+      nx = Q<T>{nx.w / n, nx.x / n, nx.y / n, nx.z / n};
+      V3<T> lg = quat_log(nx);
+      q[qo] = lg.x;
+      q[qo + 1] = lg.y;
+      q[qo + 2] = lg.z;
+    }
+  });
+}
+
+// Kernel body: load the world's state, run nsteps, store.
+template <class M, class T> __device__ __forceinline__ void run(const StepArgs& a) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= a.nworld) return;
+  const int S = a.stride;
+  T* gq = (T*)a.q;
+  T* gv = (T*)a.v;
+  T* gc = (T*)a.ctrl;
+  T q[M::NQ], v[M::NV], ctrl[M::NV], qdd[M::NV];
+#pragma unroll
+  for (int j = 0; j < M::NQ; j++) q[j] = gq[j * S + w];
+#pragma unroll
+  for (int j = 0; j < M::NV; j++) { v[j] = gv[j * S + w]; ctrl[j] = gc[j * S + w]; qdd[j] = T(0); }
+  T tgt[M::NPD > 0 ? M::NPD : 1];
+#pragma unroll
+  for (int d = 0; d < M::NPD; d++) tgt[d] = ((const T*)a.targets)[d * S + w];
+  u64 rng = 0;
+  if constexpr (M::NNOISE > 0) rng = a.rng[w];
+  T* rows = M::HAS_CONTACT ? (T*)a.contact_rows + w : nullptr;
+  const int n = a.nsteps;
+  for (int s = 0; s < n; s++) {
+    const bool last = (s == n - 1) && a.write_contacts;
+    step_world<M, T>(q, v, ctrl, qdd, tgt, rng, rows, S, last);
+  }
+#pragma unroll
+  for (int j = 0; j < M::NQ; j++) gq[j * S + w] = q[j];
+#pragma unroll
+  for (int j = 0; j < M::NV; j++) {
+    gv[j * S + w] = v[j];
+    gc[j * S + w] = ctrl[j];
+    ((T*)a.qdd)[j * S + w] = qdd[j];
+  }
+  if constexpr (M::NNOISE > 0) a.rng[w] = rng;
+}
+
+}  // namespace phz

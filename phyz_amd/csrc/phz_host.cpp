@@ -1,0 +1,870 @@
+// phz_host.cpp — host side of the MI355X batched stepper: the BatchSim object
+// behind the C ABI of include/phyz_amd.h.
+//
+// Mirrors crates/phyz-gpu/src/cuda/mod.rs (BatchSim<B>) and the packing rules of
+// crates/phyz-gpu/src/layout.rs, with a HIP runtime in place of
+// KernelBackend/CudaBackend (crates/phyz-gpu/src/cuda/nvrtc.rs). Where the
+// reference compiles one generic kernel source with NVRTC and launches four
+// passes per step, this compiles phz_device.h with hiprtc against the uploaded
+// model (every body loop unrolled, model constants folded) and launches one
+// fused kernel per span of steps.
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/phyz_amd.h"
+
+// Text of phz_device.h, embedded at build time.
+static const char* const kDeviceSrc =
+#include "phz_device_src.inc"
+    ;
+
+extern "C" {
+hipError_t phz_io_pack(const double* src, void* dst, int nworld, int width, int stride, int f64, hipStream_t s);
+hipError_t phz_io_unpack(const void* src, double* dst, int nworld, int width, int stride, int f64, hipStream_t s);
+hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s);
+hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s);
+}
+
+namespace {
+
+constexpr int kBodyStride = PHZ_BODY_STRIDE;
+constexpr int kGeomStride = PHZ_GEOM_STRIDE;
+constexpr int kPdStride = PHZ_PD_DOF_STRIDE;
+constexpr int kMaxBodies = PHZ_MAX_BODIES;
+
+thread_local std::string g_create_error;
+
+std::string fmt(const char* f, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, f);
+  std::vsnprintf(buf, sizeof(buf), f, ap);
+  va_end(ap);
+  return buf;
+}
+
+int ndof_of(int jt) { return jt == 2 ? 0 : (jt == 3 ? 3 : (jt == 4 ? 6 : 1)); }
+
+struct BodyD {
+  int parent, jtype, qoff, voff;
+  double mass, com[3], inertia[6], ptj_rot[9], ptj_pos[3], axis[3], damping, stiffness, spring_ref, armature;
+};
+struct ModelD {
+  int nb = 0, nq = 0, nv = 0;
+  std::vector<BodyD> b;
+  double g[3] = {0, 0, 0};
+  double dt = 0;
+};
+
+bool is_int(double x) { return std::isfinite(x) && x == std::floor(x); }
+
+// Unpack and validate a body table (layout.rs:19-38 slots). The checks are the
+// reference's (mod.rs:498-510: body cap, nq == nv) plus what a device kernel
+// needs to be safe: topological order, offsets inside nq/nv, finite values.
+bool parse_model(const double* t, uint32_t nb, uint32_t nq, uint32_t nv, const double* g, double dt, ModelD& m,
+                 std::string& err) {
+  if (!t || !g) { err = "null body table or gravity"; return false; }
+  if (nb == 0) { err = "model has no bodies"; return false; }
+  if (nb > (uint32_t)kMaxBodies) {
+    err = fmt("model has %u bodies but the kernels hold at most %d per world", nb, kMaxBodies);
+    return false;
+  }
+  if (nq != nv) {
+    err = fmt("kernels assume nq == nv (exponential-coordinate ball/free joints); model has nq %u nv %u", nq, nv);
+    return false;
+  }
+  if (!(std::isfinite(dt) && dt > 0)) { err = "dt must be finite and positive"; return false; }
+  m.nb = (int)nb; m.nq = (int)nq; m.nv = (int)nv; m.dt = dt;
+  for (int k = 0; k < 3; k++) {
+    if (!std::isfinite(g[k])) { err = "gravity must be finite"; return false; }
+    m.g[k] = g[k];
+  }
+  m.b.assign(nb, BodyD{});
+  int nsum = 0;
+  for (uint32_t i = 0; i < nb; i++) {
+    const double* r = t + (size_t)i * kBodyStride;
+    for (int k = 0; k < 33; k++)
+      if (!std::isfinite(r[k])) { err = fmt("body %u: non-finite value in slot %d", i, k); return false; }
+    if (!is_int(r[0]) || !is_int(r[1]) || !is_int(r[2]) || !is_int(r[3])) {
+      err = fmt("body %u: parent, joint type and offsets must be integers", i);
+      return false;
+    }
+    BodyD& b = m.b[i];
+    b.parent = (int)r[0]; b.jtype = (int)r[1]; b.qoff = (int)r[2]; b.voff = (int)r[3];
+    if (b.parent < -1 || b.parent >= (int)i) {
+      err = fmt("body %u: parent %d breaks topological order (parent < child)", i, b.parent);
+      return false;
+    }
+    if (b.jtype < 0 || b.jtype > 4) { err = fmt("body %u: unknown joint type %d", i, b.jtype); return false; }
+    const int nd = ndof_of(b.jtype);
+    if (b.qoff < 0 || b.voff < 0 || b.qoff + nd > (int)nq || b.voff + nd > (int)nv) {
+      err = fmt("body %u: joint offsets (q %d, v %d, %d DOF) exceed nq %u / nv %u", i, b.qoff, b.voff, nd, nq, nv);
+      return false;
+    }
+    nsum += nd;
+    b.mass = r[4];
+    for (int k = 0; k < 3; k++) b.com[k] = r[5 + k];
+    for (int k = 0; k < 6; k++) b.inertia[k] = r[8 + k];
+    for (int k = 0; k < 9; k++) b.ptj_rot[k] = r[14 + k];
+    for (int k = 0; k < 3; k++) b.ptj_pos[k] = r[23 + k];
+    for (int k = 0; k < 3; k++) b.axis[k] = r[26 + k];
+    b.damping = r[29]; b.stiffness = r[30]; b.spring_ref = r[31]; b.armature = r[32];
+  }
+  if (nsum != (int)nv) { err = fmt("joint DOFs sum to %d but nv is %u", nsum, nv); return false; }
+  // Every velocity slot belongs to exactly one joint.
+  std::vector<int> used(nv, 0);
+  for (const BodyD& b : m.b)
+    for (int k = 0; k < ndof_of(b.jtype); k++)
+      if (used[b.voff + k]++) { err = "joint velocity offsets overlap"; return false; }
+  return true;
+}
+
+struct Features {
+  bool contact = false;
+  double ground_h = 0, mu = 0;
+  std::vector<double> geom;  // nb x 24
+  int collidable = 0;
+  int npd = 0;
+  std::vector<double> pd;  // npd x 8
+  bool noise = false;
+  uint64_t seed = 0;
+  int dist = 0;
+  double a = 0, b = 1;
+  std::vector<int> noise_dofs;
+};
+
+// ── code generation ──────────────────────────────────────────────────────────
+std::string num(double x) {
+  char buf[40];
+  std::snprintf(buf, sizeof(buf), "%.17g", x);
+  std::string s(buf);
+  if (s.find_first_of(".eEn") == std::string::npos) s += ".0";
+  return s;
+}
+template <class F> std::string arr1(int n, F f) {
+  std::string s = "{";
+  for (int i = 0; i < n; i++) { if (i) s += ", "; s += f(i); }
+  return s + "}";
+}
+template <class F> std::string arr2(int n, int m, F f) {
+  std::string s = "{";
+  for (int i = 0; i < n; i++) {
+    if (i) s += ", ";
+    s += "{";
+    for (int j = 0; j < m; j++) { if (j) s += ", "; s += f(i, j); }
+    s += "}";
+  }
+  return s + "}";
+}
+
+std::string gen_model(const ModelD& m, const Features& f) {
+  const int nb = m.nb;
+  // Rigid spatial inertia [[Ic + m cx cx^T, m cx], [m cx^T, m 1]] as symmetric blocks.
+  std::vector<double> A(nb * 6), B(nb * 9), C(nb * 6), iinv(nb * 6), K(nb * 9), K2(nb * 9);
+  std::vector<int> ptj_id(nb), need_world(nb, 0);
+  int maxnd = 0;
+  for (int i = 0; i < nb; i++) {
+    const BodyD& b = m.b[i];
+    maxnd = std::max(maxnd, ndof_of(b.jtype));
+    const double mm = b.mass, cx = b.com[0], cy = b.com[1], cz = b.com[2];
+    double X[9] = {0, -cz, cy, cz, 0, -cx, -cy, cx, 0};
+    double XXt[9];
+    for (int r = 0; r < 3; r++)
+      for (int c = 0; c < 3; c++) XXt[r * 3 + c] = X[r * 3] * X[c * 3] + X[r * 3 + 1] * X[c * 3 + 1] + X[r * 3 + 2] * X[c * 3 + 2];
+    double Ic[9] = {b.inertia[0], b.inertia[3], b.inertia[4], b.inertia[3], b.inertia[1],
+                    b.inertia[5], b.inertia[4], b.inertia[5], b.inertia[2]};
+    const int up[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
+    for (int k = 0; k < 6; k++) {
+      const int r = up[k][0], c = up[k][1];
+      A[i * 6 + k] = Ic[r * 3 + c] + XXt[r * 3 + c] * mm;
+      C[i * 6 + k] = r == c ? mm : 0.0;
+    }
+    for (int k = 0; k < 9; k++) B[i * 9 + k] = X[k] * mm;
+    // Cofactor inverse of the COM inertia (phyz_kernels.cu:545-560).
+    const double xx = b.inertia[0], yy = b.inertia[1], zz = b.inertia[2], xy = b.inertia[3], xz = b.inertia[4],
+                 yz = b.inertia[5];
+    const double c00 = yy * zz - yz * yz, c01 = xz * yz - xy * zz, c02 = xy * yz - xz * yy;
+    const double det = xx * c00 + xy * c01 + xz * c02;
+    if (std::fabs(det) < 1e-20) {
+      for (int k = 0; k < 6; k++) iinv[i * 6 + k] = 0.0;
+    } else {
+      const double c11 = xx * zz - xz * xz, c12 = xy * xz - xx * yz, c22 = xx * yy - xy * xy, inv = 1.0 / det;
+      const double v[6] = {inv * c00, inv * c01, inv * c02, inv * c11, inv * c12, inv * c22};
+      for (int k = 0; k < 6; k++) iinv[i * 6 + k] = v[k];
+    }
+    // Rodrigues at -q (joint.rs:255-262): E_J = I + K s + K^2 (1 - c), s = sin(-q), c = cos(-q).
+    const double ax = b.axis[0], ay = b.axis[1], az = b.axis[2];
+    const double k9[9] = {0, -az, ay, az, 0, -ax, -ay, ax, 0};
+    for (int k = 0; k < 9; k++) K[i * 9 + k] = k9[k];
+    for (int r = 0; r < 3; r++)
+      for (int c = 0; c < 3; c++)
+        K2[i * 9 + r * 3 + c] = k9[r * 3] * k9[c] + k9[r * 3 + 1] * k9[3 + c] + k9[r * 3 + 2] * k9[6 + c];
+    const double id[9] = {1, 0, 0, 0, 1, 0, 0, 0, 1};
+    ptj_id[i] = 1;
+    for (int k = 0; k < 9; k++) if (b.ptj_rot[k] != id[k]) ptj_id[i] = 0;
+  }
+  if (f.contact)
+    for (int i = 0; i < nb; i++)
+      if ((int)f.geom[i * kGeomStride] != 0)
+        for (int j = i; j >= 0; j = m.b[j].parent) need_world[j] = 1;
+
+  std::ostringstream o;
+  const int npd = f.npd, nn = f.noise ? (int)f.noise_dofs.size() : 0;
+  o << "struct Model {\n";
+  o << "  static constexpr int NB = " << nb << ", NQ = " << m.nq << ", NV = " << m.nv << ", MAXNDOF = " << maxnd
+    << ";\n";
+  o << "  static constexpr bool HAS_CONTACT = " << (f.contact ? "true" : "false") << ";\n";
+  o << "  static constexpr int NPD = " << npd << ", NNOISE = " << nn << ", noise_dist = " << f.dist << ";\n";
+  o << "  static constexpr double dt = " << num(m.dt) << ";\n";
+  o << "  static constexpr double gravity[3] = " << arr1(3, [&](int k) { return num(m.g[k]); }) << ";\n";
+  o << "  static constexpr double ground_h = " << num(f.ground_h) << ", mu = " << num(f.mu) << ";\n";
+  o << "  static constexpr double noise_a = " << num(f.a) << ", noise_b = " << num(f.b) << ";\n";
+  auto ib = [&](const char* name, auto get) {
+    o << "  static constexpr int " << name << "[" << nb << "] = " << arr1(nb, [&](int i) { return std::to_string(get(i)); }) << ";\n";
+  };
+  auto bb = [&](const char* name, auto get) {
+    o << "  static constexpr bool " << name << "[" << nb << "] = "
+      << arr1(nb, [&](int i) { return std::string(get(i) ? "true" : "false"); }) << ";\n";
+  };
+  auto db = [&](const char* name, auto get) {
+    o << "  static constexpr double " << name << "[" << nb << "] = " << arr1(nb, [&](int i) { return num(get(i)); }) << ";\n";
+  };
+  auto d2 = [&](const char* name, int w, auto get) {
+    o << "  static constexpr double " << name << "[" << nb << "][" << w << "] = "
+      << arr2(nb, w, [&](int i, int k) { return num(get(i, k)); }) << ";\n";
+  };
+  ib("parent", [&](int i) { return m.b[i].parent; });
+  ib("jtype", [&](int i) { return m.b[i].jtype; });
+  ib("qoff", [&](int i) { return m.b[i].qoff; });
+  ib("voff", [&](int i) { return m.b[i].voff; });
+  bb("ptj_identity", [&](int i) { return ptj_id[i]; });
+  bb("need_world", [&](int i) { return need_world[i]; });
+  d2("ptj_rot", 9, [&](int i, int k) { return m.b[i].ptj_rot[k]; });
+  d2("ptj_pos", 3, [&](int i, int k) { return m.b[i].ptj_pos[k]; });
+  d2("axis", 3, [&](int i, int k) { return m.b[i].axis[k]; });
+  d2("rev_k", 9, [&](int i, int k) { return K[i * 9 + k]; });
+  d2("rev_k2", 9, [&](int i, int k) { return K2[i * 9 + k]; });
+  db("damping", [&](int i) { return m.b[i].damping; });
+  db("stiffness", [&](int i) { return m.b[i].stiffness; });
+  db("spring_ref", [&](int i) { return m.b[i].spring_ref; });
+  db("armature", [&](int i) { return m.b[i].armature; });
+  db("mass", [&](int i) { return m.b[i].mass; });
+  d2("com", 3, [&](int i, int k) { return m.b[i].com[k]; });
+  d2("inA", 6, [&](int i, int k) { return A[i * 6 + k]; });
+  d2("inB", 9, [&](int i, int k) { return B[i * 9 + k]; });
+  d2("inC", 6, [&](int i, int k) { return C[i * 6 + k]; });
+  d2("iinv", 6, [&](int i, int k) { return iinv[i * 6 + k]; });
+  auto g = [&](int i, int s) { return f.contact ? f.geom[i * kGeomStride + s] : 0.0; };
+  ib("gtype", [&](int i) { return f.contact ? (int)g(i, 0) : 0; });
+  d2("gp", 6, [&](int i, int k) { return g(i, 1 + k); });
+  db("gk", [&](int i) { return g(i, 8); });
+  db("gd", [&](int i) { return g(i, 9); });
+  d2("gopos", 3, [&](int i, int k) { return g(i, 10 + k); });
+  d2("gorot", 9, [&](int i, int k) { return f.contact ? g(i, 13 + k) : (k % 4 == 0 ? 1.0 : 0.0); });
+  const int npa = std::max(npd, 1), nna = std::max(nn, 1);
+  auto pdv = [&](int d, int s) { return npd ? f.pd[d * kPdStride + s] : 0.0; };
+  o << "  static constexpr int pd_q[" << npa << "] = " << arr1(npa, [&](int d) { return std::to_string((int)pdv(d, 0)); }) << ";\n";
+  o << "  static constexpr int pd_v[" << npa << "] = " << arr1(npa, [&](int d) { return std::to_string((int)pdv(d, 1)); }) << ";\n";
+  o << "  static constexpr double pd_kp[" << npa << "] = " << arr1(npa, [&](int d) { return num(pdv(d, 2)); }) << ";\n";
+  o << "  static constexpr double pd_kd[" << npa << "] = " << arr1(npa, [&](int d) { return num(pdv(d, 3)); }) << ";\n";
+  o << "  static constexpr double pd_max[" << npa << "] = " << arr1(npa, [&](int d) { return num(pdv(d, 4)); }) << ";\n";
+  o << "  static constexpr int noise_dof[" << nna << "] = "
+    << arr1(nna, [&](int k) { return std::to_string(nn ? f.noise_dofs[k] : 0); }) << ";\n";
+  o << "};\n";
+  return o.str();
+}
+
+std::string gen_source(const ModelD& m, const Features& f, bool f64, int block) {
+  std::string s = kDeviceSrc;
+  s += "\n// ---- model-specialised instantiation ----\n";
+  s += gen_model(m, f);
+  s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(block) +
+       ") phz_step(phz::StepArgs a) { phz::run<Model, " + (f64 ? "double" : "float") + ">(a); }\n";
+  return s;
+}
+
+// ── hiprtc compile with an in-process and on-disk cache ────────────────────
+uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
+  for (unsigned char c : s) { h ^= c; h *= 1099511628211ull; }
+  return h;
+}
+const std::vector<std::string>& compile_options() {
+  static const std::vector<std::string> opts = {
+      "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffinite-math-only", "-fno-signed-zeros",
+      // Packed FP32 (v_pk_*_f32) stays off in every kernel of this library.
+      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+      "-Rpass-analysis=kernel-resource-usage"};
+  return opts;
+}
+std::string cache_dir() {
+  if (const char* e = std::getenv("PHZ_KERNEL_CACHE")) return e;
+  Dl_info info;
+  if (dladdr((void*)&cache_dir, &info) && info.dli_fname) {
+    std::string p = info.dli_fname;
+    auto slash = p.rfind('/');
+    std::string d = (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) + "/_kcache";
+    mkdir(d.c_str(), 0755);
+    if (access(d.c_str(), W_OK) == 0) return d;
+  }
+  std::string d = "/tmp/phyz_amd_kcache";
+  mkdir(d.c_str(), 0755);
+  return d;
+}
+
+struct CodeObject {
+  std::vector<char> code;
+  std::string log;
+};
+std::mutex g_compile_mu;
+std::unordered_map<uint64_t, std::shared_ptr<CodeObject>> g_code_cache;
+
+std::shared_ptr<CodeObject> compile_source(const std::string& src, std::string& err) {
+  std::string key_text = src;
+  for (const auto& o : compile_options()) key_text += "\n" + o;
+  const uint64_t key = fnv1a(key_text);
+  std::lock_guard<std::mutex> lk(g_compile_mu);
+  auto it = g_code_cache.find(key);
+  if (it != g_code_cache.end()) return it->second;
+  const std::string dir = cache_dir();
+  const std::string path = dir + fmt("/%016llx.co", (unsigned long long)key);
+  // PHZ_KERNEL_REBUILD=1 ignores cached code objects (the build step uses it).
+  const char* rebuild = std::getenv("PHZ_KERNEL_REBUILD");
+  if (!(rebuild && rebuild[0] == '1')) {
+    std::ifstream in(path, std::ios::binary);
+    if (in) {
+      auto co = std::make_shared<CodeObject>();
+      co->code.assign(std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>());
+      std::ifstream lg(path + ".log");
+      if (lg) co->log.assign(std::istreambuf_iterator<char>(lg), std::istreambuf_iterator<char>());
+      if (!co->code.empty()) { g_code_cache[key] = co; return co; }
+    }
+  }
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "phz_step.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+    err = "hiprtcCreateProgram failed";
+    return nullptr;
+  }
+  std::vector<const char*> opts;
+  for (const auto& o : compile_options()) opts.push_back(o.c_str());
+  hiprtcResult rc = hiprtcCompileProgram(prog, (int)opts.size(), opts.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  std::string log(log_size, '\0');
+  if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+  if (rc != HIPRTC_SUCCESS) {
+    err = std::string("hiprtc compile of the step kernel failed: ") + hiprtcGetErrorString(rc) + "\n" + log;
+    hiprtcDestroyProgram(&prog);
+    return nullptr;
+  }
+  size_t code_size = 0;
+  hiprtcGetCodeSize(prog, &code_size);
+  auto co = std::make_shared<CodeObject>();
+  co->code.resize(code_size);
+  hiprtcGetCode(prog, co->code.data());
+  co->log = log;
+  hiprtcDestroyProgram(&prog);
+  const std::string tmp = path + fmt(".tmp%d", (int)getpid());
+  {
+    std::ofstream out(tmp, std::ios::binary);
+    out.write(co->code.data(), (std::streamsize)co->code.size());
+  }
+  std::rename(tmp.c_str(), path.c_str());
+  {
+    std::ofstream out(path + ".log");
+    out << co->log;
+  }
+  g_code_cache[key] = co;
+  return co;
+}
+
+// Parse "VGPRs: N", "AGPRs: N", "SGPRs: N", "ScratchSize [bytes/lane]: N" from the remarks.
+int64_t remark_value(const std::string& log, const char* label) {
+  auto p = log.find(label);
+  if (p == std::string::npos) return -1;
+  p += std::strlen(label);
+  while (p < log.size() && (log[p] == ' ' || log[p] == ':')) p++;
+  return std::strtoll(log.c_str() + p, nullptr, 10);
+}
+
+struct StepArgs {  // must match phz::StepArgs in phz_device.h
+  void* q;
+  void* v;
+  void* ctrl;
+  void* qdd;
+  const void* targets;
+  uint64_t* rng;
+  void* contact_rows;
+  int nworld;
+  int stride;
+  int nsteps;
+  int write_contacts;
+};
+
+int env_int(const char* name, int def) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : def;
+}
+
+}  // namespace
+
+struct phz_sim {
+  ModelD model;
+  Features feat;
+  int nworld = 0, stride = 0;
+  bool f64 = false;
+  int device = -1;
+  int block = 64;
+  int max_steps = 1000;
+  hipStream_t stream = nullptr;
+  void *q = nullptr, *v = nullptr, *ctrl = nullptr, *qdd = nullptr, *targets = nullptr, *rows = nullptr;
+  uint64_t* rng = nullptr;
+  double* staging = nullptr;
+  size_t staging_bytes = 0;
+  std::shared_ptr<CodeObject> code;
+  hipModule_t module = nullptr;
+  hipFunction_t fn = nullptr;
+  bool graphs = true;
+  hipGraphExec_t gexec = nullptr;
+  uint32_t graph_steps = 0;
+  uint64_t graph_epoch = 0;
+  uint64_t epoch = 1;
+  std::string err;
+
+  size_t esize() const { return f64 ? 8 : 4; }
+  bool has_device() const { return device >= 0; }
+
+  int fail(const std::string& e) { err = e; return 1; }
+  bool hip_ok(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    err = fmt("%s: %s", what, hipGetErrorString(e));
+    return false;
+  }
+  void drop_graph() {
+    if (gexec) { hipGraphExecDestroy(gexec); gexec = nullptr; }
+    graph_steps = 0;
+  }
+  void invalidate() {  // a new kernel or buffer: recompile lazily, re-capture
+    drop_graph();
+    if (module) { hipModuleUnload(module); module = nullptr; fn = nullptr; }
+    code.reset();
+    epoch++;
+  }
+  bool alloc(void** p, size_t bytes, const char* what) {
+    if (!hip_ok(hipMalloc(p, std::max<size_t>(bytes, 256)), what)) return false;
+    return hip_ok(phz_io_zero(*p, std::max<size_t>(bytes, 256), stream), what);
+  }
+  bool ensure_staging(size_t bytes) {
+    if (bytes <= staging_bytes) return true;
+    if (staging) hipFree(staging);
+    staging = nullptr;
+    staging_bytes = 0;
+    if (!hip_ok(hipMalloc((void**)&staging, bytes), "staging alloc")) return false;
+    staging_bytes = bytes;
+    return true;
+  }
+  // host [nworld][width] f64 -> device SoA
+  bool upload_rows(const double* host, void* dst, int width, const char* what) {
+    if (width <= 0) return true;
+    const size_t bytes = (size_t)nworld * width * sizeof(double);
+    if (!ensure_staging(bytes)) return false;
+    if (!hip_ok(hipMemcpyAsync(staging, host, bytes, hipMemcpyHostToDevice, stream), what)) return false;
+    return hip_ok(phz_io_pack(staging, dst, nworld, width, stride, f64 ? 1 : 0, stream), what);
+  }
+  bool download_rows(const void* src, double* host, int width, const char* what) {
+    if (width <= 0) return true;
+    const size_t bytes = (size_t)nworld * width * sizeof(double);
+    if (!ensure_staging(bytes)) return false;
+    if (!hip_ok(phz_io_unpack(src, staging, nworld, width, stride, f64 ? 1 : 0, stream), what)) return false;
+    if (!hip_ok(hipMemcpyAsync(host, staging, bytes, hipMemcpyDeviceToHost, stream), what)) return false;
+    return hip_ok(hipStreamSynchronize(stream), what);
+  }
+
+  bool compile() {
+    if (code) return true;
+    std::string e;
+    const std::string src = gen_source(model, feat, f64, block);
+    if (const char* dump = std::getenv("PHZ_DUMP_SOURCE")) {
+      std::ofstream out(dump);
+      out << src;
+    }
+    code = compile_source(src, e);
+    if (!code) { err = e; return false; }
+    return true;
+  }
+  bool load_kernel() {
+    if (fn) return true;
+    if (!compile()) return false;
+    if (!hip_ok(hipModuleLoadData(&module, code->code.data()), "hipModuleLoadData")) return false;
+    return hip_ok(hipModuleGetFunction(&fn, module, "phz_step"), "hipModuleGetFunction");
+  }
+  bool launch(int nsteps) {
+    StepArgs a{q, v, ctrl, qdd, targets, rng, rows, nworld, stride, nsteps, feat.contact ? 1 : 0};
+    void* params[] = {&a};
+    const unsigned grid = (unsigned)((nworld + block - 1) / block);
+    return hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
+                  "step kernel launch");
+  }
+  bool issue(uint32_t n) {
+    for (uint32_t done = 0; done < n;) {
+      const uint32_t k = std::min<uint32_t>(n - done, (uint32_t)max_steps);
+      if (!launch((int)k)) return false;
+      done += k;
+    }
+    return true;
+  }
+  bool step_many(uint32_t n) {
+    if (!has_device()) { err = "host-only sim (device_ordinal -1) cannot step"; return false; }
+    if (n == 0) return true;
+    if (nworld == 0) return true;
+    if (!load_kernel()) return false;
+    if (!graphs) return issue(n);
+    if (!(gexec && graph_steps == n && graph_epoch == epoch)) {
+      drop_graph();
+      if (!hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"))
+        return false;
+      const bool issued = issue(n);
+      hipGraph_t graph = nullptr;
+      // End the capture even when a launch failed (mod.rs:862-867).
+      hipError_t ec = hipStreamEndCapture(stream, &graph);
+      if (!issued) { if (graph) hipGraphDestroy(graph); return false; }
+      if (!hip_ok(ec, "hipStreamEndCapture")) return false;
+      hipError_t ei = hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0);
+      hipGraphDestroy(graph);
+      if (!hip_ok(ei, "hipGraphInstantiate")) { gexec = nullptr; return false; }
+      graph_steps = n;
+      graph_epoch = epoch;
+    }
+    return hip_ok(hipGraphLaunch(gexec, stream), "hipGraphLaunch");
+  }
+
+  ~phz_sim() {
+    if (has_device()) {
+      hipSetDevice(device);
+      if (stream) hipStreamSynchronize(stream);
+      drop_graph();
+      if (module) hipModuleUnload(module);
+      for (void* p : {q, v, ctrl, qdd, targets, rows, (void*)rng, (void*)staging})
+        if (p) hipFree(p);
+      if (stream) hipStreamDestroy(stream);
+    }
+  }
+};
+
+namespace {
+bool set_device(phz_sim* s) { return !s->has_device() || s->hip_ok(hipSetDevice(s->device), "hipSetDevice"); }
+
+int set_contact(phz_sim* s, double ground_h, double friction, const double* geom, const double* gains, double k,
+                double d, uint32_t* collidable_out) {
+  if (!geom) return s->fail("null geometry table");
+  if (!(std::isfinite(ground_h) && std::isfinite(friction))) return s->fail("ground height and friction must be finite");
+  const int nb = s->model.nb;
+  std::vector<double> g(geom, geom + (size_t)nb * kGeomStride);
+  int collidable = 0;
+  for (int i = 0; i < nb; i++) {
+    double* r = &g[(size_t)i * kGeomStride];
+    if (!is_int(r[0]) || r[0] < 0 || r[0] > 5) return s->fail(fmt("body %d: unknown geometry type %g", i, r[0]));
+    if (gains) { r[8] = gains[i * 2]; r[9] = gains[i * 2 + 1]; }
+    else { r[8] = k; r[9] = d; }
+    for (int q = 1; q < 22; q++)
+      if (!std::isfinite(r[q])) return s->fail(fmt("body %d: non-finite geometry slot %d", i, q));
+    if ((int)r[0] != 0) collidable++;
+  }
+  if (collidable == 0)
+    return s->fail("ground contact enabled but no body has GPU-collidable geometry "
+                   "(supported: sphere, box, capsule, cylinder, mesh)");
+  if (!set_device(s)) return 1;
+  s->feat.contact = true;
+  s->feat.ground_h = ground_h;
+  s->feat.mu = friction;
+  s->feat.geom = std::move(g);
+  s->feat.collidable = collidable;
+  if (s->has_device() && !s->rows) {
+    if (!s->alloc(&s->rows, (size_t)nb * 8 * s->stride * s->esize(), "contact rows alloc")) return 1;
+  }
+  s->invalidate();
+  if (collidable_out) *collidable_out = (uint32_t)collidable;
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t nv, const double gravity[3],
+                   double dt, uint32_t nworld, int precision, int device_ordinal, phz_sim** out) {
+  g_create_error.clear();
+  if (!out) { g_create_error = "null output pointer"; return 1; }
+  *out = nullptr;
+  if (precision != PHZ_F32 && precision != PHZ_F64) { g_create_error = "precision must be PHZ_F32 or PHZ_F64"; return 1; }
+  if (nworld > (1u << 28)) { g_create_error = "nworld too large"; return 1; }
+  auto s = std::make_unique<phz_sim>();
+  if (!parse_model(body_table, nb, nq, nv, gravity, dt, s->model, g_create_error)) return 1;
+  s->nworld = (int)nworld;
+  s->stride = (int)((nworld + 63) / 64 * 64);
+  s->f64 = precision == PHZ_F64;
+  s->device = device_ordinal;
+  s->block = env_int("PHZ_BLOCK", 64);
+  if (s->block != 64 && s->block != 128 && s->block != 256) s->block = 64;
+  s->max_steps = std::max(1, env_int("PHZ_MAX_STEPS_PER_LAUNCH", 1000));
+  const char* ge = std::getenv("PHZ_HIP_GRAPHS");
+  s->graphs = !(ge && (!std::strcmp(ge, "0") || !std::strcmp(ge, "off") || !std::strcmp(ge, "false")));
+  if (device_ordinal >= 0) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) { g_create_error = "no HIP device available"; return 1; }
+    if (device_ordinal >= count) { g_create_error = fmt("device ordinal %d out of range (%d devices)", device_ordinal, count); return 1; }
+    if (!s->hip_ok(hipSetDevice(device_ordinal), "hipSetDevice")) { g_create_error = s->err; return 1; }
+    if (!s->hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate")) {
+      g_create_error = s->err;
+      return 1;
+    }
+    const size_t E = s->esize(), S = (size_t)s->stride;
+    if (!s->alloc(&s->q, (size_t)nq * S * E, "alloc q") || !s->alloc(&s->v, (size_t)nv * S * E, "alloc v") ||
+        !s->alloc(&s->ctrl, (size_t)nv * S * E, "alloc ctrl") || !s->alloc(&s->qdd, (size_t)nv * S * E, "alloc qdd") ||
+        !s->alloc((void**)&s->rng, S * 8, "alloc rng") ||
+        !s->hip_ok(hipStreamSynchronize(s->stream), "create sync")) {
+      g_create_error = s->err;
+      return 1;
+    }
+  }
+  *out = s.release();
+  return 0;
+}
+
+void phz_sim_destroy(phz_sim* sim) {
+  if (sim) { set_device(sim); delete sim; }
+}
+
+const char* phz_last_error(const phz_sim* sim) { return sim ? sim->err.c_str() : g_create_error.c_str(); }
+
+int phz_set_model(phz_sim* s, const double* body_table, uint32_t nb, uint32_t nq, uint32_t nv, const double gravity[3],
+                  double dt) {
+  if (!s) return 1;
+  ModelD m;
+  std::string e;
+  if (!parse_model(body_table, nb, nq, nv, gravity, dt, m, e)) return s->fail(e);
+  if (m.nb != s->model.nb || m.nq != s->model.nq || m.nv != s->model.nv)
+    return s->fail(fmt("set_model: shape changed (%d bodies, nq %d, nv %d vs %d bodies, nq %d, nv %d); build a new simulator",
+                       m.nb, m.nq, m.nv, s->model.nb, s->model.nq, s->model.nv));
+  s->model = m;
+  s->invalidate();
+  return 0;
+}
+
+int phz_enable_ground_contact(phz_sim* s, double ground_height, double stiffness, double damping, double friction,
+                              const double* geom_table, uint32_t* collidable_out) {
+  if (!s) return 1;
+  if (!(std::isfinite(stiffness) && std::isfinite(damping))) return s->fail("stiffness and damping must be finite");
+  return set_contact(s, ground_height, friction, geom_table, nullptr, stiffness, damping, collidable_out);
+}
+
+int phz_enable_ground_contact_per_body(phz_sim* s, double ground_height, double friction, const double* gains,
+                                       const double* geom_table, uint32_t* collidable_out) {
+  if (!s) return 1;
+  if (!gains) return s->fail("null gains table");
+  return set_contact(s, ground_height, friction, geom_table, gains, 0.0, 0.0, collidable_out);
+}
+
+int phz_enable_pd_control(phz_sim* s, const double* dofs, uint32_t n) {
+  if (!s) return 1;
+  if (n == 0 || !dofs) return s->fail("PD pipeline needs at least one servoed DOF");
+  for (uint32_t d = 0; d < n; d++) {
+    const double* r = dofs + (size_t)d * kPdStride;
+    if (!is_int(r[0]) || !is_int(r[1]) || r[0] < 0 || r[1] < 0 || r[0] >= s->model.nq || r[1] >= s->model.nv)
+      return s->fail(fmt("PD DOF out of range: q_index %g (nq %d), v_index %g (nv %d)", r[0], s->model.nq, r[1], s->model.nv));
+    for (int k = 2; k < 5; k++) if (!std::isfinite(r[k])) return s->fail("PD gains must be finite");
+  }
+  if (!set_device(s)) return 1;
+  const bool same = s->feat.npd == (int)n;
+  s->feat.pd.assign(dofs, dofs + (size_t)n * kPdStride);
+  // Re-enabling with the same servo count keeps the targets (mod.rs:772-778).
+  if (s->has_device() && !same) {
+    if (s->targets) { hipFree(s->targets); s->targets = nullptr; }
+    if (!s->alloc(&s->targets, (size_t)n * s->stride * s->esize(), "targets alloc")) return 1;
+  }
+  s->feat.npd = (int)n;
+  s->invalidate();
+  return 0;
+}
+
+int phz_set_position_targets(phz_sim* s, const double* rows) {
+  if (!s) return 1;
+  if (s->feat.npd == 0) return s->fail("PD control not enabled — call enable_pd_control first");
+  if (!rows) return s->fail("null targets");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->upload_rows(rows, s->targets, s->feat.npd, "upload targets") ? 0 : 1;
+}
+
+int phz_enable_control_noise(phz_sim* s, uint64_t seed, int dist, double a, double b, const uint32_t* v_indices,
+                             uint32_t n) {
+  if (!s) return 1;
+  if (dist != PHZ_NOISE_NORMAL && dist != PHZ_NOISE_UNIFORM) return s->fail("unknown noise distribution");
+  if (!(std::isfinite(a) && std::isfinite(b))) return s->fail("noise parameters must be finite");
+  if (n > 0 && !v_indices) return s->fail("null DOF list");
+  std::vector<int> dofs;
+  for (uint32_t k = 0; k < n; k++) {
+    if (v_indices[k] >= (uint32_t)s->model.nv) return s->fail(fmt("noise DOF %u out of range (nv %d)", v_indices[k], s->model.nv));
+    dofs.push_back((int)v_indices[k]);
+  }
+  if (!set_device(s)) return 1;
+  s->feat.noise = n > 0;
+  s->feat.seed = seed;
+  s->feat.dist = dist;
+  s->feat.a = a;
+  s->feat.b = b;
+  s->feat.noise_dofs = dofs;
+  if (s->has_device() && !s->hip_ok(phz_io_seed(s->rng, seed, s->nworld, s->stream), "seed rng")) return 1;
+  s->invalidate();
+  return 0;
+}
+
+int phz_load_states(phz_sim* s, const double* q, const double* v, const double* ctrl) {
+  if (!s) return 1;
+  if (!q || !v) return s->fail("null q or v");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (!s->upload_rows(q, s->q, s->model.nq, "upload q") || !s->upload_rows(v, s->v, s->model.nv, "upload v")) return 1;
+  if (ctrl) {
+    if (!s->upload_rows(ctrl, s->ctrl, s->model.nv, "upload ctrl")) return 1;
+  } else if (!s->hip_ok(phz_io_zero(s->ctrl, (size_t)s->model.nv * s->stride * s->esize(), s->stream), "zero ctrl")) {
+    return 1;
+  }
+  if (s->feat.noise && !s->hip_ok(phz_io_seed(s->rng, s->feat.seed, s->nworld, s->stream), "seed rng")) return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "load_states") ? 0 : 1;
+}
+
+int phz_set_controls(phz_sim* s, const double* ctrl) {
+  if (!s) return 1;
+  if (!ctrl) return s->fail("null ctrl");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (!s->upload_rows(ctrl, s->ctrl, s->model.nv, "upload ctrl")) return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "set_controls") ? 0 : 1;
+}
+
+int phz_step(phz_sim* s) { return phz_step_many(s, 1); }
+
+int phz_step_many(phz_sim* s, uint32_t n) {
+  if (!s) return 1;
+  if (!set_device(s)) return 1;
+  return s->step_many(n) ? 0 : 1;
+}
+
+int phz_set_graphs_enabled(phz_sim* s, int on) {
+  if (!s) return 1;
+  s->graphs = on != 0;
+  if (!s->graphs) s->drop_graph();
+  return 0;
+}
+int phz_graphs_enabled(const phz_sim* s) { return s && s->graphs ? 1 : 0; }
+
+int phz_synchronize(phz_sim* s) {
+  if (!s) return 1;
+  if (!s->has_device()) return 0;
+  if (!set_device(s)) return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "synchronize") ? 0 : 1;
+}
+
+int phz_readback_states(phz_sim* s, double* q, double* v) {
+  if (!s) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (q && !s->download_rows(s->q, q, s->model.nq, "readback q")) return 1;
+  if (v && !s->download_rows(s->v, v, s->model.nv, "readback v")) return 1;
+  return 0;
+}
+int phz_readback_controls(phz_sim* s, double* ctrl) {
+  if (!s || !ctrl) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->download_rows(s->ctrl, ctrl, s->model.nv, "readback ctrl") ? 0 : 1;
+}
+int phz_readback_qdd(phz_sim* s, double* qdd) {
+  if (!s || !qdd) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->download_rows(s->qdd, qdd, s->model.nv, "readback qdd") ? 0 : 1;
+}
+int phz_readback_contacts(phz_sim* s, double* rows) {
+  if (!s) return 1;
+  if (!s->feat.contact) return s->fail("ground contact not enabled — call enable_ground_contact first");
+  if (!rows) return s->fail("null output");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->download_rows(s->rows, rows, s->model.nb * 8, "readback contacts") ? 0 : 1;
+}
+int phz_readback_rng(phz_sim* s, uint64_t* states) {
+  if (!s || !states) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (!s->hip_ok(hipMemcpyAsync(states, s->rng, (size_t)s->nworld * 8, hipMemcpyDeviceToHost, s->stream), "readback rng"))
+    return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "readback rng") ? 0 : 1;
+}
+int phz_load_rng(phz_sim* s, const uint64_t* states) {
+  if (!s || !states) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (!s->hip_ok(hipMemcpyAsync(s->rng, states, (size_t)s->nworld * 8, hipMemcpyHostToDevice, s->stream), "load rng"))
+    return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "load rng") ? 0 : 1;
+}
+int phz_collidable_bodies(const phz_sim* s) { return s && s->feat.contact ? s->feat.collidable : 0; }
+
+int phz_compile(phz_sim* s) {
+  if (!s) return 1;
+  return s->compile() ? 0 : 1;
+}
+
+int phz_time_step_many(phz_sim* s, uint32_t n, uint32_t reps, double* ms_per_rep) {
+  if (!s || !ms_per_rep) return 1;
+  if (!s->has_device()) return s->fail("host-only sim cannot step");
+  if (!set_device(s)) return 1;
+  if (!s->load_kernel()) return 1;
+  std::vector<hipEvent_t> ev(2 * (size_t)reps);
+  for (auto& e : ev)
+    if (!s->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
+  bool ok = true;
+  for (uint32_t r = 0; r < reps && ok; r++) {
+    ok = s->hip_ok(hipEventRecord(ev[2 * r], s->stream), "hipEventRecord") && s->step_many(n) &&
+         s->hip_ok(hipEventRecord(ev[2 * r + 1], s->stream), "hipEventRecord");
+  }
+  ok = ok && s->hip_ok(hipStreamSynchronize(s->stream), "timing sync");
+  for (uint32_t r = 0; r < reps && ok; r++) {
+    float ms = 0;
+    ok = s->hip_ok(hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]), "hipEventElapsedTime");
+    ms_per_rep[r] = ms;
+  }
+  for (auto& e : ev) hipEventDestroy(e);
+  return ok ? 0 : 1;
+}
+
+int phz_kernel_info(phz_sim* s, int64_t* info) {
+  if (!s || !info) return 1;
+  if (!s->compile()) return 1;
+  const std::string& log = s->code->log;
+  info[0] = remark_value(log, "VGPRs:");
+  info[1] = remark_value(log, "AGPRs:");
+  info[2] = remark_value(log, "SGPRs:");
+  info[3] = remark_value(log, "ScratchSize [bytes/lane]:");
+  info[4] = s->block;
+  info[5] = s->max_steps;
+  return 0;
+}
+
+}  // extern "C"

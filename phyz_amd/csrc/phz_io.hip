@@ -1,0 +1,80 @@
+// phz_io.hip — state layout kernels (ahead-of-time compiled for gfx950).
+//
+// The C ABI hands over world-major f64 rows (the reference wire layout,
+// crates/phyz-gpu/src/layout.rs:327-373); the step kernel keeps state as
+// structure-of-arrays [j][stride] in the sim's precision so that lane-per-world
+// loads and stores coalesce. These kernels convert between the two on device,
+// so a host upload or readback is one contiguous copy plus one launch.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+// dst[j * stride + w] = (T) src[w * width + j]
+template <class T>
+__global__ void pack_rows(const double* __restrict__ src, T* __restrict__ dst, int nworld, int width, int stride) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= nworld) return;
+  for (int j = 0; j < width; j++) dst[(size_t)j * stride + w] = (T)src[(size_t)w * width + j];
+}
+
+// dst[w * width + j] = (double) src[j * stride + w]
+template <class T>
+__global__ void unpack_rows(const T* __restrict__ src, double* __restrict__ dst, int nworld, int width, int stride) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= nworld) return;
+  for (int j = 0; j < width; j++) dst[(size_t)w * width + j] = (double)src[(size_t)j * stride + w];
+}
+
+template <class T> __global__ void fill_zero(T* __restrict__ dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = T(0);
+}
+
+// SplitMix64 world seeds (crates/phyz-gpu/src/policy_pipeline.rs:417-424).
+__global__ void seed_worlds(uint64_t* __restrict__ rng, uint64_t seed, int nworld) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= nworld) return;
+  uint64_t z = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(w + 1);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z = z ^ (z >> 31);
+  rng[w] = z ? z : 1;
+}
+
+constexpr int kBlock = 256;
+inline int blocks(size_t n) { return (int)((n + kBlock - 1) / kBlock); }
+
+}  // namespace
+
+extern "C" {
+
+hipError_t phz_io_pack(const double* src, void* dst, int nworld, int width, int stride, int f64, hipStream_t s) {
+  if (nworld <= 0 || width <= 0) return hipSuccess;
+  if (f64) hipLaunchKernelGGL(pack_rows<double>, dim3(blocks(nworld)), dim3(kBlock), 0, s, src, (double*)dst, nworld, width, stride);
+  else hipLaunchKernelGGL(pack_rows<float>, dim3(blocks(nworld)), dim3(kBlock), 0, s, src, (float*)dst, nworld, width, stride);
+  return hipGetLastError();
+}
+
+hipError_t phz_io_unpack(const void* src, double* dst, int nworld, int width, int stride, int f64, hipStream_t s) {
+  if (nworld <= 0 || width <= 0) return hipSuccess;
+  if (f64) hipLaunchKernelGGL(unpack_rows<double>, dim3(blocks(nworld)), dim3(kBlock), 0, s, (const double*)src, dst, nworld, width, stride);
+  else hipLaunchKernelGGL(unpack_rows<float>, dim3(blocks(nworld)), dim3(kBlock), 0, s, (const float*)src, dst, nworld, width, stride);
+  return hipGetLastError();
+}
+
+// Zero-fill with a kernel (no hipMemsetAsync, so a captured graph stays valid).
+hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  const size_t n = bytes / 4;
+  hipLaunchKernelGGL(fill_zero<uint32_t>, dim3(blocks(n)), dim3(kBlock), 0, s, (uint32_t*)dst, n);
+  return hipGetLastError();
+}
+
+hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s) {
+  if (nworld <= 0) return hipSuccess;
+  hipLaunchKernelGGL(seed_worlds, dim3(blocks(nworld)), dim3(kBlock), 0, s, rng, seed, nworld);
+  return hipGetLastError();
+}
+
+}  // extern "C"

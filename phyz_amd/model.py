@@ -1,0 +1,294 @@
+"""Model description and the f64 wire tables the C ABI takes.
+
+Host-side mirror of the reference's model types and packers:
+
+* ``SpatialInertia`` / ``SpatialTransform``  — phyz-math (tang) semantics:
+  inertia about the COM; transform ``rot`` = parent->joint coordinate map,
+  ``pos`` = joint origin in parent coordinates (crates/phyz-model/src/joint.rs:31-36).
+* ``Joint`` / ``ModelBuilder``               — crates/phyz-model/src/joint.rs:27-160,
+  crates/phyz-model/src/model.rs:379-551 (q/v offsets assigned in body order,
+  default gravity (0, 0, -9.81), dt 1e-3).
+* ``pack_bodies`` / ``pack_geometries`` / ``pack_pd_dofs`` — the slot layouts of
+  crates/phyz-gpu/src/layout.rs:19-93, in f64 instead of f32, with integer slots
+  stored as exact integer-valued doubles instead of bit casts.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+GRAVITY = 9.81
+
+# Joint type codes (layout.rs:23) and geometry codes (layout.rs:43).
+REVOLUTE, PRISMATIC, FIXED, BALL, FREE = 0, 1, 2, 3, 4
+G_NONE, G_SPHERE, G_BOX, G_CAPSULE, G_CYLINDER, G_MESH = 0, 1, 2, 3, 4, 5
+
+BODY_STRIDE = 36
+GEOM_STRIDE = 24
+PD_DOF_STRIDE = 8
+CONTACT_ROW = 8
+MAX_BODIES = 32
+
+_NDOF = {REVOLUTE: 1, PRISMATIC: 1, FIXED: 0, BALL: 3, FREE: 6}
+
+
+def joint_ndof(jtype: int) -> int:
+    return _NDOF[jtype]
+
+
+def _mat3(m) -> np.ndarray:
+    a = np.asarray(m, dtype=np.float64).reshape(3, 3)
+    return a.copy()
+
+
+def _vec3(v) -> np.ndarray:
+    return np.asarray(v, dtype=np.float64).reshape(3).copy()
+
+
+def rotation_axis_angle(axis, angle: float) -> np.ndarray:
+    """Rotation matrix of `angle` about unit `axis` (Rodrigues, active sense)."""
+    a = _vec3(axis)
+    a = a / np.linalg.norm(a)
+    k = np.array([[0, -a[2], a[1]], [a[2], 0, -a[0]], [-a[1], a[0], 0]])
+    return np.eye(3) + math.sin(angle) * k + (1 - math.cos(angle)) * (k @ k)
+
+
+@dataclasses.dataclass
+class SpatialTransform:
+    rot: np.ndarray = dataclasses.field(default_factory=lambda: np.eye(3))
+    pos: np.ndarray = dataclasses.field(default_factory=lambda: np.zeros(3))
+
+    @staticmethod
+    def identity() -> "SpatialTransform":
+        return SpatialTransform()
+
+    @staticmethod
+    def from_translation(p) -> "SpatialTransform":
+        return SpatialTransform(np.eye(3), _vec3(p))
+
+    @staticmethod
+    def new(rot, pos) -> "SpatialTransform":
+        return SpatialTransform(_mat3(rot), _vec3(pos))
+
+    def compose(self, other: "SpatialTransform") -> "SpatialTransform":
+        """self.compose(other): rot = self.rot @ other.rot, pos = other.pos + other.rot^T self.pos."""
+        return SpatialTransform(self.rot @ other.rot, other.pos + other.rot.T @ self.pos)
+
+
+@dataclasses.dataclass
+class SpatialInertia:
+    mass: float
+    com: np.ndarray
+    inertia: np.ndarray  # 3x3 about the COM
+
+    @staticmethod
+    def new(mass: float, com, inertia) -> "SpatialInertia":
+        return SpatialInertia(float(mass), _vec3(com), _mat3(inertia))
+
+    @staticmethod
+    def sphere(mass: float, radius: float) -> "SpatialInertia":
+        i = 0.4 * mass * radius * radius
+        return SpatialInertia.new(mass, np.zeros(3), np.eye(3) * i)
+
+    @staticmethod
+    def point_mass(mass: float, com) -> "SpatialInertia":
+        return SpatialInertia.new(mass, com, np.zeros((3, 3)))
+
+    @staticmethod
+    def rod(mass: float, half_len: float) -> "SpatialInertia":
+        """Uniform rod hanging along -Y from the joint (the reference test fixture)."""
+        length = 2.0 * half_len
+        i = mass * length * length / 12.0
+        return SpatialInertia.new(mass, [0.0, -half_len, 0.0], np.diag([i, 0.0, i]))
+
+
+@dataclasses.dataclass
+class Geometry:
+    """One collision shape per body (the device contacts through collisions[0]; layout.rs:199-208)."""
+    kind: int
+    params: Sequence[float] = ()  # sphere (r); box (hx, hy, hz); capsule (r, length); cylinder (r, height); mesh aabb (min3, max3)
+    origin: SpatialTransform = dataclasses.field(default_factory=SpatialTransform)
+
+    @staticmethod
+    def sphere(radius: float, origin: Optional[SpatialTransform] = None) -> "Geometry":
+        return Geometry(G_SPHERE, (radius,), origin or SpatialTransform())
+
+    @staticmethod
+    def box(half_extents, origin: Optional[SpatialTransform] = None) -> "Geometry":
+        return Geometry(G_BOX, tuple(half_extents), origin or SpatialTransform())
+
+    @staticmethod
+    def capsule(radius: float, length: float, origin: Optional[SpatialTransform] = None) -> "Geometry":
+        return Geometry(G_CAPSULE, (radius, length), origin or SpatialTransform())
+
+    @staticmethod
+    def cylinder(radius: float, height: float, origin: Optional[SpatialTransform] = None) -> "Geometry":
+        return Geometry(G_CYLINDER, (radius, height), origin or SpatialTransform())
+
+    @staticmethod
+    def mesh_aabb(lo, hi, origin: Optional[SpatialTransform] = None) -> "Geometry":
+        return Geometry(G_MESH, tuple(lo) + tuple(hi), origin or SpatialTransform())
+
+
+@dataclasses.dataclass
+class Joint:
+    jtype: int
+    parent_to_joint: SpatialTransform = dataclasses.field(default_factory=SpatialTransform)
+    axis: np.ndarray = dataclasses.field(default_factory=lambda: np.array([0.0, 0.0, 1.0]))
+    damping: float = 0.0
+    stiffness: float = 0.0
+    spring_ref: float = 0.0
+    armature: float = 0.0
+
+    def ndof(self) -> int:
+        return joint_ndof(self.jtype)
+
+
+@dataclasses.dataclass
+class Body:
+    name: str
+    parent: int
+    joint: Joint
+    inertia: SpatialInertia
+    geometry: Optional[Geometry] = None
+
+
+@dataclasses.dataclass
+class Model:
+    bodies: List[Body]
+    gravity: np.ndarray
+    dt: float
+    nq: int
+    nv: int
+    q_offsets: List[int]
+    v_offsets: List[int]
+
+    @property
+    def nbodies(self) -> int:
+        return len(self.bodies)
+
+    def default_state(self):
+        return np.zeros(self.nq), np.zeros(self.nv)
+
+
+class ModelBuilder:
+    """Builder with the reference's method names (model.rs:379-551)."""
+
+    def __init__(self):
+        self._bodies: List[Body] = []
+        self._gravity = np.array([0.0, 0.0, -GRAVITY])
+        self._dt = 0.001
+
+    def gravity(self, g) -> "ModelBuilder":
+        self._gravity = _vec3(g)
+        return self
+
+    def dt(self, dt: float) -> "ModelBuilder":
+        self._dt = float(dt)
+        return self
+
+    def add_body(self, name: str, parent: int, joint: Joint, inertia: SpatialInertia,
+                 geometry: Optional[Geometry] = None) -> "ModelBuilder":
+        self._bodies.append(Body(name, int(parent), joint, inertia, geometry))
+        return self
+
+    def add_revolute_body(self, name, parent, parent_to_joint, inertia, axis=(0.0, 0.0, 1.0), **kw):
+        return self.add_body(name, parent, Joint(REVOLUTE, parent_to_joint, _vec3(axis), **kw), inertia)
+
+    def add_prismatic_body(self, name, parent, parent_to_joint, axis, inertia, **kw):
+        return self.add_body(name, parent, Joint(PRISMATIC, parent_to_joint, _vec3(axis), **kw), inertia)
+
+    def add_spherical_body(self, name, parent, parent_to_joint, inertia, **kw):
+        return self.add_body(name, parent, Joint(BALL, parent_to_joint, np.zeros(3), **kw), inertia)
+
+    def add_free_body(self, name, parent, parent_to_joint, inertia, geometry=None):
+        return self.add_body(name, parent, Joint(FREE, parent_to_joint, np.zeros(3)), inertia, geometry)
+
+    def add_fixed_body(self, name, parent, parent_to_joint, inertia, geometry=None):
+        return self.add_body(name, parent, Joint(FIXED, parent_to_joint, np.zeros(3)), inertia, geometry)
+
+    def build(self) -> Model:
+        nq = nv = 0
+        qo, vo = [], []
+        for b in self._bodies:
+            qo.append(nq)
+            vo.append(nv)
+            nq += b.joint.ndof()
+            nv += b.joint.ndof()
+        return Model(list(self._bodies), self._gravity.copy(), self._dt, nq, nv, qo, vo)
+
+
+def pack_bodies(model: Model) -> np.ndarray:
+    """Body table, nb x 36 f64, layout.rs:19-38 slot meanings (pack_bodies, layout.rs:103-156)."""
+    nb = model.nbodies
+    t = np.zeros((nb, BODY_STRIDE), dtype=np.float64)
+    for i, b in enumerate(model.bodies):
+        j = b.joint
+        t[i, 0] = b.parent
+        t[i, 1] = j.jtype
+        t[i, 2] = model.q_offsets[i]
+        t[i, 3] = model.v_offsets[i]
+        t[i, 4] = b.inertia.mass
+        t[i, 5:8] = b.inertia.com
+        I = b.inertia.inertia
+        t[i, 8:14] = [I[0, 0], I[1, 1], I[2, 2], I[0, 1], I[0, 2], I[1, 2]]
+        t[i, 14:23] = j.parent_to_joint.rot.reshape(9)
+        t[i, 23:26] = j.parent_to_joint.pos
+        t[i, 26:29] = j.axis
+        t[i, 29] = j.damping
+        t[i, 30] = j.stiffness
+        t[i, 31] = j.spring_ref
+        t[i, 32] = j.armature
+    return t
+
+
+def pack_geometries(model: Model, stiffness: float = 0.0, damping: float = 0.0,
+                    gains: Optional[Sequence] = None):
+    """Geometry table, nb x 24 f64 (pack_geometries, layout.rs:182-280).
+
+    Returns (table, collidable_count). `gains` is a per-body list of
+    (stiffness, damping); otherwise the global pair is written to every body.
+    """
+    nb = model.nbodies
+    g = np.zeros((nb, GEOM_STRIDE), dtype=np.float64)
+    collidable = 0
+    for i, b in enumerate(model.bodies):
+        g[i, 13:22] = np.eye(3).reshape(9)
+        geo = b.geometry
+        if geo is not None:
+            g[i, 10:13] = geo.origin.pos
+            g[i, 13:22] = geo.origin.rot.reshape(9)
+            g[i, 0] = geo.kind
+            p = list(geo.params)
+            g[i, 1:1 + len(p)] = p
+            collidable += 1
+        if gains is not None:
+            g[i, 8], g[i, 9] = gains[i]
+        else:
+            g[i, 8], g[i, 9] = stiffness, damping
+    return g, collidable
+
+
+def uniform_frequency_gains(model: Model, omega: float, zeta: float):
+    """BodyContactGains::uniform_frequency (contact_pipeline.rs:293-305): k = m w^2, d = 2 zeta m w."""
+    return [(b.inertia.mass * omega * omega, 2.0 * zeta * b.inertia.mass * omega) for b in model.bodies]
+
+
+@dataclasses.dataclass
+class PdDof:
+    q_index: int
+    v_index: int
+    kp: float
+    kd: float
+    max_force: float
+
+
+def pack_pd_dofs(dofs: Sequence[PdDof]) -> np.ndarray:
+    """PD table, n x 8 f64 (pack_pd_dofs, layout.rs:314-325)."""
+    t = np.zeros((len(dofs), PD_DOF_STRIDE), dtype=np.float64)
+    for i, d in enumerate(dofs):
+        t[i, :5] = [d.q_index, d.v_index, d.kp, d.kd, d.max_force]
+    return t

@@ -1,0 +1,207 @@
+"""BatchSim — Python binding with the reference's batched-simulator surface.
+
+Method names, argument meaning and error behaviour follow
+crates/phyz-gpu/src/cuda/mod.rs:430-1003 (BatchSim<B>): build from a model and
+a world count, optionally enable ground contact and PD servos, then
+load_states / set_controls / step / step_many / readback_states /
+readback_contacts. Errors raise PhzError with the library's message, where the
+reference returns Err(String) (try_step, enable_*) or panics (step).
+Everything here calls the HIP library through its C ABI; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from .model import Model, PdDof, pack_bodies, pack_geometries, pack_pd_dofs
+
+F32, F64 = 0, 1
+NOISE_NORMAL, NOISE_UNIFORM = 0, 1
+
+
+class PhzError(RuntimeError):
+    pass
+
+
+def _dp(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(_lib.dp)
+
+
+def _rows(a, n, width, name) -> np.ndarray:
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.float64))
+    if a.shape != (n, width):
+        raise ValueError(f"{name}: expected shape {(n, width)}, got {a.shape}")
+    return a
+
+
+class BatchSim:
+    """`nworld` copies of one model stepped in lockstep on one MI355X."""
+
+    def __init__(self, model: Model, nworld: int, precision: str = "f32", device: int = 0):
+        self._L = _lib.load()
+        self.model = model
+        self.nworld = int(nworld)
+        self.precision = precision
+        self.nb, self.nq, self.nv = model.nbodies, model.nq, model.nv
+        self._npd = 0
+        table = np.ascontiguousarray(pack_bodies(model))
+        g = np.ascontiguousarray(model.gravity, dtype=np.float64)
+        h = C.c_void_p()
+        rc = self._L.phz_sim_create(_dp(table), self.nb, self.nq, self.nv, _dp(g), float(model.dt), self.nworld,
+                                    F64 if precision == "f64" else F32, int(device), C.byref(h))
+        if rc != 0:
+            raise PhzError(self._L.phz_last_error(None).decode())
+        self._h = h
+
+    # ── lifecycle ──
+    def close(self):
+        if getattr(self, "_h", None):
+            self._L.phz_sim_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int):
+        if rc != 0:
+            raise PhzError(self._L.phz_last_error(self._h).decode())
+
+    # ── model / configuration ──
+    def set_model(self, model: Model):
+        table = np.ascontiguousarray(pack_bodies(model))
+        g = np.ascontiguousarray(model.gravity, dtype=np.float64)
+        self._check(self._L.phz_set_model(self._h, _dp(table), model.nbodies, model.nq, model.nv, _dp(g), float(model.dt)))
+        self.model = model
+
+    def enable_ground_contact(self, ground_height: float, stiffness: float, damping: float, friction: float,
+                              geometry: Optional[np.ndarray] = None) -> int:
+        geom = pack_geometries(self.model)[0] if geometry is None else geometry
+        geom = np.ascontiguousarray(geom, dtype=np.float64)
+        n = C.c_uint32(0)
+        self._check(self._L.phz_enable_ground_contact(self._h, float(ground_height), float(stiffness), float(damping),
+                                                      float(friction), _dp(geom), C.byref(n)))
+        return int(n.value)
+
+    def enable_ground_contact_per_body(self, ground_height: float, friction: float, gains: Sequence,
+                                       geometry: Optional[np.ndarray] = None) -> int:
+        if len(gains) != self.nb:
+            raise PhzError(f"body_gains has {len(gains)} entries but the model has {self.nb} bodies")
+        geom = pack_geometries(self.model)[0] if geometry is None else geometry
+        geom = np.ascontiguousarray(geom, dtype=np.float64)
+        kd = np.ascontiguousarray(np.asarray(gains, dtype=np.float64).reshape(self.nb, 2))
+        n = C.c_uint32(0)
+        self._check(self._L.phz_enable_ground_contact_per_body(self._h, float(ground_height), float(friction), _dp(kd),
+                                                               _dp(geom), C.byref(n)))
+        return int(n.value)
+
+    def enable_pd_control(self, dofs: Sequence[PdDof]):
+        t = np.ascontiguousarray(pack_pd_dofs(dofs)) if len(dofs) else np.zeros((0, 8))
+        self._check(self._L.phz_enable_pd_control(self._h, _dp(t) if len(dofs) else None, len(dofs)))
+        self._npd = len(dofs)
+
+    def set_position_targets(self, targets):
+        if self._npd == 0:
+            self._check(self._L.phz_set_position_targets(self._h, None))
+        self._check(self._L.phz_set_position_targets(self._h, _dp(_rows(targets, self.nworld, self._npd, "targets"))))
+
+    def enable_control_noise(self, seed: int, dist: int, a: float, b: float, dofs: Sequence[int]):
+        arr = (C.c_uint32 * max(len(dofs), 1))(*dofs)
+        self._check(self._L.phz_enable_control_noise(self._h, int(seed), int(dist), float(a), float(b), arr, len(dofs)))
+
+    # ── state I/O ──
+    def load_states(self, q, v, ctrl=None):
+        qq = _rows(q, self.nworld, self.nq, "q")
+        vv = _rows(v, self.nworld, self.nv, "v")
+        cc = None if ctrl is None else _rows(ctrl, self.nworld, self.nv, "ctrl")
+        self._check(self._L.phz_load_states(self._h, _dp(qq), _dp(vv), _dp(cc)))
+
+    def set_controls(self, ctrl):
+        self._check(self._L.phz_set_controls(self._h, _dp(_rows(ctrl, self.nworld, self.nv, "ctrl"))))
+
+    def readback_states(self):
+        q = np.zeros((self.nworld, self.nq))
+        v = np.zeros((self.nworld, self.nv))
+        self._check(self._L.phz_readback_states(self._h, _dp(q), _dp(v)))
+        return q, v
+
+    def readback_contacts(self) -> np.ndarray:
+        rows = np.zeros((self.nworld, self.nb, 8))
+        self._check(self._L.phz_readback_contacts(self._h, _dp(rows)))
+        return rows
+
+    def readback_controls(self) -> np.ndarray:
+        c = np.zeros((self.nworld, self.nv))
+        self._check(self._L.phz_readback_controls(self._h, _dp(c)))
+        return c
+
+    def readback_qdd(self) -> np.ndarray:
+        a = np.zeros((self.nworld, self.nv))
+        self._check(self._L.phz_readback_qdd(self._h, _dp(a)))
+        return a
+
+    def readback_rng(self) -> np.ndarray:
+        r = np.zeros(self.nworld, dtype=np.uint64)
+        self._check(self._L.phz_readback_rng(self._h, r.ctypes.data_as(_lib.u64p)))
+        return r
+
+    def load_rng(self, states):
+        r = np.ascontiguousarray(np.asarray(states, dtype=np.uint64))
+        self._check(self._L.phz_load_rng(self._h, r.ctypes.data_as(_lib.u64p)))
+
+    # ── stepping ──
+    def step(self):
+        self._check(self._L.phz_step(self._h))
+
+    def try_step(self):
+        self.step()
+
+    def step_many(self, n: int):
+        self._check(self._L.phz_step_many(self._h, int(n)))
+
+    def synchronize(self):
+        self._check(self._L.phz_synchronize(self._h))
+
+    def set_graphs_enabled(self, on: bool):
+        self._check(self._L.phz_set_graphs_enabled(self._h, 1 if on else 0))
+
+    @property
+    def graphs_enabled(self) -> bool:
+        return bool(self._L.phz_graphs_enabled(self._h))
+
+    @property
+    def collidable_bodies(self) -> int:
+        return int(self._L.phz_collidable_bodies(self._h))
+
+    # ── build / measurement ──
+    def compile(self):
+        self._check(self._L.phz_compile(self._h))
+
+    def kernel_info(self) -> dict:
+        info = (C.c_int64 * 6)()
+        self._check(self._L.phz_kernel_info(self._h, info))
+        keys = ("vgpr", "agpr", "sgpr", "scratch_bytes", "block", "max_steps_per_launch")
+        return dict(zip(keys, [int(x) for x in info]))
+
+    def time_step_many(self, n: int, reps: int) -> np.ndarray:
+        ms = np.zeros(reps)
+        self._check(self._L.phz_time_step_many(self._h, int(n), int(reps), _dp(ms)))
+        return ms
+
+
+def from_workload(w, precision: str, nworld: Optional[int] = None, device: int = 0) -> BatchSim:
+    """A BatchSim configured for a phyz_amd.workloads.Workload (contact, PD, control noise)."""
+    n = w.nworld if nworld is None else nworld
+    sim = BatchSim(w.model, n, precision, device)
+    if w.contact is not None:
+        sim.enable_ground_contact(w.contact.ground_height, w.contact.stiffness, w.contact.damping, w.contact.friction)
+    if w.pd is not None:
+        sim.enable_pd_control(w.pd)
+    if w.noise is not None:
+        sim.enable_control_noise(w.noise.seed, w.noise.dist, w.noise.a, w.noise.b, w.noise.dofs)
+    return sim

@@ -1,0 +1,155 @@
+"""HIP step kernel against the f64 oracle, through the C ABI (BatchSim).
+
+Per-step parity follows the reference's GPU-vs-CPU suites
+(crates/phyz-gpu/tests/cuda_vs_cpu.rs:183-397) with the tolerances of the
+north star: qdd normwise relative error <= 1e-10 per step on the f64 kernels,
+<= 1e-4 on the f32 kernels. Inputs are the workloads' seeded states, plus
+states taken from an oracle rollout so that contact, PD saturation and fast
+joints are exercised.
+"""
+import numpy as np
+import pytest
+
+from phyz_amd import workloads as W
+from phyz_amd.sim import BatchSim, from_workload
+from tests.helpers import abs_err_rows, as_precision, oracle_for, rel_err_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL_QDD = {"f64": 1e-10, "f32": 1e-4}
+CASES = [(1, "f64"), (2, "f64"), (2, "f32"), (3, "f32"), (4, "f32"), (4, "f64"), (5, "f64")]
+
+
+def _states(w, orc, nworld, warm_steps):
+    q, v, c, tg = w.initial_state(nworld)
+    if warm_steps:
+        rng = orc.rng_states(nworld)
+        orc.step_batch(q, v, c, warm_steps, targets=tg, rng=rng, threads=8)
+    return q, v, c, tg
+
+
+def _cpu_step(orc, w, q0, v0, ctrl):
+    """One oracle step from (q0, v0) with the controls the device applied."""
+    n = q0.shape[0]
+    qdd = np.zeros((n, w.model.nv))
+    q1, v1 = np.zeros_like(q0), np.zeros_like(v0)
+    rows = np.zeros((n, w.model.nbodies, 8))
+    for k in range(n):
+        ext = None
+        if w.contact is not None:
+            ext, rows[k] = orc.contact(q0[k], v0[k])
+        qdd[k] = orc.aba(q0[k], v0[k], ctrl[k], ext)
+        q1[k], v1[k] = orc.integrate(q0[k], v0[k], qdd[k])
+    return qdd, q1, v1, rows
+
+
+@pytest.mark.parametrize("cfg,prec", CASES)
+@pytest.mark.parametrize("warm", [0, 300])
+def test_step_parity(cfg, prec, warm):
+    w = W.config(cfg)
+    orc = oracle_for(w)
+    nworld = 200  # not a multiple of the 64-lane wave: exercises the tail guard
+    q, v, c, tg = _states(w, orc, nworld, warm)
+    q, v, c = (as_precision(a, prec) for a in (q, v, c))
+    sim = from_workload(w, prec, nworld=nworld)
+    sim.load_states(q, v, c)
+    if tg is not None:
+        tg = as_precision(tg, prec)
+        sim.set_position_targets(tg)
+    sim.step()
+    qg, vg = sim.readback_states()
+    ctrl = sim.readback_controls()
+    qdd = sim.readback_qdd()
+    print(f"cfg {cfg} {prec} warm {warm}: kernel {sim.kernel_info()}", flush=True)
+
+    # Controls the device applied: PD law and the control stream.
+    if w.pd is not None:
+        for d in w.pd:
+            tau = np.clip(d.kp * (tg[:, d.q_index] - q[:, d.q_index]) - d.kd * v[:, d.v_index], -d.max_force, d.max_force)
+            tol = 1e-12 if prec == "f64" else 1e-5
+            assert np.allclose(ctrl[:, d.v_index], tau, rtol=tol, atol=tol * d.max_force)
+    if w.noise is not None and prec == "f64" and warm == 0:
+        # Replay of the per-world stream (oracle draws in f64 with 53-bit uniforms).
+        rng = orc.rng_states(nworld)
+        qc, vc, cc = q.copy(), v.copy(), c.copy()
+        orc.step_batch(qc, vc, cc, 1, targets=tg, rng=rng, threads=8)
+        np.testing.assert_allclose(ctrl[:, w.noise.dofs], cc[:, w.noise.dofs], rtol=1e-13, atol=1e-13)
+
+    ctrl_in = as_precision(ctrl, prec)
+    qdd_c, q1_c, v1_c, rows_c = _cpu_step(orc, w, q, v, ctrl_in)
+    e = rel_err_rows(qdd, qdd_c)
+    print(f"  qdd rel err max {e.max():.3e} median {np.median(e):.3e}", flush=True)
+    assert np.all(np.isfinite(qdd))
+    tol = np.full(nworld, TOL_QDD[prec])
+    if prec == "f32" and w.contact is not None:
+        # Stick-regime friction (slip speed / 1e-3, phyz_kernels.cu:542) amplifies
+        # f32 rounding of the contact-point velocity ~1000x, so the law evaluated
+        # in f32 arithmetic has its own per-step floor, sometimes above 1e-4. Each
+        # world is held to max(1e-4, 4 x that floor).
+        floor = np.array([rel_err_rows(orc.qdd_f32(q[k], v[k], ctrl_in[k]), qdd_c[k]) for k in range(nworld)])
+        tol = np.maximum(tol, 4.0 * floor)
+        print(f"  f32 floor max {floor.max():.3e}; worlds within 1e-4: {(e <= 1e-4).mean():.3f}", flush=True)
+    assert np.all(e <= tol), f"qdd rel err {e.max():.3e} (world {e.argmax()})"
+    scale_v = np.maximum(np.abs(v1_c).max(axis=1), 1.0)
+    assert (abs_err_rows(vg, v1_c) / scale_v).max() <= 10 * TOL_QDD[prec]
+    assert abs_err_rows(qg, q1_c).max() <= 10 * TOL_QDD[prec] * max(1.0, np.abs(q1_c).max())
+    if w.contact is not None:
+        rows = sim.readback_contacts()
+        touching = rows_c[:, :, 0] > 0
+        if warm:
+            assert touching.any(), "warm state should be in contact"
+        agree = (rows[:, :, 0] > 0) == touching
+        assert agree.mean() > 0.99
+        both = agree & touching
+        if both.any():
+            f_err = np.abs(rows[:, :, 5:8] - rows_c[:, :, 5:8]).max(axis=-1)[both]
+            f_scale = np.maximum(np.abs(rows_c[:, :, 5:8]).max(axis=-1)[both], 1.0)
+            print(f"  contact rows: {both.sum()} touching, force rel err {(f_err / f_scale).max():.3e}", flush=True)
+            assert (f_err / f_scale).max() <= (1e-9 if prec == "f64" else 1e-3)
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+def test_graph_replay_bit_identical(prec):
+    """Graph replay equals direct launches bit for bit (cuda_vs_cpu.rs:1295-1378),
+    and one 10-step span equals ten 1-step spans."""
+    w = W.config(2)
+    q, v, c, _ = w.initial_state(128)
+    outs = []
+    for graphs, chunks in ((True, [10]), (False, [10]), (False, [1] * 10), (True, [3, 7])):
+        sim = from_workload(w, prec, nworld=128)
+        sim.set_graphs_enabled(graphs)
+        sim.load_states(q, v, c)
+        for n in chunks:
+            sim.step_many(n)
+        outs.append(sim.readback_states())
+    for o in outs[1:]:
+        assert np.array_equal(o[0], outs[0][0]) and np.array_equal(o[1], outs[0][1])
+
+
+def test_worlds_independent_and_nan_isolated():
+    """A NaN injected into one world stays in that world (no cross-world state)."""
+    w = W.config(3)
+    q, v, c, _ = w.initial_state(130)
+    q[7, 6] = np.nan
+    sim = from_workload(w, "f32", nworld=130)
+    sim.load_states(q, v, c)
+    sim.step_many(20)
+    qg, vg = sim.readback_states()
+    bad = ~np.isfinite(qg).all(axis=1) | ~np.isfinite(vg).all(axis=1)
+    assert bad[7]
+    assert not bad[np.arange(130) != 7].any()
+
+
+def test_trajectory_f64_double_pendulum():
+    """500 f64 steps of the README double pendulum against the oracle rollout."""
+    w = W.config(1)
+    orc = oracle_for(w)
+    q, v, c, _ = w.initial_state(256)
+    sim = from_workload(w, "f64", nworld=256)
+    sim.load_states(q, v, c)
+    sim.step_many(500)
+    qg, vg = sim.readback_states()
+    orc.step_batch(q, v, c, 500, threads=8)
+    err = np.maximum(abs_err_rows(qg, q), abs_err_rows(vg, v))
+    print(f"500-step max state divergence {err.max():.3e} (median {np.median(err):.3e})", flush=True)
+    assert np.median(err) <= 1e-8
