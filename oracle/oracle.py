@@ -76,15 +76,22 @@ COUNTERS = ("add", "mul", "div", "sqrt", "trans", "other")
 class Oracle:
     """f64 CPU restatement of one model's step (see oracle/phz_oracle.hpp)."""
 
-    def __init__(self, model, contact=None, pd=None, noise=None):
-        from phyz_amd.model import pack_bodies
+    def __init__(self, model=None, contact=None, pd=None, noise=None, tables=None):
+        """From a phyz_amd.model.Model, or from raw tables=(body_table, nq, nv, gravity, dt)."""
         L = lib()
-        self.model = model
-        self.nb, self.nq, self.nv = model.nbodies, model.nq, model.nv
-        table = np.ascontiguousarray(pack_bodies(model))
-        g = np.ascontiguousarray(model.gravity, dtype=np.float64)
+        if tables is not None:
+            table, nq, nv, gravity, dt = tables
+            self.model = None
+            self.nb, self.nq, self.nv = table.shape[0], int(nq), int(nv)
+        else:
+            from phyz_amd.model import pack_bodies
+            table, gravity, dt = pack_bodies(model), model.gravity, model.dt
+            self.model = model
+            self.nb, self.nq, self.nv = model.nbodies, model.nq, model.nv
+        table = np.ascontiguousarray(table, dtype=np.float64)
+        g = np.ascontiguousarray(gravity, dtype=np.float64)
         err = C.create_string_buffer(256)
-        h = L.orc_model_create(_d(table), self.nb, self.nq, self.nv, _d(g), float(model.dt), err, 256)
+        h = L.orc_model_create(_d(table), self.nb, self.nq, self.nv, _d(g), float(dt), err, 256)
         if not h:
             raise ValueError(err.value.decode())
         self._h = C.c_void_p(h)

@@ -1,0 +1,146 @@
+"""C ABI and host logic, without a GPU.
+
+The library loads, exports every symbol include/phyz_amd.h declares, rejects
+the inputs the reference rejects with the reference's messages
+(crates/phyz-gpu/src/cuda/mod.rs:498-510, 573-597, 765-796, 988-997;
+crates/phyz-gpu/src/layout.rs:281-311), and compiles model-specialised kernels
+on a host-only sim (device ordinal -1). Packing follows layout.rs slot for slot.
+"""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from phyz_amd import _lib
+from phyz_amd import workloads as W
+from phyz_amd.model import (BODY_STRIDE, FREE, Geometry, Joint, ModelBuilder, PdDof, SpatialInertia,
+                            SpatialTransform, pack_bodies, pack_geometries, pack_pd_dofs, rotation_axis_angle)
+from phyz_amd.sim import BatchSim, PhzError
+from tests import models as TM
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "phyz_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(phz_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = C.CDLL(_lib.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    for s in syms:
+        assert hasattr(L, s), f"{s} declared in include/phyz_amd.h but not exported"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def host_sim(model, n=8, prec="f32"):
+    return BatchSim(model, n, prec, device=-1)
+
+
+def test_rejects_oversized_and_malformed_models():
+    b = ModelBuilder()
+    for i in range(33):
+        b.add_revolute_body(f"l{i}", i - 1, SpatialTransform.identity(), SpatialInertia.sphere(1.0, 0.1))
+    with pytest.raises(PhzError, match="33 bodies but the kernels hold at most 32"):
+        host_sim(b.build())
+    m = TM.double_pendulum_offset()
+    t = pack_bodies(m)
+    L = _lib.load()
+    g = np.asarray(m.gravity, dtype=np.float64)
+    h = C.c_void_p()
+    assert L.phz_sim_create(t.ctypes.data_as(_lib.dp), 2, 2, 3, g.ctypes.data_as(_lib.dp), 0.001, 4, 0, -1, C.byref(h)) != 0
+    assert "nq == nv" in L.phz_last_error(None).decode()
+    bad = t.copy()
+    bad[1, 0] = 1.0  # body 1 its own parent
+    assert L.phz_sim_create(bad.ctypes.data_as(_lib.dp), 2, 2, 2, g.ctypes.data_as(_lib.dp), 0.001, 4, 0, -1, C.byref(h)) != 0
+    assert "topological" in L.phz_last_error(None).decode()
+    bad = t.copy()
+    bad[0, 4] = np.nan
+    assert L.phz_sim_create(bad.ctypes.data_as(_lib.dp), 2, 2, 2, g.ctypes.data_as(_lib.dp), 0.001, 4, 0, -1, C.byref(h)) != 0
+    bad = t.copy()
+    bad[1, 2] = 5.0  # q offset past nq
+    assert L.phz_sim_create(bad.ctypes.data_as(_lib.dp), 2, 2, 2, g.ctypes.data_as(_lib.dp), 0.001, 4, 0, -1, C.byref(h)) != 0
+
+
+def test_error_paths_match_reference():
+    s = host_sim(TM.double_pendulum_offset())
+    with pytest.raises(PhzError, match="no body has GPU-collidable geometry"):
+        s.enable_ground_contact(0.0, 1.0, 1.0, 0.5)
+    with pytest.raises(PhzError, match="ground contact not enabled"):
+        s.readback_contacts()
+    with pytest.raises(PhzError, match="PD control not enabled"):
+        s.set_position_targets(np.zeros((8, 1)))
+    with pytest.raises(PhzError, match="PD pipeline needs at least one servoed DOF"):
+        s.enable_pd_control([])
+    with pytest.raises(PhzError, match="PD DOF out of range"):
+        s.enable_pd_control([PdDof(5, 0, 1.0, 0.1, 1.0)])
+    with pytest.raises(PhzError, match="shape changed"):
+        s.set_model(TM.arm_6dof())
+    with pytest.raises(PhzError, match="host-only"):
+        s.step()
+    with pytest.raises(PhzError, match="out of range"):
+        s.enable_control_noise(1, 0, 0.0, 1.0, [7])
+
+
+def test_set_model_same_shape_and_collidable_count():
+    m = TM.shapes()["sphere"]
+    s = host_sim(m)
+    assert s.enable_ground_contact(0.0, 1e4, 100.0, 0.5) == 1
+    assert s.collidable_bodies == 1
+    m2 = TM.shapes()["box"]
+    s.set_model(m2)  # same shape: accepted, kernel recompiled lazily
+    s.compile()
+
+
+def test_host_only_sim_compiles_workload_kernels():
+    """hiprtc compiles the gfx950 step kernel for every workload without a GPU."""
+    for idx in W.ALL:
+        w = W.config(idx)
+        from phyz_amd.sim import from_workload
+        s = from_workload(w, w.precisions[0], nworld=64, device=-1)
+        s.compile()
+        info = s.kernel_info()
+        assert info["vgpr"] > 0 and info["block"] == 64
+
+
+def test_pack_bodies_slots():
+    """layout.rs:19-38 slot meanings."""
+    rot = rotation_axis_angle([0, 0, 1], 0.3)
+    m = (ModelBuilder()
+         .add_body("a", -1, Joint(FREE, SpatialTransform.new(rot, [1, 2, 3]), np.zeros(3)),
+                   SpatialInertia.new(2.0, [0.1, 0.2, 0.3], [[1, 0.1, 0.2], [0.1, 2, 0.3], [0.2, 0.3, 3]]))
+         .add_revolute_body("b", 0, SpatialTransform.from_translation([0, 0, -1]), SpatialInertia.sphere(1, 0.1),
+                            axis=(0, 1, 0), damping=0.5, stiffness=2.0, spring_ref=0.1, armature=0.01)
+         .build())
+    t = pack_bodies(m)
+    assert t.shape == (2, BODY_STRIDE)
+    assert list(t[0, :5]) == [-1, 4, 0, 0, 2.0] and list(t[1, :4]) == [0, 0, 6, 6]
+    np.testing.assert_array_equal(t[0, 5:8], [0.1, 0.2, 0.3])
+    np.testing.assert_array_equal(t[0, 8:14], [1, 2, 3, 0.1, 0.2, 0.3])
+    np.testing.assert_array_equal(t[0, 14:23], rot.reshape(9))
+    np.testing.assert_array_equal(t[0, 23:26], [1, 2, 3])
+    np.testing.assert_array_equal(t[1, 26:33], [0, 1, 0, 0.5, 2.0, 0.1, 0.01])
+    g, n = pack_geometries(m, 10.0, 2.0)
+    assert n == 0 and g[0, 13] == 1 and g[0, 17] == 1 and g[0, 21] == 1 and g[0, 8] == 10.0 and g[0, 9] == 2.0
+    pd = pack_pd_dofs([PdDof(6, 6, 30.0, 2.0, 25.0)])
+    np.testing.assert_array_equal(pd[0, :5], [6, 6, 30.0, 2.0, 25.0])
+
+
+@pytest.mark.parametrize("idx,nb,nv", [(1, 2, 2), (2, 7, 7), (3, 9, 14), (4, 22, 27), (5, 25, 24)])
+def test_workload_shapes(idx, nb, nv):
+    """Body counts and widths of the five workloads."""
+    w = W.config(idx)
+    assert w.model.nbodies == nb and w.model.nv == nv and w.model.nq == nv
+    q, v, c, tg = w.initial_state(16)
+    assert q.shape == (16, nv) and np.isfinite(q).all()
+    if idx == 3:
+        assert sum(1 for b in w.model.bodies if b.geometry is not None) == 4
+    if idx == 4:
+        assert sum(1 for b in w.model.bodies if b.geometry is not None) == 10
+        assert sum(1 for b in w.model.bodies if b.joint.jtype == 0) == 21
+    if idx == 5:
+        assert tg.shape == (16, 24) and len(w.pd) == 24
