@@ -108,7 +108,7 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
     }
 
 
-def cpu_baseline(w, sim, prec, budget_s=12.0):
+def cpu_baseline(w, sim, prec, budget_s=20.0):
     """Oracle (f64 port of the reference CPU step) on the host cores, on a bounded
     sample of the workload; plus a one-step parity check of the sampled worlds."""
     from tests.helpers import as_precision, oracle_for, rel_err_rows
@@ -164,8 +164,8 @@ def cpu_baseline(w, sim, prec, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=1000)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's rollout length)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: one timed span)")
     ap.add_argument("--workload", type=int, default=2)
     ap.add_argument("--reps", type=int, default=7)
     ap.add_argument("--no-cpu", action="store_true")
@@ -190,6 +190,10 @@ def main():
 
     from phyz_amd import workloads as W
     w = W.config(args.workload)
+    if args.steps is None:
+        args.steps = w.nsteps
+    if args.warmup is None:
+        args.warmup = args.steps
     flops_tab = json.load(open(FLOPS_JSON))
     traffic_tab = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else None
     precs = [args.precision] if args.precision else list(w.precisions)
