@@ -412,323 +412,504 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
   return ext;
 }
 
-// One full step of one world. State arrays are in registers.
-template <class M, class T>
-__device__ __forceinline__ void step_world(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
-                                           const T* tgt, u64& rng, T* rows, int S, bool write_rows) {
+// ── per-world step, organised by body groups ────────────────────────────────
+// The host partitions the tree (Model::PMODE):
+//   0  one group owns every body: one lane per world, no exchange.
+//   1  fixed trunk: the trunk is the chain of fixed joints from the world; its
+//      transforms, velocities and accelerations are constants, so every group
+//      recomputes them (they fold away) and the subtrees below it are
+//      independent. One wave per subtree group, no exchange.
+//   2  floating trunk: group 0 owns the trunk (the bodies above the branch
+//      points); the other groups own subtrees. Every group recomputes the
+//      trunk's pass 1 from its own copy of the trunk state; subtree groups hand
+//      their articulated inertia and bias force contributions to group 0
+//      through LDS, group 0 finishes the trunk and hands back the branch-point
+//      accelerations and the new trunk state. Two workgroup barriers per step.
+// A workgroup is NG waves over the same 64 worlds; wave g runs group g's code.
+template <class M, class T> struct WS {
+  Xf<T> X[M::NB];
+  SV<T> vel[M::NB], cb[M::NB], pA[M::NB], acc[M::NB];
+  R3<T> Rw[M::NB];
+  V3<T> Pw[M::NB];
+  Sym<T> IA[M::NB];
+  T U[M::NB][M::MAXD][6];
+  T Lm[M::NB][M::MAXD][M::MAXD];
+  T Dinv[M::NB][M::MAXD];
+  T uu[M::NB][M::MAXD];
+  bool ok[M::NB];
+};
+
+template <class M, class T, int i>
+__device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v, T* rows, int S, bool write_rows,
+                                           bool do_contact) {
+  constexpr int jt = M::jtype[i];
+  constexpr int p = M::parent[i];
+  constexpr int qo = M::qoff[i], vo = M::voff[i];
+  const R3<T> Rp = R3<T>{{T(M::ptj_rot[i][0]), T(M::ptj_rot[i][1]), T(M::ptj_rot[i][2]), T(M::ptj_rot[i][3]),
+                          T(M::ptj_rot[i][4]), T(M::ptj_rot[i][5]), T(M::ptj_rot[i][6]), T(M::ptj_rot[i][7]),
+                          T(M::ptj_rot[i][8])}};
+  const V3<T> pp = v3(T(M::ptj_pos[i][0]), T(M::ptj_pos[i][1]), T(M::ptj_pos[i][2]));
+  Xf<T>& X = ws.X[i];
+  SV<T> vj = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  if constexpr (jt == J_REV) {
+    T s, c;
+    dsincos(-q[qo], &s, &c);
+    const T omc = T(1) - c;
+    R3<T> EJ;
+#pragma unroll
+    for (int k = 0; k < 9; k++) EJ.m[k] = T(k % 4 == 0 ? 1.0 : 0.0) + T(M::rev_k[i][k]) * s + T(M::rev_k2[i][k]) * omc;
+    X.E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+    X.r = pp;
+    vj.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+  } else if constexpr (jt == J_PRIS) {
+    X.E = Rp;
+    X.r = pp + tmul(Rp, v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * q[qo]);
+    vj.l = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+  } else if constexpr (jt == J_BALL || jt == J_FREE) {
+    R3<T> EJ = transpose(quat_mat(quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]))));
+    X.E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+    if constexpr (jt == J_FREE) {
+      X.r = pp + tmul(Rp, v3(q[qo + 3], q[qo + 4], q[qo + 5]));
+      vj.l = v3(v[vo + 3], v[vo + 4], v[vo + 5]);
+    } else {
+      X.r = pp;
+    }
+    vj.a = v3(v[vo], v[vo + 1], v[vo + 2]);
+  } else {
+    X.E = Rp;
+    X.r = pp;
+  }
+  if constexpr (p < 0) {
+    ws.vel[i] = vj;
+    ws.cb[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  } else {
+    ws.vel[i] = apply_motion(X, ws.vel[p]) + vj;
+    ws.cb[i] = cross_motion(ws.vel[i], vj);
+  }
+  ws.pA[i] = cross_force(ws.vel[i], sym_mul(rigid_inertia<M, T, i>(), ws.vel[i]));
+  if constexpr (M::need_world[i]) {
+    if constexpr (p < 0) {
+      ws.Rw[i] = transpose(X.E);
+      ws.Pw[i] = X.r;
+    } else {
+      ws.Rw[i] = mul_bt(ws.Rw[p], X.E);
+      ws.Pw[i] = ws.Pw[p] + mul(ws.Rw[p], X.r);
+    }
+  }
+  if constexpr (M::gtype[i] != G_NONE) {
+    if (do_contact) {
+      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], rows, S, write_rows);
+      ws.pA[i] = ws.pA[i] - f;
+    }
+  }
+}
+
+// Joint solve of body i (U, D = LDL^T, u) and its articulated inertia / bias
+// force as seen by the parent (I_a, p_a), from I_A and p_A. Returns false for
+// a body without DOFs (then Ia, pa are I_A, p_A unchanged).
+template <class M, class T, int i>
+__device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v, const T* ctrl, Sym<T>& Ia,
+                                           SV<T>& pa) {
+  constexpr int nd = ndof_of(M::jtype[i]);
+  constexpr int p = M::parent[i];
+  constexpr int vo = M::voff[i], qo = M::qoff[i];
+  constexpr int MAXD = M::MAXD;
+  ws.ok[i] = true;
+  Ia = ws.IA[i];
+  pa = ws.pA[i];
+  if constexpr (nd > 0) {
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      SV<T> uk = sym_mul(ws.IA[i], subspace<M, T, i>(k));
+      ws.U[i][k][0] = uk.a.x; ws.U[i][k][1] = uk.a.y; ws.U[i][k][2] = uk.a.z;
+      ws.U[i][k][3] = uk.l.x; ws.U[i][k][4] = uk.l.y; ws.U[i][k][5] = uk.l.z;
+      T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
+      if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
+      ws.uu[i][k] = tau - dot(subspace<M, T, i>(k), ws.pA[i]);
+    }
+    T D[MAXD][MAXD];
+#pragma unroll
+    for (int r = 0; r < nd; r++)
+#pragma unroll
+      for (int c = 0; c <= r; c++) {
+        SV<T> sr = subspace<M, T, i>(r);
+        SV<T> ucol = {v3(ws.U[i][c][0], ws.U[i][c][1], ws.U[i][c][2]), v3(ws.U[i][c][3], ws.U[i][c][4], ws.U[i][c][5])};
+        D[r][c] = dot(sr, ucol) + (r == c ? T(M::armature[i] + M::dt * M::damping[i]) : T(0));
+      }
+    // LDL^T with the pivots stored inverted (same singular test as aba.rs:210).
+    T E[MAXD][MAXD];
+#pragma unroll
+    for (int j = 0; j < nd; j++) {
+      T dj = D[j][j];
+#pragma unroll
+      for (int k = 0; k < j; k++) dj = dj - ws.Lm[i][j][k] * E[j][k];
+      ws.ok[i] = ws.ok[i] && !(dabs(dj) < T(1e-20));
+      ws.Dinv[i][j] = T(1) / dj;
+#pragma unroll
+      for (int r = j + 1; r < nd; r++) {
+        T e = D[r][j];
+#pragma unroll
+        for (int k = 0; k < j; k++) e = e - ws.Lm[i][r][k] * E[j][k];
+        E[r][j] = e;
+        ws.Lm[i][r][j] = e * ws.Dinv[i][j];
+      }
+    }
+    if constexpr (p >= 0) {
+      // W = U D^-1, one row of U at a time.
+      T W[MAXD][6];
+#pragma unroll
+      for (int r = 0; r < 6; r++) {
+        T y[MAXD];
+#pragma unroll
+        for (int k = 0; k < nd; k++) {
+          y[k] = ws.U[i][k][r];
+#pragma unroll
+          for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
+        }
+#pragma unroll
+        for (int k = 0; k < nd; k++) y[k] = y[k] * ws.Dinv[i][k];
+#pragma unroll
+        for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+          for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
+#pragma unroll
+        for (int k = 0; k < nd; k++) W[k][r] = y[k];
+      }
+#pragma unroll
+      for (int r = 0; r < 3; r++)
+#pragma unroll
+        for (int c = r; c < 3; c++) {
+          T s0 = W[0][r] * ws.U[i][0][c], s1 = W[0][3 + r] * ws.U[i][0][3 + c];
+#pragma unroll
+          for (int k = 1; k < nd; k++) { s0 = s0 + W[k][r] * ws.U[i][k][c]; s1 = s1 + W[k][3 + r] * ws.U[i][k][3 + c]; }
+          Ia.a[sx(r, c)] = Ia.a[sx(r, c)] - s0;
+          Ia.c[sx(r, c)] = Ia.c[sx(r, c)] - s1;
+        }
+#pragma unroll
+      for (int r = 0; r < 3; r++)
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+          T s0 = W[0][r] * ws.U[i][0][3 + c];
+#pragma unroll
+          for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * ws.U[i][k][3 + c];
+          Ia.b[r * 3 + c] = Ia.b[r * 3 + c] - s0;
+        }
+      SV<T> wu;
+#pragma unroll
+      for (int r = 0; r < 6; r++) {
+        T s0 = W[0][r] * ws.uu[i][0];
+#pragma unroll
+        for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * ws.uu[i][k];
+        sv_set(wu, r, s0);
+      }
+      pa = pa + sym_mul(Ia, ws.cb[i]) + wu;
+    }
+  }
+}
+
+template <class M, class T, int i> __device__ __forceinline__ void body_pass3(WS<M, T>& ws, T* qdd) {
+  constexpr int nd = ndof_of(M::jtype[i]);
+  constexpr int p = M::parent[i];
+  constexpr int vo = M::voff[i];
+  constexpr int MAXD = M::MAXD;
+  SV<T> ap;
+  if constexpr (p < 0) {
+    SV<T> a0 = {v3(T(0), T(0), T(0)), v3(T(-M::gravity[0]), T(-M::gravity[1]), T(-M::gravity[2]))};
+    ap = apply_motion(ws.X[i], a0) + ws.cb[i];
+  } else {
+    ap = apply_motion(ws.X[i], ws.acc[p]) + ws.cb[i];
+  }
+  if constexpr (nd > 0) {
+    T y[MAXD];
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      T uta = ws.U[i][k][0] * ap.a.x + ws.U[i][k][1] * ap.a.y + ws.U[i][k][2] * ap.a.z + ws.U[i][k][3] * ap.l.x +
+              ws.U[i][k][4] * ap.l.y + ws.U[i][k][5] * ap.l.z;
+      y[k] = ws.uu[i][k] - uta;
+#pragma unroll
+      for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
+    }
+#pragma unroll
+    for (int k = 0; k < nd; k++) y[k] = y[k] * ws.Dinv[i][k];
+#pragma unroll
+    for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+      for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      y[k] = ws.ok[i] ? y[k] : T(0);
+      qdd[vo + k] = y[k];
+      ap = ap + subspace<M, T, i>(k) * y[k];
+    }
+  }
+  ws.acc[i] = ap;
+}
+
+// Semi-implicit Euler for body i's joint (integrate.rs:41-92); v += dt qdd first.
+template <class M, class T, int i> __device__ __forceinline__ void body_integrate(T* q, T* v, const T* qdd) {
+  constexpr int jt = M::jtype[i];
+  constexpr int nd = ndof_of(jt);
+  constexpr int qo = M::qoff[i], vo = M::voff[i];
+  const T dt = T(M::dt);
+#pragma unroll
+  for (int k = 0; k < nd; k++) v[vo + k] = v[vo + k] + dt * qdd[vo + k];
+  if constexpr (jt == J_REV || jt == J_PRIS) {
+    q[qo] = q[qo] + dt * v[vo];
+  } else if constexpr (jt == J_BALL || jt == J_FREE) {
+    Q<T> cur = quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]));
+    if constexpr (jt == J_FREE) {
+      V3<T> wl = qrotate(cur, v3(v[vo + 3], v[vo + 4], v[vo + 5]));
+      q[qo + 3] = q[qo + 3] + dt * wl.x;
+      q[qo + 4] = q[qo + 4] + dt * wl.y;
+      q[qo + 5] = q[qo + 5] + dt * wl.z;
+    }
+    Q<T> nx = qmul(cur, quat_exp(v3(v[vo], v[vo + 1], v[vo + 2]) * dt));
+    T n = dsqrt(nx.w * nx.w + nx.x * nx.x + nx.y * nx.y + nx.z * nx.z);
+    nx = Q<T>{nx.w / n, nx.x / n, nx.y / n, nx.z / n};
+    V3<T> lg = quat_log(nx);
+    q[qo] = lg.x;
+    q[qo + 1] = lg.y;
+    q[qo + 2] = lg.z;
+  }
+}
+
+// Articulated inertia / bias force of body i propagated to its parent:
+// I_A[p] += X^T I_a X, p_A[p] += X^T p_a.
+template <class M, class T, int i>
+__device__ __forceinline__ void propagate(WS<M, T>& ws, const Sym<T>& Ia, const SV<T>& pa, Sym<T>& dI, SV<T>& dp) {
+  dI = sym_xtix(Ia, ws.X[i]);
+  dp = inv_apply_force(ws.X[i], pa);
+}
+
+// LDS exchange slots (floating trunk): slot s holds 64 lanes of T.
+template <class T> __device__ __forceinline__ void lds_put(T* lds, int slot, int lane, T x) { lds[slot * 64 + lane] = x; }
+template <class T> __device__ __forceinline__ T lds_get(const T* lds, int slot, int lane) { return lds[slot * 64 + lane]; }
+template <class T> __device__ __forceinline__ void put_sym(T* lds, int s, int lane, const Sym<T>& I, const SV<T>& p) {
+#pragma unroll
+  for (int k = 0; k < 6; k++) { lds_put(lds, s + k, lane, I.a[k]); lds_put(lds, s + 6 + k, lane, I.c[k]); }
+#pragma unroll
+  for (int k = 0; k < 9; k++) lds_put(lds, s + 12 + k, lane, I.b[k]);
+  lds_put(lds, s + 21, lane, p.a.x); lds_put(lds, s + 22, lane, p.a.y); lds_put(lds, s + 23, lane, p.a.z);
+  lds_put(lds, s + 24, lane, p.l.x); lds_put(lds, s + 25, lane, p.l.y); lds_put(lds, s + 26, lane, p.l.z);
+}
+template <class T> __device__ __forceinline__ void add_sym(const T* lds, int s, int lane, Sym<T>& I, SV<T>& p) {
+#pragma unroll
+  for (int k = 0; k < 6; k++) { I.a[k] = I.a[k] + lds_get(lds, s + k, lane); I.c[k] = I.c[k] + lds_get(lds, s + 6 + k, lane); }
+#pragma unroll
+  for (int k = 0; k < 9; k++) I.b[k] = I.b[k] + lds_get(lds, s + 12 + k, lane);
+  p.a = p.a + v3(lds_get(lds, s + 21, lane), lds_get(lds, s + 22, lane), lds_get(lds, s + 23, lane));
+  p.l = p.l + v3(lds_get(lds, s + 24, lane), lds_get(lds, s + 25, lane), lds_get(lds, s + 26, lane));
+}
+
+// One step of group G for one world (lane). State arrays are in registers; a
+// group reads and writes only the DOFs of its own bodies (plus the trunk's).
+template <class M, class T, int G>
+__device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+                                           const T* tgt, u64& rng, T* rows, int S, bool write_rows, T* lds, int lane) {
   constexpr int NB = M::NB;
-  // ── control noise (one draw per listed DOF, list order) ──
+  constexpr int NL = M::glen[G];
+  constexpr int NT = M::NTRUNK;
+  constexpr bool FLOAT = M::PMODE == 2;
+  // ── control noise: every group advances the whole stream; values only for its DOFs ──
   if constexpr (M::NNOISE > 0) {
     if constexpr (M::noise_dist == 1) {
       sfor<0, M::NNOISE>([&](auto K) {
         constexpr int k = decltype(K)::value;
         T u = uniform01(rng, T(0));
-        ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b - M::noise_a) * u;
+        if constexpr (M::dof_owner[M::noise_dof[k]] == G)
+          ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b - M::noise_a) * u;
       });
     } else {
       sfor<0, (M::NNOISE + 1) / 2>([&](auto K) {
         constexpr int k = 2 * decltype(K)::value;
+        constexpr bool mine0 = M::dof_owner[M::noise_dof[k]] == G;
+        constexpr bool mine1 = k + 1 < M::NNOISE && M::dof_owner[M::noise_dof[k + 1 < M::NNOISE ? k + 1 : k]] == G;
         T u1 = uniform01(rng, T(0));
         T u2 = uniform01(rng, T(0));
-        T r = dsqrt(T(-2) * dlog(T(1) - u1));
-        T sn, cs;
-        dsincos(T(6.283185307179586) * u2, &sn, &cs);
-        ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
-        if constexpr (k + 1 < M::NNOISE) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
+        if constexpr (mine0 || mine1) {
+          T r = dsqrt(T(-2) * dlog(T(1) - u1));
+          T sn, cs;
+          dsincos(T(6.283185307179586) * u2, &sn, &cs);
+          if constexpr (mine0) ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
+          if constexpr (mine1) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
+        }
       });
     }
   }
   // ── PD servo (crates/phyz-gpu/cuda/phyz_kernels.cu:464-483) ──
   sfor<0, M::NPD>([&](auto K) {
     constexpr int d = decltype(K)::value;
-    T tau = T(M::pd_kp[d]) * (tgt[d] - q[M::pd_q[d]]) - T(M::pd_kd[d]) * v[M::pd_v[d]];
-    ctrl[M::pd_v[d]] = dmin(dmax(tau, T(-M::pd_max[d])), T(M::pd_max[d]));
+    if constexpr (M::dof_owner[M::pd_v[d]] == G) {
+      T tau = T(M::pd_kp[d]) * (tgt[d] - q[M::pd_q[d]]) - T(M::pd_kd[d]) * v[M::pd_v[d]];
+      ctrl[M::pd_v[d]] = dmin(dmax(tau, T(-M::pd_max[d])), T(M::pd_max[d]));
+    }
   });
 
-  Xf<T> X[NB];
-  SV<T> vel[NB], cb[NB], pA[NB];
-  R3<T> Rw[NB];
-  V3<T> Pw[NB];
-  // ── pass 1: transforms, velocities, bias forces, contact ──
-  sfor<0, NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    constexpr int jt = M::jtype[i];
+  WS<M, T> ws;
+  // ── pass 1: trunk (every group), then own bodies ──
+  sfor<0, NT>([&](auto K) {
+    constexpr int i = M::tlist[decltype(K)::value];
+    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, G == 0);
+  });
+  sfor<0, NL>([&](auto K) {
+    constexpr int i = M::glist[G][decltype(K)::value];
+    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, true);
+  });
+  // ── pass 2: own bodies, leaves first ──
+  sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; ws.IA[i] = rigid_inertia<M, T, i>(); });
+  rfor<NL>([&](auto K) {
+    constexpr int i = M::glist[G][decltype(K)::value];
     constexpr int p = M::parent[i];
-    constexpr int qo = M::qoff[i], vo = M::voff[i];
-    const R3<T> Rp = R3<T>{{T(M::ptj_rot[i][0]), T(M::ptj_rot[i][1]), T(M::ptj_rot[i][2]), T(M::ptj_rot[i][3]),
-                            T(M::ptj_rot[i][4]), T(M::ptj_rot[i][5]), T(M::ptj_rot[i][6]), T(M::ptj_rot[i][7]),
-                            T(M::ptj_rot[i][8])}};
-    const V3<T> pp = v3(T(M::ptj_pos[i][0]), T(M::ptj_pos[i][1]), T(M::ptj_pos[i][2]));
-    SV<T> vj = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
-    if constexpr (jt == J_REV) {
-      T s, c;
-      dsincos(-q[qo], &s, &c);
-      const T omc = T(1) - c;
-      R3<T> EJ;
-#pragma unroll
-      for (int k = 0; k < 9; k++) EJ.m[k] = T(k % 4 == 0 ? 1.0 : 0.0) + T(M::rev_k[i][k]) * s + T(M::rev_k2[i][k]) * omc;
-      X[i].E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
-      X[i].r = pp;
-      vj.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
-    } else if constexpr (jt == J_PRIS) {
-      X[i].E = Rp;
-      X[i].r = pp + tmul(Rp, v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * q[qo]);
-      vj.l = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
-    } else if constexpr (jt == J_BALL || jt == J_FREE) {
-      R3<T> EJ = transpose(quat_mat(quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]))));
-      X[i].E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
-      if constexpr (jt == J_FREE) {
-        X[i].r = pp + tmul(Rp, v3(q[qo + 3], q[qo + 4], q[qo + 5]));
-        vj.l = v3(v[vo + 3], v[vo + 4], v[vo + 5]);
+    Sym<T> Ia;
+    SV<T> pa;
+    body_solve<M, T, i>(ws, q, v, ctrl, Ia, pa);
+    if constexpr (p >= 0) {
+      if constexpr (M::is_trunk[p] && M::PMODE == 1) {
+        // A fixed trunk absorbs the subtree: nothing above it moves.
+      } else if constexpr (M::is_trunk[p] && FLOAT && G != 0) {
+        Sym<T> dI;
+        SV<T> dp;
+        propagate<M, T, i>(ws, Ia, pa, dI, dp);
+        if (!ws.ok[i]) { dI = Sym<T>{}; dp = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))}; }
+        put_sym(lds, M::slot_contrib[i], lane, dI, dp);
       } else {
-        X[i].r = pp;
+        if (ws.ok[i]) {
+          Sym<T> dI;
+          SV<T> dp;
+          propagate<M, T, i>(ws, Ia, pa, dI, dp);
+          sym_add(ws.IA[p], dI);
+          ws.pA[p] = ws.pA[p] + dp;
+        }
       }
-      vj.a = v3(v[vo], v[vo + 1], v[vo + 2]);
-    } else {
-      X[i].E = Rp;
-      X[i].r = pp;
-    }
-    if constexpr (p < 0) {
-      vel[i] = vj;
-      cb[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
-    } else {
-      vel[i] = apply_motion(X[i], vel[p]) + vj;
-      cb[i] = cross_motion(vel[i], vj);
-    }
-    pA[i] = cross_force(vel[i], sym_mul(rigid_inertia<M, T, i>(), vel[i]));
-    if constexpr (M::need_world[i]) {
-      if constexpr (p < 0) {
-        Rw[i] = transpose(X[i].E);
-        Pw[i] = X[i].r;
-      } else {
-        Rw[i] = mul_bt(Rw[p], X[i].E);
-        Pw[i] = Pw[p] + mul(Rw[p], X[i].r);
-      }
-    }
-    if constexpr (M::gtype[i] != G_NONE) {
-      SV<T> f = contact_body<M, T, i>(Rw[i], Pw[i], vel[i], rows, S, write_rows);
-      pA[i] = pA[i] - f;
     }
   });
-
-  // ── pass 2: articulated inertias, leaves to root ──
-  Sym<T> IA[NB];
-  sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; IA[i] = rigid_inertia<M, T, i>(); });
-  constexpr int MAXD = M::MAXNDOF > 0 ? M::MAXNDOF : 1;
-  T U[NB][MAXD][6];
-  T Lm[NB][MAXD][MAXD];
-  T Dinv[NB][MAXD];
-  T uu[NB][MAXD];
-  bool ok[NB];
-  rfor<NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    constexpr int jt = M::jtype[i];
-    constexpr int nd = ndof_of(jt);
-    constexpr int p = M::parent[i];
-    constexpr int vo = M::voff[i], qo = M::qoff[i];
-    ok[i] = true;
-    Sym<T> Ia = IA[i];
-    SV<T> pa = pA[i];
-    if constexpr (nd > 0) {
-#pragma unroll
-      for (int k = 0; k < nd; k++) {
-        SV<T> uk = sym_mul(IA[i], subspace<M, T, i>(k));
-        U[i][k][0] = uk.a.x; U[i][k][1] = uk.a.y; U[i][k][2] = uk.a.z;
-        U[i][k][3] = uk.l.x; U[i][k][4] = uk.l.y; U[i][k][5] = uk.l.z;
-        T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
-        if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
-        uu[i][k] = tau - dot(subspace<M, T, i>(k), pA[i]);
-      }
-      T D[MAXD][MAXD];
-#pragma unroll
-      for (int r = 0; r < nd; r++)
-#pragma unroll
-        for (int c = 0; c <= r; c++) {
-          SV<T> sr = subspace<M, T, i>(r);
-          SV<T> ucol = {v3(U[i][c][0], U[i][c][1], U[i][c][2]), v3(U[i][c][3], U[i][c][4], U[i][c][5])};
-          D[r][c] = dot(sr, ucol) + (r == c ? T(M::armature[i] + M::dt * M::damping[i]) : T(0));
-        }
-      // LDL^T with the pivots stored inverted (same singular test as aba.rs:210).
-      T E[MAXD][MAXD];
-#pragma unroll
-      for (int j = 0; j < nd; j++) {
-        T dj = D[j][j];
-#pragma unroll
-        for (int k = 0; k < j; k++) dj = dj - Lm[i][j][k] * E[j][k];
-        ok[i] = ok[i] && !(dabs(dj) < T(1e-20));
-        Dinv[i][j] = T(1) / dj;
-#pragma unroll
-        for (int r = j + 1; r < nd; r++) {
-          T e = D[r][j];
-#pragma unroll
-          for (int k = 0; k < j; k++) e = e - Lm[i][r][k] * E[j][k];
-          E[r][j] = e;
-          Lm[i][r][j] = e * Dinv[i][j];
-        }
-      }
-      if constexpr (p >= 0) {
-        // W = U D^-1, one row of U at a time.
-        T W[MAXD][6];
-#pragma unroll
-        for (int r = 0; r < 6; r++) {
-          T y[MAXD];
-#pragma unroll
-          for (int k = 0; k < nd; k++) {
-            y[k] = U[i][k][r];
-#pragma unroll
-            for (int t = 0; t < k; t++) y[k] = y[k] - Lm[i][k][t] * y[t];
+  if constexpr (FLOAT) {
+    __syncthreads();
+    if constexpr (G == 0) {
+      // Contributions of the other groups' subtrees, in body order.
+      sfor<0, NB>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (M::slot_contrib[i] >= 0) add_sym(lds, M::slot_contrib[i], lane, ws.IA[M::parent[i]], ws.pA[M::parent[i]]);
+      });
+      rfor<NT>([&](auto K) {
+        constexpr int i = M::tlist[decltype(K)::value];
+        constexpr int p = M::parent[i];
+        Sym<T> Ia;
+        SV<T> pa;
+        body_solve<M, T, i>(ws, q, v, ctrl, Ia, pa);
+        if constexpr (p >= 0) {
+          if (ws.ok[i]) {
+            Sym<T> dI;
+            SV<T> dp;
+            propagate<M, T, i>(ws, Ia, pa, dI, dp);
+            sym_add(ws.IA[p], dI);
+            ws.pA[p] = ws.pA[p] + dp;
           }
-#pragma unroll
-          for (int k = 0; k < nd; k++) y[k] = y[k] * Dinv[i][k];
-#pragma unroll
-          for (int k = nd - 1; k >= 0; k--)
-#pragma unroll
-            for (int t = k + 1; t < nd; t++) y[k] = y[k] - Lm[i][t][k] * y[t];
-#pragma unroll
-          for (int k = 0; k < nd; k++) W[k][r] = y[k];
         }
-#pragma unroll
-        for (int r = 0; r < 3; r++)
-#pragma unroll
-          for (int c = r; c < 3; c++) {
-            T s0 = W[0][r] * U[i][0][c], s1 = W[0][3 + r] * U[i][0][3 + c];
-#pragma unroll
-            for (int k = 1; k < nd; k++) { s0 = s0 + W[k][r] * U[i][k][c]; s1 = s1 + W[k][3 + r] * U[i][k][3 + c]; }
-            Ia.a[sx(r, c)] = Ia.a[sx(r, c)] - s0;
-            Ia.c[sx(r, c)] = Ia.c[sx(r, c)] - s1;
-          }
-#pragma unroll
-        for (int r = 0; r < 3; r++)
-#pragma unroll
-          for (int c = 0; c < 3; c++) {
-            T s0 = W[0][r] * U[i][0][3 + c];
-#pragma unroll
-            for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * U[i][k][3 + c];
-            Ia.b[r * 3 + c] = Ia.b[r * 3 + c] - s0;
-          }
-        SV<T> wu;
-#pragma unroll
-        for (int r = 0; r < 6; r++) {
-          T s0 = W[0][r] * uu[i][0];
-#pragma unroll
-          for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * uu[i][k];
-          sv_set(wu, r, s0);
+      });
+      // Trunk accelerations, then the trunk's new state, for the other groups.
+      sfor<0, NT>([&](auto K) {
+        constexpr int i = M::tlist[decltype(K)::value];
+        body_pass3<M, T, i>(ws, qdd);
+        if constexpr (M::slot_acc[i] >= 0) {
+          const int s = M::slot_acc[i];
+          lds_put(lds, s, lane, ws.acc[i].a.x); lds_put(lds, s + 1, lane, ws.acc[i].a.y); lds_put(lds, s + 2, lane, ws.acc[i].a.z);
+          lds_put(lds, s + 3, lane, ws.acc[i].l.x); lds_put(lds, s + 4, lane, ws.acc[i].l.y); lds_put(lds, s + 5, lane, ws.acc[i].l.z);
         }
-        pa = pa + sym_mul(Ia, cb[i]) + wu;
-        if (ok[i]) {
-          sym_add(IA[p], sym_xtix(Ia, X[i]));
-          pA[p] = pA[p] + inv_apply_force(X[i], pa);
+        body_integrate<M, T, i>(q, v, qdd);
+      });
+      sfor<0, M::NQ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (M::dof_group[j] == -1) {
+          lds_put(lds, M::slot_state + 2 * M::tdof[j], lane, q[j]);
+          lds_put(lds, M::slot_state + 2 * M::tdof[j] + 1, lane, v[j]);
         }
-      }
-    } else if constexpr (p >= 0) {
-      sym_add(IA[p], sym_xtix(Ia, X[i]));
-      pA[p] = pA[p] + inv_apply_force(X[i], pa);
+      });
     }
-  });
-
-  // ── pass 3: accelerations, root to leaves ──
-  SV<T> acc[NB];
-  sfor<0, NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    constexpr int jt = M::jtype[i];
-    constexpr int nd = ndof_of(jt);
-    constexpr int p = M::parent[i];
-    constexpr int vo = M::voff[i];
-    SV<T> ap;
-    if constexpr (p < 0) {
-      SV<T> a0 = {v3(T(0), T(0), T(0)), v3(T(-M::gravity[0]), T(-M::gravity[1]), T(-M::gravity[2]))};
-      ap = apply_motion(X[i], a0) + cb[i];
-    } else {
-      ap = apply_motion(X[i], acc[p]) + cb[i];
+    __syncthreads();
+    if constexpr (G != 0) {
+      sfor<0, NT>([&](auto K) {
+        constexpr int i = M::tlist[decltype(K)::value];
+        if constexpr (M::slot_acc[i] >= 0) {
+          const int s = M::slot_acc[i];
+          ws.acc[i] = SV<T>{v3(lds_get(lds, s, lane), lds_get(lds, s + 1, lane), lds_get(lds, s + 2, lane)),
+                            v3(lds_get(lds, s + 3, lane), lds_get(lds, s + 4, lane), lds_get(lds, s + 5, lane))};
+        }
+      });
+      sfor<0, M::NQ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (M::dof_group[j] == -1) {
+          q[j] = lds_get(lds, M::slot_state + 2 * M::tdof[j], lane);
+          v[j] = lds_get(lds, M::slot_state + 2 * M::tdof[j] + 1, lane);
+        }
+      });
     }
-    if constexpr (nd > 0) {
-      T y[MAXD];
-#pragma unroll
-      for (int k = 0; k < nd; k++) {
-        T uta = U[i][k][0] * ap.a.x + U[i][k][1] * ap.a.y + U[i][k][2] * ap.a.z + U[i][k][3] * ap.l.x +
-                U[i][k][4] * ap.l.y + U[i][k][5] * ap.l.z;
-        y[k] = uu[i][k] - uta;
-#pragma unroll
-        for (int t = 0; t < k; t++) y[k] = y[k] - Lm[i][k][t] * y[t];
-      }
-#pragma unroll
-      for (int k = 0; k < nd; k++) y[k] = y[k] * Dinv[i][k];
-#pragma unroll
-      for (int k = nd - 1; k >= 0; k--)
-#pragma unroll
-        for (int t = k + 1; t < nd; t++) y[k] = y[k] - Lm[i][t][k] * y[t];
-#pragma unroll
-      for (int k = 0; k < nd; k++) {
-        y[k] = ok[i] ? y[k] : T(0);
-        qdd[vo + k] = y[k];
-        ap = ap + subspace<M, T, i>(k) * y[k];
-      }
-    }
-    acc[i] = ap;
-  });
-
-  // ── semi-implicit Euler (crates/phyz-rigid/src/integrate.rs:83-92) ──
-  const T dt = T(M::dt);
-#pragma unroll
-  for (int j = 0; j < M::NV; j++) v[j] = v[j] + dt * qdd[j];
-  sfor<0, NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    constexpr int jt = M::jtype[i];
-    constexpr int qo = M::qoff[i], vo = M::voff[i];
-    if constexpr (jt == J_REV || jt == J_PRIS) {
-      q[qo] = q[qo] + dt * v[vo];
-    } else if constexpr (jt == J_BALL || jt == J_FREE) {
-      Q<T> cur = quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]));
-      if constexpr (jt == J_FREE) {
-        V3<T> wl = qrotate(cur, v3(v[vo + 3], v[vo + 4], v[vo + 5]));
-        q[qo + 3] = q[qo + 3] + dt * wl.x;
-        q[qo + 4] = q[qo + 4] + dt * wl.y;
-        q[qo + 5] = q[qo + 5] + dt * wl.z;
-      }
-      Q<T> nx = qmul(cur, quat_exp(v3(v[vo], v[vo + 1], v[vo + 2]) * dt));
-      T n = dsqrt(nx.w * nx.w + nx.x * nx.x + nx.y * nx.y + nx.z * nx.z);
-      nx = Q<T>{nx.w / n, nx.x / n, nx.y / n, nx.z / n};
-      V3<T> lg = quat_log(nx);
-      q[qo] = lg.x;
-      q[qo + 1] = lg.y;
-      q[qo + 2] = lg.z;
-    }
+  } else {
+    // Trunk accelerations (constants for a fixed trunk; the whole tree otherwise empty).
+    sfor<0, NT>([&](auto K) {
+      constexpr int i = M::tlist[decltype(K)::value];
+      body_pass3<M, T, i>(ws, qdd);
+    });
+  }
+  // ── pass 3 and integration: own bodies ──
+  sfor<0, NL>([&](auto K) {
+    constexpr int i = M::glist[G][decltype(K)::value];
+    body_pass3<M, T, i>(ws, qdd);
+    body_integrate<M, T, i>(q, v, qdd);
   });
 }
 
-// Kernel body: load the world's state, run nsteps, store.
-template <class M, class T> __device__ __forceinline__ void run(const StepArgs& a) {
-  const int w = blockIdx.x * blockDim.x + threadIdx.x;
-  if (w >= a.nworld) return;
+// Kernel body for group G: load the world's state, run nsteps, store. A group
+// loads the DOFs it owns and the trunk's; it stores only the DOFs it owns
+// (group 0 also stores the trunk's and the RNG state).
+template <class M, class T, int G> __device__ __forceinline__ void run_group(const StepArgs& a, int lane, T* lds) {
+  const int w = blockIdx.x * 64 + lane;
+  const bool live = w < a.nworld;
+  if constexpr (M::PMODE != 2) {
+    if (!live) return;
+  }
+  const int wl = live ? w : a.nworld - 1;  // out-of-range lanes shadow the last world (no stores)
   const int S = a.stride;
   T* gq = (T*)a.q;
   T* gv = (T*)a.v;
   T* gc = (T*)a.ctrl;
   T q[M::NQ], v[M::NV], ctrl[M::NV], qdd[M::NV];
-#pragma unroll
-  for (int j = 0; j < M::NQ; j++) q[j] = gq[j * S + w];
-#pragma unroll
-  for (int j = 0; j < M::NV; j++) { v[j] = gv[j * S + w]; ctrl[j] = gc[j * S + w]; qdd[j] = T(0); }
+  sfor<0, M::NQ>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    if constexpr (M::dof_group[j] == G || M::dof_group[j] == -1) {
+      q[j] = gq[j * S + wl];
+      v[j] = gv[j * S + wl];
+      ctrl[j] = gc[j * S + wl];
+    } else {
+      q[j] = T(0); v[j] = T(0); ctrl[j] = T(0);
+    }
+    qdd[j] = T(0);
+  });
   T tgt[M::NPD > 0 ? M::NPD : 1];
-#pragma unroll
-  for (int d = 0; d < M::NPD; d++) tgt[d] = ((const T*)a.targets)[d * S + w];
+  sfor<0, M::NPD>([&](auto K) {
+    constexpr int d = decltype(K)::value;
+    if constexpr (M::dof_owner[M::pd_v[d]] == G) tgt[d] = ((const T*)a.targets)[d * S + wl];
+    else tgt[d] = T(0);
+  });
   u64 rng = 0;
-  if constexpr (M::NNOISE > 0) rng = a.rng[w];
-  T* rows = M::HAS_CONTACT ? (T*)a.contact_rows + w : nullptr;
+  if constexpr (M::NNOISE > 0) rng = a.rng[wl];
+  T* rows = M::HAS_CONTACT ? (T*)a.contact_rows + wl : nullptr;
   const int n = a.nsteps;
   for (int s = 0; s < n; s++) {
-    const bool last = (s == n - 1) && a.write_contacts;
-    step_world<M, T>(q, v, ctrl, qdd, tgt, rng, rows, S, last);
+    const bool last = (s == n - 1) && a.write_contacts && live;
+    step_group<M, T, G>(q, v, ctrl, qdd, tgt, rng, rows, S, last, lds, lane);
   }
-#pragma unroll
-  for (int j = 0; j < M::NQ; j++) gq[j * S + w] = q[j];
-#pragma unroll
-  for (int j = 0; j < M::NV; j++) {
-    gv[j * S + w] = v[j];
-    gc[j * S + w] = ctrl[j];
-    ((T*)a.qdd)[j * S + w] = qdd[j];
-  }
-  if constexpr (M::NNOISE > 0) a.rng[w] = rng;
+  if (!live) return;
+  sfor<0, M::NQ>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    if constexpr (M::dof_group[j] == G || (G == 0 && M::dof_group[j] == -1)) {
+      gq[j * S + w] = q[j];
+      gv[j * S + w] = v[j];
+      gc[j * S + w] = ctrl[j];
+      ((T*)a.qdd)[j * S + w] = qdd[j];
+    }
+  });
+  if constexpr (M::NNOISE > 0 && G == 0) a.rng[w] = rng;
 }
 
 }  // namespace phz

@@ -14,6 +14,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -173,6 +174,88 @@ template <class F> std::string arr2(int n, int m, F f) {
   return s + "}";
 }
 
+// How the step kernel splits a world's bodies over the waves of a workgroup
+// (see the PMODE comment in phz_device.h).
+struct Plan {
+  int mode = 0;
+  std::vector<int> trunk;                // topological order
+  std::vector<std::vector<int>> groups;  // bodies owned by each wave, topological order
+};
+
+Plan plan_partition(const ModelD& m) {
+  const int nb = m.nb;
+  Plan pl;
+  std::vector<int> all(nb);
+  for (int i = 0; i < nb; i++) all[i] = i;
+  const char* env = std::getenv("PHZ_PARTITION");
+  const std::string want = env ? env : "auto";
+  auto lane_per_world = [&]() { pl = Plan{}; pl.groups.push_back(all); return pl; };
+  if (want == "0") return lane_per_world();
+  std::vector<std::vector<int>> kids(nb);
+  for (int i = 0; i < nb; i++) if (m.b[i].parent >= 0) kids[m.b[i].parent].push_back(i);
+  std::vector<int> size(nb, 1);
+  for (int i = nb - 1; i >= 0; i--) if (m.b[i].parent >= 0) size[m.b[i].parent] += size[i];
+  std::vector<char> trunk(nb, 0);
+  // Fixed trunk: the bodies welded to the world through fixed joints.
+  bool any_fixed = false;
+  for (int i = 0; i < nb; i++) {
+    const BodyD& b = m.b[i];
+    trunk[i] = b.jtype == 2 && (b.parent < 0 || trunk[b.parent]);
+    any_fixed = any_fixed || trunk[i];
+  }
+  int mode = 1;
+  if (!any_fixed) {
+    // Floating trunk: every body on a path from a root to a branch point
+    // (a body with two or more children whose subtrees hold two or more bodies).
+    mode = 2;
+    for (int i = 0; i < nb; i++) {
+      int heavy = 0;
+      for (int c : kids[i]) heavy += size[c] >= 2;
+      if (heavy >= 2)
+        for (int j = i; j >= 0; j = m.b[j].parent) trunk[j] = 1;
+    }
+  }
+  std::vector<std::vector<int>> parts;
+  for (int i = 0; i < nb; i++) {
+    if (trunk[i] || m.b[i].parent < 0 || !trunk[m.b[i].parent]) continue;
+    std::vector<int> part;
+    for (int j = i; j < nb; j++) {
+      int a = j;
+      while (a >= 0 && a != i && !trunk[a]) a = m.b[a].parent;
+      if (a == i) part.push_back(j);
+    }
+    parts.push_back(part);
+  }
+  for (int i = 0; i < nb; i++)  // floating roots outside any trunk (several independent trees)
+    if (!trunk[i] && m.b[i].parent < 0) {
+      std::vector<int> part;
+      for (int j = i; j < nb; j++) {
+        int a = j;
+        while (a >= 0 && a != i) a = m.b[a].parent;
+        if (a == i) part.push_back(j);
+      }
+      parts.push_back(part);
+    }
+  const bool forced = want == "1" || want == "2";
+  if (parts.size() < 2) return lane_per_world();
+  if (mode == 2 && !forced && nb < 14) return lane_per_world();
+  // At most 8 waves: merge the two smallest parts while there are more.
+  while (parts.size() > 8) {
+    std::sort(parts.begin(), parts.end(), [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); });
+    parts[1].insert(parts[1].end(), parts[0].begin(), parts[0].end());
+    parts.erase(parts.begin());
+  }
+  // Group 0 carries the trunk (floating trunk), so it takes the smallest part.
+  std::stable_sort(parts.begin(), parts.end(), [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); });
+  pl.mode = mode;
+  for (int i = 0; i < nb; i++) if (trunk[i]) pl.trunk.push_back(i);
+  for (auto& p : parts) {
+    std::sort(p.begin(), p.end());
+    pl.groups.push_back(p);
+  }
+  return pl;
+}
+
 std::string gen_model(const ModelD& m, const Features& f) {
   const int nb = m.nb;
   // Rigid spatial inertia [[Ic + m cx cx^T, m cx], [m cx^T, m 1]] as symmetric blocks.
@@ -224,10 +307,58 @@ std::string gen_model(const ModelD& m, const Features& f) {
       if ((int)f.geom[i * kGeomStride] != 0)
         for (int j = i; j >= 0; j = m.b[j].parent) need_world[j] = 1;
 
+  const Plan pl = plan_partition(m);
+  const int ng = (int)pl.groups.size();
+  int maxg = 1;
+  for (auto& g : pl.groups) maxg = std::max(maxg, (int)g.size());
+  std::vector<int> is_trunk(nb, 0), owner(nb, 0);
+  for (int i : pl.trunk) is_trunk[i] = 1;
+  for (int g = 0; g < ng; g++) for (int i : pl.groups[g]) owner[i] = g;
+  std::vector<int> dof_group(m.nv, 0), dof_owner(m.nv, 0), tdof(m.nv, -1);
+  int ntd = 0;
+  for (int i = 0; i < nb; i++)
+    for (int k = 0; k < ndof_of(m.b[i].jtype); k++) {
+      const int j = m.b[i].voff + k;
+      dof_group[j] = is_trunk[i] ? -1 : owner[i];
+      dof_owner[j] = is_trunk[i] ? 0 : owner[i];
+      if (is_trunk[i]) tdof[j] = ntd++;
+    }
+  // LDS slots (floating trunk): 27 per subtree root handed to group 0, 6 per
+  // trunk body whose acceleration other groups read, 2 per trunk DOF.
+  std::vector<int> slot_contrib(nb, -1), slot_acc(nb, -1);
+  int nslot = 0;
+  if (pl.mode == 2) {
+    for (int i = 0; i < nb; i++)
+      if (!is_trunk[i] && m.b[i].parent >= 0 && is_trunk[m.b[i].parent] && owner[i] != 0) {
+        slot_contrib[i] = nslot;
+        nslot += 27;
+        if (slot_acc[m.b[i].parent] < 0) { slot_acc[m.b[i].parent] = -2; }
+      }
+    for (int i = 0; i < nb; i++) if (slot_acc[i] == -2) { slot_acc[i] = nslot; nslot += 6; }
+  }
+  const int slot_state = nslot;
+  if (pl.mode == 2) nslot += 2 * ntd;
+
   std::ostringstream o;
   const int npd = f.npd, nn = f.noise ? (int)f.noise_dofs.size() : 0;
   o << "struct Model {\n";
-  o << "  static constexpr int NB = " << nb << ", NQ = " << m.nq << ", NV = " << m.nv << ", MAXNDOF = " << maxnd
+  o << "  static constexpr int NB = " << nb << ", NQ = " << m.nq << ", NV = " << m.nv
+    << ", MAXD = " << std::max(maxnd, 1) << ";\n";
+  o << "  static constexpr int PMODE = " << pl.mode << ", NG = " << ng << ", NTRUNK = " << pl.trunk.size()
+    << ", MAXG = " << maxg << ", NSLOT = " << nslot << ", slot_state = " << slot_state << ";\n";
+  const int nta = std::max((int)pl.trunk.size(), 1);
+  o << "  static constexpr int tlist[" << nta << "] = "
+    << arr1(nta, [&](int k) { return std::to_string(pl.trunk.empty() ? 0 : pl.trunk[k]); }) << ";\n";
+  o << "  static constexpr int glen[" << ng << "] = " << arr1(ng, [&](int g) { return std::to_string(pl.groups[g].size()); })
+    << ";\n";
+  o << "  static constexpr int glist[" << ng << "][" << maxg << "] = "
+    << arr2(ng, maxg, [&](int g, int k) { return std::to_string(k < (int)pl.groups[g].size() ? pl.groups[g][k] : 0); })
+    << ";\n";
+  o << "  static constexpr int dof_group[" << m.nv << "] = " << arr1(m.nv, [&](int j) { return std::to_string(dof_group[j]); })
+    << ";\n";
+  o << "  static constexpr int dof_owner[" << m.nv << "] = " << arr1(m.nv, [&](int j) { return std::to_string(dof_owner[j]); })
+    << ";\n";
+  o << "  static constexpr int tdof[" << m.nv << "] = " << arr1(m.nv, [&](int j) { return std::to_string(tdof[j]); })
     << ";\n";
   o << "  static constexpr bool HAS_CONTACT = " << (f.contact ? "true" : "false") << ";\n";
   o << "  static constexpr int NPD = " << npd << ", NNOISE = " << nn << ", noise_dist = " << f.dist << ";\n";
@@ -250,6 +381,9 @@ std::string gen_model(const ModelD& m, const Features& f) {
       << arr2(nb, w, [&](int i, int k) { return num(get(i, k)); }) << ";\n";
   };
   ib("parent", [&](int i) { return m.b[i].parent; });
+  bb("is_trunk", [&](int i) { return is_trunk[i]; });
+  ib("slot_contrib", [&](int i) { return slot_contrib[i]; });
+  ib("slot_acc", [&](int i) { return slot_acc[i]; });
   ib("jtype", [&](int i) { return m.b[i].jtype; });
   ib("qoff", [&](int i) { return m.b[i].qoff; });
   ib("voff", [&](int i) { return m.b[i].voff; });
@@ -290,12 +424,22 @@ std::string gen_model(const ModelD& m, const Features& f) {
   return o.str();
 }
 
-std::string gen_source(const ModelD& m, const Features& f, bool f64, int block) {
+// One workgroup = NG waves over the same 64 worlds; wave g runs group g.
+std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups) {
+  const int ng = (int)plan_partition(m).groups.size();
+  *ngroups = ng;
+  const std::string T = f64 ? "double" : "float";
   std::string s = kDeviceSrc;
   s += "\n// ---- model-specialised instantiation ----\n";
   s += gen_model(m, f);
-  s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(block) +
-       ") phz_step(phz::StepArgs a) { phz::run<Model, " + (f64 ? "double" : "float") + ">(a); }\n";
+  s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(64 * ng) + ") phz_step(phz::StepArgs a) {\n";
+  s += "  __shared__ " + T + " lds[(Model::NSLOT > 0 ? Model::NSLOT : 1) * 64];\n";
+  s += "  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n";
+  s += "  const int lane = threadIdx.x & 63;\n";
+  s += "  switch (g) {\n";
+  for (int g = 0; g < ng; g++)
+    s += "    case " + std::to_string(g) + ": phz::run_group<Model, " + T + ", " + std::to_string(g) + ">(a, lane, lds); break;\n";
+  s += "    default: break;\n  }\n}\n";
   return s;
 }
 
@@ -498,7 +642,9 @@ struct phz_sim {
   bool compile() {
     if (code) return true;
     std::string e;
-    const std::string src = gen_source(model, feat, f64, block);
+    int ng = 1;
+    const std::string src = gen_source(model, feat, f64, &ng);
+    block = 64 * ng;
     if (const char* dump = std::getenv("PHZ_DUMP_SOURCE")) {
       std::ofstream out(dump);
       out << src;
@@ -516,7 +662,7 @@ struct phz_sim {
   bool launch(int nsteps) {
     StepArgs a{q, v, ctrl, qdd, targets, rng, rows, nworld, stride, nsteps, feat.contact ? 1 : 0};
     void* params[] = {&a};
-    const unsigned grid = (unsigned)((nworld + block - 1) / block);
+    const unsigned grid = (unsigned)((nworld + 63) / 64);
     return hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
                   "step kernel launch");
   }
@@ -618,8 +764,6 @@ int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t 
   s->stride = (int)((nworld + 63) / 64 * 64);
   s->f64 = precision == PHZ_F64;
   s->device = device_ordinal;
-  s->block = env_int("PHZ_BLOCK", 64);
-  if (s->block != 64 && s->block != 128 && s->block != 256) s->block = 64;
   s->max_steps = std::max(1, env_int("PHZ_MAX_STEPS_PER_LAUNCH", 1000));
   const char* ge = std::getenv("PHZ_HIP_GRAPHS");
   s->graphs = !(ge && (!std::strcmp(ge, "0") || !std::strcmp(ge, "off") || !std::strcmp(ge, "false")));
