@@ -104,7 +104,7 @@ def test_host_only_sim_compiles_workload_kernels():
         s = from_workload(w, w.precisions[0], nworld=64, device=-1)
         s.compile()
         info = s.kernel_info()
-        assert info["vgpr"] > 0 and info["block"] == 64
+        assert info["vgpr"] > 0 and info["block"] % 64 == 0 and info["scratch_bytes"] == 0
 
 
 def test_pack_bodies_slots():
