@@ -104,8 +104,9 @@ int phz_load_rng(phz_sim* sim, const uint64_t* states);
 /* BatchSim::collidable_bodies (mod.rs:1000-1003). */
 int phz_collidable_bodies(const phz_sim* sim);
 
-/* Compile the step kernel for the current configuration now (otherwise it is
- * compiled at the first step). Works on host-only sims. */
+/* Compile the step kernel (and the control-loop kernels, once kinematics or
+ * the policy are enabled) for the current configuration now; otherwise each is
+ * compiled at its first launch. Works on host-only sims. */
 int phz_compile(phz_sim* sim);
 /* Measurement: `reps` spans of n steps, each bracketed by hipEvents on the
  * sim's stream; ms_per_rep[reps] receives the event times. */
@@ -114,6 +115,78 @@ int phz_time_step_many(phz_sim* sim, uint32_t n, uint32_t reps, double* ms_per_r
  * [1] AGPRs, [2] SGPRs, [3] private (scratch) bytes per lane, [4] block size,
  * [5] max steps per launch. */
 int phz_kernel_info(phz_sim* sim, int64_t* info);
+
+/* ── Device-resident control loop (mod.rs:1004-1376; policy_pipeline.rs) ──── */
+
+#define PHZ_XF_STRIDE 18      /* policy_pipeline.rs:21-29 XF_STRIDE */
+#define PHZ_OBS_OP_STRIDE 4   /* policy_pipeline.rs:31-32 OBS_OP_STRIDE */
+#define PHZ_POLICY_MAX_IN 128 /* policy_pipeline.rs:34-42 */
+#define PHZ_POLICY_MAX_H 256
+#define PHZ_POLICY_MAX_OUT 32
+
+/* BatchSim::enable_kinematics / compute_kinematics / readback_kinematics
+ * (mod.rs:1004-1040). The readout is [nworld][nb][18]: rotation world->body
+ * (row-major), body origin in world, angular and linear velocity in the body
+ * frame. compute runs FK over the current q, v on the device. */
+int phz_enable_kinematics(phz_sim* sim);
+int phz_compute_kinematics(phz_sim* sim);
+int phz_readback_kinematics(phz_sim* sim, double* rows);
+
+/* BatchSim::enable_policy (mod.rs:1045-1140) with PolicySpec
+ * (policy_pipeline.rs:300-416) passed flat:
+ *   ops        n_in x 4 rows [kind, a, b, c] of ObsOp::pack (policy_pipeline.rs:115-137)
+ *   aux        n_aux values of pack_obs_ops' aux buffer (ComOverSupport payloads)
+ *   hidden     width of both hidden layers
+ *   act_slots  n_out PD servo slots (registration order) receiving base + clamp(action)
+ *   act_clamp  scalar clamp, used when act_clamp_slots is NULL
+ *   act_clamp_slots  n_out per-action clamps, or NULL
+ *   noise_rho  AR(1) coefficient of the exploration noise
+ *   input_noise  n_in per-input noise scales
+ *   history_steps  control steps of observation/action history kept on device
+ * Needs PD control. Re-enabling with the same widths and history keeps the
+ * weights, std, streams and history buffers, like the reference. */
+int phz_enable_policy(phz_sim* sim, const double* ops, uint32_t n_in, const double* aux, uint32_t n_aux,
+                      uint32_t hidden, const uint32_t* act_slots, uint32_t n_out, double act_clamp,
+                      const double* act_clamp_slots, double noise_rho, const double* input_noise,
+                      uint32_t history_steps);
+/* BatchSim::set_policy_weights (mod.rs:1149-1162): n_in*h + h + h*h + h + h*n_out + n_out
+ * values, W1 b1 W2 b2 W3 b3, each W row-major [out][in]. */
+int phz_set_policy_weights(phz_sim* sim, const double* weights, uint64_t n);
+/* BatchSim::set_policy_std (mod.rs:1164-1177): n_out standard deviations. */
+int phz_set_policy_std(phz_sim* sim, const double* stdv, uint32_t n);
+/* BatchSim::set_policy_base_targets (mod.rs:1179-1186): [nworld][n_pd] rows. */
+int phz_set_policy_base_targets(phz_sim* sim, const double* rows);
+/* BatchSim::seed_policy (mod.rs:1188-1203): world_seed(seed, w) streams, AR(1) state zeroed. */
+int phz_seed_policy(phz_sim* sim, uint64_t seed);
+/* BatchSim::run_policy (mod.rs:1205-1270): FK, observation row `step`, MLP,
+ * Gaussian sample into action row `step` and the PD targets. */
+int phz_run_policy(phz_sim* sim, uint32_t step);
+/* BatchSim::readback_policy_history (mod.rs:1272-1302) for steps [start, end):
+ * obs [step][nworld][n_in], out [step][nworld][n_out + 1] (actions, then log-prob). */
+int phz_readback_policy_history(phz_sim* sim, uint32_t start, uint32_t end, double* obs, double* out);
+/* BatchSim::readback_targets (mod.rs:1304-1309): [nworld][n_pd]. */
+int phz_readback_targets(phz_sim* sim, double* rows);
+
+/* BatchSim::enable_state_history / record_state / readback_state_history
+ * (mod.rs:1313-1376): q [slot][nworld][nq], v [slot][nworld][nv]. */
+int phz_enable_state_history(phz_sim* sim, uint32_t slots);
+int phz_record_state(phz_sim* sim, uint32_t slot);
+int phz_readback_state_history(phz_sim* sim, uint32_t start, uint32_t end, double* q, double* v);
+
+/* Extension: a collector's rollout as one call, the loop of
+ * docs/design/cuda-backend.md section 7 — for c in [0, n_control):
+ * run_policy(first + c); step_many(control_every); if record_states,
+ * record_state(first + c). Captured into one hipGraph when graphs are enabled. */
+int phz_rollout(phz_sim* sim, uint32_t first_step, uint32_t n_control, uint32_t control_every, int record_states);
+/* Measurement: reps rollouts (as phz_rollout), each bracketed by hipEvents. */
+int phz_time_rollout(phz_sim* sim, uint32_t first_step, uint32_t n_control, uint32_t control_every,
+                     int record_states, uint32_t reps, double* ms_per_rep);
+/* Measurement: reps launches of one control-loop kernel (0 = FK/observation,
+ * 1 = policy) for history row `step`, each bracketed by hipEvents. */
+int phz_time_control_kernel(phz_sim* sim, int which, uint32_t step, uint32_t reps, double* ms_per_rep);
+/* Resource use of a control-loop kernel (0 = FK/observation, 1 = policy), as
+ * phz_kernel_info; [4] is the block size, [5] the worlds per workgroup. */
+int phz_control_kernel_info(phz_sim* sim, int which, int64_t* info);
 
 #ifdef __cplusplus
 }

@@ -48,6 +48,25 @@ SIGNATURES = {
     "phz_compile": (C.c_int, [SIM]),
     "phz_time_step_many": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp]),
     "phz_kernel_info": (C.c_int, [SIM, i64p]),
+    "phz_enable_kinematics": (C.c_int, [SIM]),
+    "phz_compute_kinematics": (C.c_int, [SIM]),
+    "phz_readback_kinematics": (C.c_int, [SIM, dp]),
+    "phz_enable_policy": (C.c_int, [SIM, dp, C.c_uint32, dp, C.c_uint32, C.c_uint32, u32p, C.c_uint32, C.c_double, dp,
+                                    C.c_double, dp, C.c_uint32]),
+    "phz_set_policy_weights": (C.c_int, [SIM, dp, C.c_uint64]),
+    "phz_set_policy_std": (C.c_int, [SIM, dp, C.c_uint32]),
+    "phz_set_policy_base_targets": (C.c_int, [SIM, dp]),
+    "phz_seed_policy": (C.c_int, [SIM, C.c_uint64]),
+    "phz_run_policy": (C.c_int, [SIM, C.c_uint32]),
+    "phz_readback_policy_history": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp, dp]),
+    "phz_readback_targets": (C.c_int, [SIM, dp]),
+    "phz_enable_state_history": (C.c_int, [SIM, C.c_uint32]),
+    "phz_record_state": (C.c_int, [SIM, C.c_uint32]),
+    "phz_readback_state_history": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp, dp]),
+    "phz_rollout": (C.c_int, [SIM, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int]),
+    "phz_time_rollout": (C.c_int, [SIM, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_uint32, dp]),
+    "phz_time_control_kernel": (C.c_int, [SIM, C.c_int, C.c_uint32, C.c_uint32, dp]),
+    "phz_control_kernel_info": (C.c_int, [SIM, C.c_int, i64p]),
 }
 
 

@@ -2,8 +2,9 @@
 
     python -m phyz_amd.build
 
-1. Embed csrc/phz_device.h as a raw string (csrc/phz_device_src.inc) so the
-   library can hand it to hiprtc with each model's constants.
+1. Embed csrc/phz_device.h and csrc/phz_control.h as raw strings
+   (csrc/phz_device_src.inc, csrc/phz_control_src.inc) so the library can hand
+   them to hiprtc with each model's constants.
 2. Compile the host library (csrc/phz_host.cpp) and the ahead-of-time layout
    kernels (csrc/phz_io.hip) for gfx950 and link them with hiprtc.
 
@@ -30,16 +31,20 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm 7 expected under /opt/rocm)")
 
 
-def embed_device_source() -> str:
-    src = open(os.path.join(CSRC, "phz_device.h")).read()
-    delim = "PHZ_DEVICE_SRC"
+def _embed(header: str, inc: str, delim: str) -> str:
+    src = open(os.path.join(CSRC, header)).read()
     assert f"){delim}\"" not in src
-    out = os.path.join(CSRC, "phz_device_src.inc")
+    out = os.path.join(CSRC, inc)
     text = f'R"{delim}({src}){delim}"\n'
     if not os.path.exists(out) or open(out).read() != text:
         with open(out, "w") as f:
             f.write(text)
     return out
+
+
+def embed_device_source() -> None:
+    _embed("phz_device.h", "phz_device_src.inc", "PHZ_DEVICE_SRC")
+    _embed("phz_control.h", "phz_control_src.inc", "PHZ_CONTROL_SRC")
 
 
 def _run(cmd, verbose):

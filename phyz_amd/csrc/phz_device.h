@@ -439,18 +439,17 @@ template <class M, class T> struct WS {
   bool ok[M::NB];
 };
 
+// Joint transform X = X_J(q) X_ptj of body i and its joint velocity S qd
+// (crates/phyz-model/src/joint.rs:253-360 maps; the same for FK and ABA).
 template <class M, class T, int i>
-__device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v, T* rows, int S, bool write_rows,
-                                           bool do_contact) {
+__device__ __forceinline__ void joint_xf(const T* q, const T* v, Xf<T>& X, SV<T>& vj) {
   constexpr int jt = M::jtype[i];
-  constexpr int p = M::parent[i];
   constexpr int qo = M::qoff[i], vo = M::voff[i];
   const R3<T> Rp = R3<T>{{T(M::ptj_rot[i][0]), T(M::ptj_rot[i][1]), T(M::ptj_rot[i][2]), T(M::ptj_rot[i][3]),
                           T(M::ptj_rot[i][4]), T(M::ptj_rot[i][5]), T(M::ptj_rot[i][6]), T(M::ptj_rot[i][7]),
                           T(M::ptj_rot[i][8])}};
   const V3<T> pp = v3(T(M::ptj_pos[i][0]), T(M::ptj_pos[i][1]), T(M::ptj_pos[i][2]));
-  Xf<T>& X = ws.X[i];
-  SV<T> vj = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  vj = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
   if constexpr (jt == J_REV) {
     T s, c;
     dsincos(-q[qo], &s, &c);
@@ -479,6 +478,15 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
     X.E = Rp;
     X.r = pp;
   }
+}
+
+template <class M, class T, int i>
+__device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v, T* rows, int S, bool write_rows,
+                                           bool do_contact) {
+  constexpr int p = M::parent[i];
+  Xf<T>& X = ws.X[i];
+  SV<T> vj;
+  joint_xf<M, T, i>(q, v, X, vj);
   if constexpr (p < 0) {
     ws.vel[i] = vj;
     ws.cb[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};

@@ -30,9 +30,12 @@
 
 #include "../../include/phyz_amd.h"
 
-// Text of phz_device.h, embedded at build time.
+// Text of phz_device.h and phz_control.h, embedded at build time.
 static const char* const kDeviceSrc =
 #include "phz_device_src.inc"
+    ;
+static const char* const kControlSrc =
+#include "phz_control_src.inc"
     ;
 
 extern "C" {
@@ -40,6 +43,7 @@ hipError_t phz_io_pack(const double* src, void* dst, int nworld, int width, int 
 hipError_t phz_io_unpack(const void* src, double* dst, int nworld, int width, int stride, int f64, hipStream_t s);
 hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s);
 hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s);
+hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 }
 
 namespace {
@@ -512,7 +516,7 @@ std::shared_ptr<CodeObject> compile_source(const std::string& src, std::string& 
   std::string log(log_size, '\0');
   if (log_size) hiprtcGetProgramLog(prog, &log[0]);
   if (rc != HIPRTC_SUCCESS) {
-    err = std::string("hiprtc compile of the step kernel failed: ") + hiprtcGetErrorString(rc) + "\n" + log;
+    err = std::string("hiprtc compile failed: ") + hiprtcGetErrorString(rc) + "\n" + log;
     hiprtcDestroyProgram(&prog);
     return nullptr;
   }
@@ -565,6 +569,236 @@ int env_int(const char* name, int def) {
   return e ? std::atoi(e) : def;
 }
 
+// ── control loop: policy spec, code generation, weight layout ───────────────
+// PolicySpec (crates/phyz-gpu/src/policy_pipeline.rs:300-416), flat.
+struct PolicyD {
+  int n_in = 0, hidden = 0, n_out = 0, history = 0;
+  std::vector<double> ops;    // n_in x 4, ObsOp::pack rows
+  std::vector<double> aux;    // ComOverSupport payloads
+  std::vector<double> noise;  // n_in
+  std::vector<double> clamp;  // n_out (the scalar broadcast when no per-slot clamp, PolicySpec::clamp_row)
+  std::vector<int> slots;     // n_out
+  double rho = 0;
+  int nhb() const { return (hidden + 15) / 16; }
+  int nob() const { return (n_out + 15) / 16; }
+  int ks1() const { return (n_in + 3) / 4; }
+  // Worlds per wave = 16 * cb: as many 16-world column blocks as keep both
+  // hidden layers' tiles (2 x nhb x cb x 4 floats per lane) within ~290 registers.
+  int cb() const { return std::max(1, std::min(4, 36 / nhb())); }
+  size_t n_weights() const {
+    const size_t i = n_in, h = hidden, o = n_out;
+    return i * h + h + h * h + h + h * o + o;
+  }
+  // Fragment buffer (floats): W1 [nhb][ks1][64], W2 [nhb][nhb][64][4], W3 [nob][nhb][64][4], biases.
+  size_t off_w2() const { return (size_t)nhb() * ks1() * 64; }
+  size_t off_w3() const { return off_w2() + (size_t)nhb() * nhb() * 256; }
+  size_t off_bias() const { return off_w3() + (size_t)nob() * nhb() * 256; }
+  size_t frag_floats() const { return off_bias() + 16 * (size_t)(2 * nhb() + nob()); }
+  bool same_shape(const PolicyD& o) const {
+    return n_in == o.n_in && hidden == o.hidden && n_out == o.n_out && history == o.history;
+  }
+};
+
+// The MLP weights in the policy kernel's MFMA fragment order (see
+// policy_wave in phz_control.h). Input order is the reference's flat
+// W1 b1 W2 b2 W3 b3 with each W row-major [out][in] (policy_pipeline.rs:460-481).
+void policy_fragments(const PolicyD& p, const double* w, std::vector<float>& out) {
+  const int NI = p.n_in, NH = p.hidden, NO = p.n_out, NHB = p.nhb(), NOB = p.nob(), KS1 = p.ks1();
+  const double* W1 = w;
+  const double* b1 = W1 + (size_t)NH * NI;
+  const double* W2 = b1 + NH;
+  const double* b2 = W2 + (size_t)NH * NH;
+  const double* W3 = b2 + NH;
+  const double* b3 = W3 + (size_t)NO * NH;
+  out.assign(p.frag_floats(), 0.0f);
+  for (int hb = 0; hb < NHB; hb++)
+    for (int s = 0; s < KS1; s++)
+      for (int l = 0; l < 64; l++) {
+        const int n = hb * 16 + (l & 15), i = 4 * s + (l >> 4);
+        if (n < NH && i < NI) out[((size_t)hb * KS1 + s) * 64 + l] = (float)W1[(size_t)n * NI + i];
+      }
+  for (int hb = 0; hb < NHB; hb++)
+    for (int kb = 0; kb < NHB; kb++)
+      for (int l = 0; l < 64; l++)
+        for (int s = 0; s < 4; s++) {
+          const int n2 = hb * 16 + (l & 15), n1 = kb * 16 + 4 * (l >> 4) + s;
+          if (n2 < NH && n1 < NH) out[p.off_w2() + (((size_t)hb * NHB + kb) * 64 + l) * 4 + s] = (float)W2[(size_t)n2 * NH + n1];
+        }
+  for (int ob = 0; ob < NOB; ob++)
+    for (int kb = 0; kb < NHB; kb++)
+      for (int l = 0; l < 64; l++)
+        for (int s = 0; s < 4; s++) {
+          const int k = ob * 16 + (l & 15), n = kb * 16 + 4 * (l >> 4) + s;
+          if (k < NO && n < NH) out[p.off_w3() + (((size_t)ob * NHB + kb) * 64 + l) * 4 + s] = (float)W3[(size_t)k * NH + n];
+        }
+  for (int n = 0; n < NH; n++) {
+    out[p.off_bias() + n] = (float)b1[n];
+    out[p.off_bias() + 16 * NHB + n] = (float)b2[n];
+  }
+  for (int k = 0; k < NO; k++) out[p.off_bias() + 32 * NHB + k] = (float)b3[k];
+}
+
+// Debug form of a packed op for error messages (the reference prints ObsOp's Debug).
+std::string describe_op(const double* r, const std::vector<double>& aux) {
+  const int kind = (int)r[0];
+  const char* names[] = {"Const", "QMinus", "V", "BodyPitch", "BodyRoll", "BodyYawError", "BodyPosZ", "BodyPos",
+                         "ComOverSupport"};
+  if (kind < 0 || kind > 8) return fmt("Unknown(%g)", r[0]);
+  switch (kind) {
+    case 0: return fmt("Const(%g)", r[3]);
+    case 1: return fmt("QMinus(%d, %g)", (int)r[1], r[3]);
+    case 5: return fmt("BodyYawError(%d, %g)", (int)r[1], r[3]);
+    case 7: return fmt("BodyPos { body: %d, axis: %d }", (int)r[1], (int)r[2]);
+    case 8: {
+      const size_t a = (size_t)r[1];
+      std::string h = a + 1 < aux.size() && aux[a] != 0.0 ? fmt("Some(%d)", (int)aux[a + 1]) : std::string("None");
+      return fmt("ComOverSupport { support: %d points, heading_body: %s, axis: %d }", (int)r[2], h.c_str(), (int)r[3]);
+    }
+    default: return fmt("%s(%d)", names[kind], (int)r[1]);
+  }
+}
+
+// PolicySpec::validate (policy_pipeline.rs:357-416) and ObsOp::check (153-183)
+// on the packed form.
+bool validate_policy(const PolicyD& p, int nq, int nv, int nb, int npd, std::string& err) {
+  if (p.n_in < 1 || p.n_in > PHZ_POLICY_MAX_IN) { err = fmt("policy input width %d not in 1..=%d", p.n_in, PHZ_POLICY_MAX_IN); return false; }
+  if (p.hidden < 1 || p.hidden > PHZ_POLICY_MAX_H) { err = fmt("policy hidden width %d not in 1..=%d", p.hidden, PHZ_POLICY_MAX_H); return false; }
+  if (p.n_out < 1 || p.n_out > PHZ_POLICY_MAX_OUT) { err = fmt("policy output width %d not in 1..=%d", p.n_out, PHZ_POLICY_MAX_OUT); return false; }
+  if (p.history < 1) { err = "policy history_steps must be at least 1"; return false; }
+  for (int k = 0; k < p.n_in; k++) {
+    const double* r = &p.ops[(size_t)k * 4];
+    bool ok = is_int(r[0]) && r[0] >= 0 && r[0] <= 8 && is_int(r[1]) && r[1] >= 0 && is_int(r[2]) && r[2] >= 0 &&
+              std::isfinite(r[3]);
+    if (ok) {
+      const int kind = (int)r[0], a = (int)r[1], b = (int)r[2];
+      switch (kind) {
+        case 0: break;
+        case 1: ok = a < nq; break;
+        case 2: ok = a < nv; break;
+        case 3: case 4: case 5: case 6: ok = a < nb; break;
+        case 7: ok = a < nb && b < 3; break;
+        case 8: {
+          ok = is_int(r[3]) && r[3] >= 0 && r[3] < 3 && (size_t)a + 2 + 4 * (size_t)b <= p.aux.size();
+          if (ok) {
+            const double flag = p.aux[a], h = p.aux[a + 1];
+            if (flag != 0.0) ok = is_int(h) && h >= 0 && h < nb;
+            for (int j = 0; ok && j < b; j++) {
+              const double* sp = &p.aux[a + 2 + 4 * (size_t)j];
+              ok = is_int(sp[0]) && sp[0] >= 0 && sp[0] < nb && std::isfinite(sp[1]) && std::isfinite(sp[2]) &&
+                   std::isfinite(sp[3]);
+            }
+          }
+          break;
+        }
+      }
+    }
+    if (!ok) {
+      err = fmt("observation op %s out of range (nq %d, nv %d, nbodies %d)", describe_op(r, p.aux).c_str(), nq, nv, nb);
+      return false;
+    }
+  }
+  for (int k = 0; k < p.n_out; k++)
+    if (p.slots[k] >= npd) { err = fmt("action slot %d exceeds the %d registered PD servos", p.slots[k], npd); return false; }
+  for (double x : p.noise) if (!std::isfinite(x)) { err = "policy input noise must be finite"; return false; }
+  for (double x : p.clamp) if (!std::isfinite(x)) { err = "policy action clamp must be finite"; return false; }
+  if (!std::isfinite(p.rho)) { err = "policy noise_rho must be finite"; return false; }
+  return true;
+}
+
+// FK + observation kernel: the model's kinematic constants and the op table.
+std::string gen_obs_source(const ModelD& m, const PolicyD* p, bool f64) {
+  const std::string T = f64 ? "double" : "float";
+  std::string s = kDeviceSrc;
+  s += "\n";
+  s += kControlSrc;
+  s += "\n// ---- model and observation table ----\n";
+  s += gen_model(m, Features{});
+  const int n = p ? p->n_in : 0, na = std::max(n, 1);
+  const std::vector<double> empty;
+  const std::vector<double>& aux = p ? p->aux : empty;
+  const int naux = std::max<int>((int)aux.size(), 1);
+  auto op = [&](int k, int slot) { return n ? p->ops[(size_t)k * 4 + slot] : 0.0; };
+  std::ostringstream o;
+  o << "struct Obs {\n  static constexpr int N = " << n << ";\n";
+  o << "  static constexpr int kind[" << na << "] = " << arr1(na, [&](int k) { return std::to_string((int)op(k, 0)); }) << ";\n";
+  o << "  static constexpr int a[" << na << "] = " << arr1(na, [&](int k) { return std::to_string((int)op(k, 1)); }) << ";\n";
+  o << "  static constexpr int b[" << na << "] = " << arr1(na, [&](int k) { return std::to_string((int)op(k, 2)); }) << ";\n";
+  o << "  static constexpr double c[" << na << "] = " << arr1(na, [&](int k) { return num(op(k, 3)); }) << ";\n";
+  o << "  static constexpr double aux[" << naux << "] = "
+    << arr1(naux, [&](int k) { return num(aux.empty() ? 0.0 : aux[k]); }) << ";\n};\n";
+  s += o.str();
+  s += "extern \"C\" __global__ void __launch_bounds__(64) phz_obs(phz::ObsArgs a) {\n";
+  s += "  const int w = blockIdx.x * 64 + threadIdx.x;\n";
+  s += "  if (w < a.nworld) phz::obs_world<Model, Obs, " + T + ">(a, w);\n}\n";
+  return s;
+}
+
+// Policy kernel: widths, action wiring and noise scales compiled in.
+std::string gen_policy_source(const PolicyD& p, int npd, bool f64) {
+  const std::string T = f64 ? "double" : "float";
+  std::string s = kDeviceSrc;
+  s += "\n";
+  s += kControlSrc;
+  const int cb = p.cb();
+  const int lds = 16 * cb * std::max(4 * p.ks1() + 1, 16 * p.nob() + 1);
+  std::ostringstream o;
+  o << "\n// ---- policy shape ----\nstruct Pol {\n";
+  o << "  static constexpr int NI = " << p.n_in << ", NH = " << p.hidden << ", NO = " << p.n_out << ", NHB = " << p.nhb()
+    << ", NOB = " << p.nob() << ", KS1 = " << p.ks1() << ", CB = " << cb << ", NPD = " << npd << ", LDS = " << lds << ";\n";
+  o << "  static constexpr double rho = " << num(p.rho) << ";\n";
+  o << "  static constexpr double noise[" << p.n_in << "] = " << arr1(p.n_in, [&](int k) { return num(p.noise[k]); }) << ";\n";
+  o << "  static constexpr double clamp[" << p.n_out << "] = " << arr1(p.n_out, [&](int k) { return num(p.clamp[k]); }) << ";\n";
+  o << "  static constexpr int slot[" << p.n_out << "] = " << arr1(p.n_out, [&](int k) { return std::to_string(p.slots[k]); })
+    << ";\n};\n";
+  s += o.str();
+  s += "extern \"C\" __global__ void __launch_bounds__(64) phz_policy(phz::PolicyArgs a) {\n";
+  s += "  __shared__ float lds[Pol::LDS];\n";
+  s += "  phz::policy_wave<Pol, " + T + ">(a, lds);\n}\n";
+  return s;
+}
+
+struct ObsArgs {  // must match phz::ObsArgs in phz_control.h
+  const void* q;
+  const void* v;
+  void* kin;
+  float* obs;
+  int nworld;
+  int stride;
+  int write_kin;
+  int write_obs;
+};
+
+struct PolicyArgs {  // must match phz::PolicyArgs in phz_control.h
+  const float* w1;
+  const void* w2;
+  const void* w3;
+  const float* bias;
+  const float* stdv;
+  float* obs;
+  float* out;
+  uint64_t* rng;
+  float* z;
+  const void* base;
+  void* targets;
+  int nworld;
+  int stride;
+};
+
+// A hiprtc-built kernel with its module, tagged with the configuration epoch it was built for.
+struct Kern {
+  std::shared_ptr<CodeObject> code;
+  hipModule_t mod = nullptr;
+  hipFunction_t fn = nullptr;
+  uint64_t epoch = 0;
+  void reset() {
+    if (mod) hipModuleUnload(mod);
+    mod = nullptr;
+    fn = nullptr;
+    code.reset();
+    epoch = 0;
+  }
+};
+
 }  // namespace
 
 struct phz_sim {
@@ -590,6 +824,26 @@ struct phz_sim {
   uint64_t epoch = 1;
   std::string err;
 
+  // Device-resident control loop (mod.rs:1004-1376).
+  bool kin_on = false;
+  void* kin = nullptr;          // [nb * 18][stride] T, FK readout
+  Kern obs_k, pol_k;
+  uint64_t ctl_epoch = 1;       // bumped when the model, PD table or policy spec changes
+  bool policy_on = false;
+  PolicyD pol;
+  float* pw = nullptr;          // weight fragments and biases
+  float* pstd = nullptr;        // [n_out]
+  float* obs_hist = nullptr;    // [history][n_in][stride]
+  float* out_hist = nullptr;    // [history][n_out + 1][stride]
+  float* pz = nullptr;          // [n_out][stride]
+  uint64_t* prng = nullptr;     // [stride]
+  void* pbase = nullptr;        // [npd][stride] T
+  int pbase_npd = 0;
+  int hist_slots = 0;
+  void *hq = nullptr, *hv = nullptr;  // [slots][nq | nv][stride] T
+  hipGraphExec_t rexec = nullptr;     // captured rollout
+  uint64_t rkey[6] = {0, 0, 0, 0, 0, 0};
+
   size_t esize() const { return f64 ? 8 : 4; }
   bool has_device() const { return device >= 0; }
 
@@ -602,12 +856,15 @@ struct phz_sim {
   void drop_graph() {
     if (gexec) { hipGraphExecDestroy(gexec); gexec = nullptr; }
     graph_steps = 0;
+    if (rexec) { hipGraphExecDestroy(rexec); rexec = nullptr; }
   }
   void invalidate() {  // a new kernel or buffer: recompile lazily, re-capture
+    if (stream) hipStreamSynchronize(stream);  // nothing in flight uses the modules unloaded below
     drop_graph();
     if (module) { hipModuleUnload(module); module = nullptr; fn = nullptr; }
     code.reset();
     epoch++;
+    ctl_epoch++;
   }
   bool alloc(void** p, size_t bytes, const char* what) {
     if (!hip_ok(hipMalloc(p, std::max<size_t>(bytes, 256)), what)) return false;
@@ -630,11 +887,13 @@ struct phz_sim {
     if (!hip_ok(hipMemcpyAsync(staging, host, bytes, hipMemcpyHostToDevice, stream), what)) return false;
     return hip_ok(phz_io_pack(staging, dst, nworld, width, stride, f64 ? 1 : 0, stream), what);
   }
-  bool download_rows(const void* src, double* host, int width, const char* what) {
+  // elem: 1 = f64, 0 = f32 source; -1 = the sim's precision.
+  bool download_rows(const void* src, double* host, int width, const char* what, int elem = -1) {
     if (width <= 0) return true;
     const size_t bytes = (size_t)nworld * width * sizeof(double);
     if (!ensure_staging(bytes)) return false;
-    if (!hip_ok(phz_io_unpack(src, staging, nworld, width, stride, f64 ? 1 : 0, stream), what)) return false;
+    const int src_f64 = elem < 0 ? (f64 ? 1 : 0) : elem;
+    if (!hip_ok(phz_io_unpack(src, staging, nworld, width, stride, src_f64, stream), what)) return false;
     if (!hip_ok(hipMemcpyAsync(host, staging, bytes, hipMemcpyDeviceToHost, stream), what)) return false;
     return hip_ok(hipStreamSynchronize(stream), what);
   }
@@ -699,13 +958,133 @@ struct phz_sim {
     return hip_ok(hipGraphLaunch(gexec, stream), "hipGraphLaunch");
   }
 
+  // ── control loop ──
+  float* obs_row(uint32_t step) const { return obs_hist + (size_t)step * pol.n_in * stride; }
+  float* out_row(uint32_t step) const { return out_hist + (size_t)step * (pol.n_out + 1) * stride; }
+
+  // Compile (and with `load`, load) the FK/observation or the policy kernel
+  // for the current configuration epoch.
+  bool ensure_ctl(bool policy_kernel, bool load) {
+    Kern& k = policy_kernel ? pol_k : obs_k;
+    if (k.code && k.epoch != ctl_epoch) {
+      if (stream) hipStreamSynchronize(stream);
+      if (rexec) { hipGraphExecDestroy(rexec); rexec = nullptr; }
+      k.reset();
+    }
+    if (!k.code) {
+      const std::string src = policy_kernel ? gen_policy_source(pol, feat.npd, f64)
+                                            : gen_obs_source(model, policy_on ? &pol : nullptr, f64);
+      std::string e;
+      k.code = compile_source(src, e);
+      if (!k.code) { err = e; return false; }
+      k.epoch = ctl_epoch;
+    }
+    if (load && !k.fn) {
+      if (!hip_ok(hipModuleLoadData(&k.mod, k.code->code.data()), "hipModuleLoadData")) return false;
+      if (!hip_ok(hipModuleGetFunction(&k.fn, k.mod, policy_kernel ? "phz_policy" : "phz_obs"), "hipModuleGetFunction"))
+        return false;
+    }
+    return true;
+  }
+  bool launch_obs(float* obs, bool write_kin) {
+    ObsArgs a{q, v, write_kin ? kin : nullptr, obs, nworld, stride, write_kin ? 1 : 0, obs ? 1 : 0};
+    void* params[] = {&a};
+    const unsigned grid = (unsigned)((nworld + 63) / 64);
+    return hip_ok(hipModuleLaunchKernel(obs_k.fn, grid, 1, 1, 64, 1, 1, 0, stream, params, nullptr), "obs kernel launch");
+  }
+  bool launch_policy(uint32_t step) {
+    const int wpw = 16 * pol.cb();
+    PolicyArgs a{pw, pw + pol.off_w2(), pw + pol.off_w3(), pw + pol.off_bias(), pstd, obs_row(step), out_row(step),
+                 prng, pz, pbase, targets, nworld, stride};
+    void* params[] = {&a};
+    const unsigned grid = (unsigned)((nworld + wpw - 1) / wpw);
+    return hip_ok(hipModuleLaunchKernel(pol_k.fn, grid, 1, 1, 64, 1, 1, 0, stream, params, nullptr),
+                  "policy kernel launch");
+  }
+  // Everything run_policy needs, checked on the host (mod.rs:1209-1231).
+  bool policy_ready(uint32_t last_step) {
+    if (!policy_on) { err = "policy pass not enabled — call enable_policy first"; return false; }
+    if (feat.npd == 0) { err = "policy pass needs PD control"; return false; }
+    if (last_step >= (uint32_t)pol.history) {
+      err = fmt("policy step %u exceeds history_steps %d", last_step, pol.history);
+      return false;
+    }
+    if (!has_device()) { err = "host-only sim (device_ordinal -1) cannot run the policy"; return false; }
+    for (int k = 0; k < pol.n_out; k++)
+      if (pol.slots[k] >= feat.npd) {
+        err = fmt("action slot %d exceeds the %d registered PD servos", pol.slots[k], feat.npd);
+        return false;
+      }
+    if (pbase_npd != feat.npd) {  // the PD table was re-registered with another servo count
+      if (pbase) hipFree(pbase);
+      pbase = nullptr;
+      if (!alloc(&pbase, (size_t)feat.npd * stride * esize(), "base targets alloc")) return false;
+      pbase_npd = feat.npd;
+    }
+    return ensure_ctl(false, true) && ensure_ctl(true, true);
+  }
+  bool record(uint32_t slot) {
+    const size_t E = esize(), S = stride;
+    return hip_ok(phz_io_copy((char*)hq + (size_t)slot * model.nq * S * E, q, (size_t)model.nq * S * E, stream),
+                  "record_state q") &&
+           hip_ok(phz_io_copy((char*)hv + (size_t)slot * model.nv * S * E, v, (size_t)model.nv * S * E, stream),
+                  "record_state v");
+  }
+  bool issue_rollout(uint32_t first, uint32_t n, uint32_t every, bool rec) {
+    for (uint32_t c = 0; c < n; c++) {
+      if (!launch_obs(obs_row(first + c), true) || !launch_policy(first + c) || !issue(every)) return false;
+      if (rec && !record(first + c)) return false;
+    }
+    return true;
+  }
+  bool rollout(uint32_t first, uint32_t n, uint32_t every, bool rec) {
+    if (n == 0) return true;
+    if (!policy_ready(first + n - 1)) return false;
+    if (rec) {
+      if (!hist_slots) { err = "state history not enabled — call enable_state_history first"; return false; }
+      if (first + n > (uint32_t)hist_slots) {
+        err = fmt("history slot %u exceeds %d slots", first + n - 1, hist_slots);
+        return false;
+      }
+    }
+    if (every > 0 && !load_kernel()) return false;
+    if (nworld == 0) return true;
+    if (!graphs) return issue_rollout(first, n, every, rec);
+    const uint64_t key[6] = {first, n, every, rec ? 1u : 0u, epoch, ctl_epoch};
+    if (!(rexec && std::equal(key, key + 6, rkey))) {
+      if (rexec) { hipGraphExecDestroy(rexec); rexec = nullptr; }
+      if (!hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) return false;
+      const bool issued = issue_rollout(first, n, every, rec);
+      hipGraph_t graph = nullptr;
+      hipError_t ec = hipStreamEndCapture(stream, &graph);
+      if (!issued) { if (graph) hipGraphDestroy(graph); return false; }
+      if (!hip_ok(ec, "hipStreamEndCapture")) return false;
+      hipError_t ei = hipGraphInstantiate(&rexec, graph, nullptr, nullptr, 0);
+      hipGraphDestroy(graph);
+      if (!hip_ok(ei, "hipGraphInstantiate")) { rexec = nullptr; return false; }
+      std::copy(key, key + 6, rkey);
+    }
+    return hip_ok(hipGraphLaunch(rexec, stream), "hipGraphLaunch");
+  }
+  void free_policy_buffers() {
+    for (void* p : {(void*)pw, (void*)pstd, (void*)obs_hist, (void*)out_hist, (void*)pz, (void*)prng, pbase})
+      if (p) hipFree(p);
+    pw = pstd = obs_hist = out_hist = pz = nullptr;
+    prng = nullptr;
+    pbase = nullptr;
+    pbase_npd = 0;
+  }
+
   ~phz_sim() {
     if (has_device()) {
       hipSetDevice(device);
       if (stream) hipStreamSynchronize(stream);
       drop_graph();
       if (module) hipModuleUnload(module);
-      for (void* p : {q, v, ctrl, qdd, targets, rows, (void*)rng, (void*)staging})
+      obs_k.reset();
+      pol_k.reset();
+      free_policy_buffers();
+      for (void* p : {q, v, ctrl, qdd, targets, rows, (void*)rng, (void*)staging, kin, hq, hv})
         if (p) hipFree(p);
       if (stream) hipStreamDestroy(stream);
     }
@@ -714,6 +1093,24 @@ struct phz_sim {
 
 namespace {
 bool set_device(phz_sim* s) { return !s->has_device() || s->hip_ok(hipSetDevice(s->device), "hipSetDevice"); }
+
+template <class F> int time_reps(phz_sim* s, uint32_t reps, double* ms_per_rep, F body) {
+  std::vector<hipEvent_t> ev(2 * (size_t)reps);
+  for (auto& e : ev)
+    if (!s->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
+  bool ok = true;
+  for (uint32_t r = 0; r < reps && ok; r++)
+    ok = s->hip_ok(hipEventRecord(ev[2 * r], s->stream), "hipEventRecord") && body() &&
+         s->hip_ok(hipEventRecord(ev[2 * r + 1], s->stream), "hipEventRecord");
+  ok = ok && s->hip_ok(hipStreamSynchronize(s->stream), "timing sync");
+  for (uint32_t r = 0; r < reps && ok; r++) {
+    float ms = 0;
+    ok = s->hip_ok(hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]), "hipEventElapsedTime");
+    ms_per_rep[r] = ms;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  return ok ? 0 : 1;
+}
 
 int set_contact(phz_sim* s, double ground_h, double friction, const double* geom, const double* gains, double k,
                 double d, uint32_t* collidable_out) {
@@ -972,7 +1369,10 @@ int phz_collidable_bodies(const phz_sim* s) { return s && s->feat.contact ? s->f
 
 int phz_compile(phz_sim* s) {
   if (!s) return 1;
-  return s->compile() ? 0 : 1;
+  if (!s->compile()) return 1;
+  if ((s->kin_on || s->policy_on) && !s->ensure_ctl(false, false)) return 1;
+  if (s->policy_on && !s->ensure_ctl(true, false)) return 1;
+  return 0;
 }
 
 int phz_time_step_many(phz_sim* s, uint32_t n, uint32_t reps, double* ms_per_rep) {
@@ -1008,6 +1408,269 @@ int phz_kernel_info(phz_sim* s, int64_t* info) {
   info[3] = remark_value(log, "ScratchSize [bytes/lane]:");
   info[4] = s->block;
   info[5] = s->max_steps;
+  return 0;
+}
+
+
+// ── device-resident control loop (mod.rs:1004-1376) ──────────────────────────
+
+int phz_enable_kinematics(phz_sim* s) {
+  if (!s) return 1;
+  if (!set_device(s)) return 1;
+  if (s->has_device() && !s->kin &&
+      !s->alloc(&s->kin, (size_t)s->model.nb * PHZ_XF_STRIDE * s->stride * s->esize(), "kinematics alloc"))
+    return 1;
+  s->kin_on = true;
+  return 0;
+}
+
+int phz_compute_kinematics(phz_sim* s) {
+  if (!s) return 1;
+  if (!s->kin_on) return s->fail("kinematics not enabled — call enable_kinematics first");
+  if (!s->has_device()) return s->fail("host-only sim (device_ordinal -1) cannot compute kinematics");
+  if (!set_device(s)) return 1;
+  if (!s->ensure_ctl(false, true)) return 1;
+  if (s->nworld == 0) return 0;
+  return s->launch_obs(nullptr, true) ? 0 : 1;
+}
+
+int phz_readback_kinematics(phz_sim* s, double* rows) {
+  if (!s) return 1;
+  if (!s->kin_on) return s->fail("kinematics not enabled");
+  if (!rows) return s->fail("null output");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->download_rows(s->kin, rows, s->model.nb * PHZ_XF_STRIDE, "readback kinematics") ? 0 : 1;
+}
+
+int phz_enable_policy(phz_sim* s, const double* ops, uint32_t n_in, const double* aux, uint32_t n_aux, uint32_t hidden,
+                      const uint32_t* act_slots, uint32_t n_out, double act_clamp, const double* act_clamp_slots,
+                      double noise_rho, const double* input_noise, uint32_t history_steps) {
+  if (!s) return 1;
+  if (s->feat.npd == 0) return s->fail("policy pass needs PD control — call enable_pd_control first");
+  if ((n_in && (!ops || !input_noise)) || (n_out && !act_slots) || (n_aux && !aux)) return s->fail("null policy table");
+  PolicyD p;
+  p.n_in = (int)std::min<uint32_t>(n_in, 1u << 20);
+  p.hidden = (int)std::min<uint32_t>(hidden, 1u << 20);
+  p.n_out = (int)std::min<uint32_t>(n_out, 1u << 20);
+  p.history = (int)std::min<uint32_t>(history_steps, 1u << 30);
+  if (n_in <= PHZ_POLICY_MAX_IN) {
+    p.ops.assign(ops, ops + (size_t)n_in * PHZ_OBS_OP_STRIDE);
+    p.noise.assign(input_noise, input_noise + n_in);
+  }
+  if (n_aux) p.aux.assign(aux, aux + n_aux);
+  if (n_out <= PHZ_POLICY_MAX_OUT) {
+    for (uint32_t k = 0; k < n_out; k++) {
+      p.slots.push_back((int)std::min<uint32_t>(act_slots[k], 1u << 20));
+      p.clamp.push_back(act_clamp_slots ? act_clamp_slots[k] : act_clamp);
+    }
+  }
+  p.rho = noise_rho;
+  std::string e;
+  if (!validate_policy(p, s->model.nq, s->model.nv, s->model.nb, s->feat.npd, e)) return s->fail(e);
+  if (phz_enable_kinematics(s)) return 1;
+  if (!set_device(s)) return 1;
+  const bool reuse = s->policy_on && s->pol.same_shape(p);
+  if (s->stream) hipStreamSynchronize(s->stream);
+  if (s->rexec) { hipGraphExecDestroy(s->rexec); s->rexec = nullptr; }
+  s->pol = p;
+  s->policy_on = true;
+  s->ctl_epoch++;
+  if (s->has_device() && !reuse) {
+    s->free_policy_buffers();
+    const size_t S = (size_t)s->stride;
+    if (!s->alloc((void**)&s->pw, p.frag_floats() * 4, "policy weights alloc") ||
+        !s->alloc((void**)&s->pstd, (size_t)p.n_out * 4, "policy std alloc") ||
+        !s->alloc((void**)&s->prng, S * 8, "policy rng alloc") ||
+        !s->alloc((void**)&s->pz, (size_t)p.n_out * S * 4, "policy noise state alloc") ||
+        !s->alloc(&s->pbase, (size_t)s->feat.npd * S * s->esize(), "base targets alloc") ||
+        !s->alloc((void**)&s->obs_hist, (size_t)p.history * p.n_in * S * 4, "observation history alloc") ||
+        !s->alloc((void**)&s->out_hist, (size_t)p.history * (p.n_out + 1) * S * 4, "action history alloc")) {
+      s->free_policy_buffers();
+      s->policy_on = false;
+      return 1;
+    }
+    s->pbase_npd = s->feat.npd;
+    if (!s->hip_ok(hipStreamSynchronize(s->stream), "enable_policy")) return 1;
+  }
+  return 0;
+}
+
+int phz_set_policy_weights(phz_sim* s, const double* weights, uint64_t n) {
+  if (!s) return 1;
+  if (!s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
+  if (n != s->pol.n_weights())
+    return s->fail(fmt("policy expects %zu weights, got %llu", s->pol.n_weights(), (unsigned long long)n));
+  if (!weights) return s->fail("null weights");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  std::vector<float> frag;
+  policy_fragments(s->pol, weights, frag);
+  if (!s->hip_ok(hipMemcpyAsync(s->pw, frag.data(), frag.size() * 4, hipMemcpyHostToDevice, s->stream), "upload weights"))
+    return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "upload weights") ? 0 : 1;
+}
+
+int phz_set_policy_std(phz_sim* s, const double* stdv, uint32_t n) {
+  if (!s) return 1;
+  if (!s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
+  if ((int)n != s->pol.n_out) return s->fail(fmt("policy has %d actions, got %u stds", s->pol.n_out, n));
+  if (!stdv) return s->fail("null std");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  std::vector<float> f(stdv, stdv + n);
+  if (!s->hip_ok(hipMemcpyAsync(s->pstd, f.data(), n * 4, hipMemcpyHostToDevice, s->stream), "upload std")) return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "upload std") ? 0 : 1;
+}
+
+int phz_set_policy_base_targets(phz_sim* s, const double* rows) {
+  if (!s) return 1;
+  if (!s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
+  if (!rows) return s->fail("null base targets");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (s->pbase_npd != s->feat.npd) {
+    if (s->pbase) hipFree(s->pbase);
+    s->pbase = nullptr;
+    if (!s->alloc(&s->pbase, (size_t)s->feat.npd * s->stride * s->esize(), "base targets alloc")) return 1;
+    s->pbase_npd = s->feat.npd;
+  }
+  if (!s->upload_rows(rows, s->pbase, s->feat.npd, "upload base targets")) return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "set_policy_base_targets") ? 0 : 1;
+}
+
+int phz_seed_policy(phz_sim* s, uint64_t seed) {
+  if (!s) return 1;
+  if (!s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  if (!s->hip_ok(phz_io_seed(s->prng, seed, s->nworld, s->stream), "seed policy") ||
+      !s->hip_ok(phz_io_zero(s->pz, (size_t)s->pol.n_out * s->stride * 4, s->stream), "zero noise state"))
+    return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "seed_policy") ? 0 : 1;
+}
+
+int phz_run_policy(phz_sim* s, uint32_t step) {
+  if (!s) return 1;
+  if (!set_device(s)) return 1;
+  if (!s->policy_ready(step)) return 1;
+  if (s->nworld == 0) return 0;
+  return s->launch_obs(s->obs_row(step), true) && s->launch_policy(step) ? 0 : 1;
+}
+
+int phz_readback_policy_history(phz_sim* s, uint32_t start, uint32_t end, double* obs, double* out) {
+  if (!s) return 1;
+  if (!s->policy_on) return s->fail("policy pass not enabled");
+  if (end > (uint32_t)s->pol.history || start > end)
+    return s->fail(fmt("policy history range %u..%u outside 0..%d", start, end, s->pol.history));
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  const size_t W = (size_t)s->nworld;
+  for (uint32_t k = start; k < end; k++) {
+    if (obs && !s->download_rows(s->obs_row(k), obs + (k - start) * W * s->pol.n_in, s->pol.n_in, "readback obs", 0))
+      return 1;
+    if (out && !s->download_rows(s->out_row(k), out + (k - start) * W * (s->pol.n_out + 1), s->pol.n_out + 1,
+                                 "readback actions", 0))
+      return 1;
+  }
+  return 0;
+}
+
+int phz_readback_targets(phz_sim* s, double* rows) {
+  if (!s) return 1;
+  if (s->feat.npd == 0) return s->fail("PD control not enabled");
+  if (!rows) return s->fail("null output");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->download_rows(s->targets, rows, s->feat.npd, "readback targets") ? 0 : 1;
+}
+
+int phz_enable_state_history(phz_sim* s, uint32_t slots) {
+  if (!s) return 1;
+  if (slots == 0) return s->fail("state history needs at least one slot");
+  if (slots > (1u << 20)) return s->fail("state history slot count too large");
+  if (s->hist_slots == (int)slots) return 0;
+  if (!set_device(s)) return 1;
+  if (s->has_device()) {
+    if (s->stream) hipStreamSynchronize(s->stream);
+    if (s->rexec) { hipGraphExecDestroy(s->rexec); s->rexec = nullptr; }
+    for (void** p : {&s->hq, &s->hv}) { if (*p) hipFree(*p); *p = nullptr; }
+    const size_t E = s->esize(), S = s->stride;
+    if (!s->alloc(&s->hq, (size_t)slots * s->model.nq * S * E, "state history alloc") ||
+        !s->alloc(&s->hv, (size_t)slots * s->model.nv * S * E, "state history alloc")) {
+      s->hist_slots = 0;
+      return 1;
+    }
+  }
+  s->hist_slots = (int)slots;
+  return 0;
+}
+
+int phz_record_state(phz_sim* s, uint32_t slot) {
+  if (!s) return 1;
+  if (!s->hist_slots) return s->fail("state history not enabled — call enable_state_history first");
+  if (slot >= (uint32_t)s->hist_slots) return s->fail(fmt("history slot %u exceeds %d slots", slot, s->hist_slots));
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  return s->record(slot) ? 0 : 1;
+}
+
+int phz_readback_state_history(phz_sim* s, uint32_t start, uint32_t end, double* q, double* v) {
+  if (!s) return 1;
+  if (!s->hist_slots) return s->fail("state history not enabled");
+  if (end > (uint32_t)s->hist_slots || start > end)
+    return s->fail(fmt("history range %u..%u outside 0..%d", start, end, s->hist_slots));
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  const size_t W = (size_t)s->nworld, E = s->esize(), S = s->stride;
+  const int nq = s->model.nq, nv = s->model.nv;
+  for (uint32_t k = start; k < end; k++) {
+    if (q && !s->download_rows((char*)s->hq + k * nq * S * E, q + (k - start) * W * nq, nq, "readback history q"))
+      return 1;
+    if (v && !s->download_rows((char*)s->hv + k * nv * S * E, v + (k - start) * W * nv, nv, "readback history v"))
+      return 1;
+  }
+  return 0;
+}
+
+int phz_rollout(phz_sim* s, uint32_t first_step, uint32_t n_control, uint32_t control_every, int record_states) {
+  if (!s) return 1;
+  if (!set_device(s)) return 1;
+  return s->rollout(first_step, n_control, control_every, record_states != 0) ? 0 : 1;
+}
+
+
+int phz_time_rollout(phz_sim* s, uint32_t first_step, uint32_t n_control, uint32_t control_every, int record_states,
+                     uint32_t reps, double* ms_per_rep) {
+  if (!s || !ms_per_rep) return 1;
+  if (!set_device(s)) return 1;
+  // Build and capture outside the timed region.
+  if (!s->rollout(first_step, n_control, control_every, record_states != 0)) return 1;
+  return time_reps(s, reps, ms_per_rep, [&] { return s->rollout(first_step, n_control, control_every, record_states != 0); });
+}
+
+int phz_time_control_kernel(phz_sim* s, int which, uint32_t step, uint32_t reps, double* ms_per_rep) {
+  if (!s || !ms_per_rep) return 1;
+  if (which != 0 && which != 1) return s->fail("kernel must be 0 (observation) or 1 (policy)");
+  if (!set_device(s)) return 1;
+  if (!s->policy_ready(step)) return 1;
+  if (s->nworld == 0) return s->fail("no worlds");
+  return time_reps(s, reps, ms_per_rep,
+                   [&] { return which == 0 ? s->launch_obs(s->obs_row(step), true) : s->launch_policy(step); });
+}
+
+int phz_control_kernel_info(phz_sim* s, int which, int64_t* info) {
+  if (!s || !info) return 1;
+  if (which != 0 && which != 1) return s->fail("kernel must be 0 (observation) or 1 (policy)");
+  if (which == 1 && !s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
+  if (!s->ensure_ctl(which == 1, false)) return 1;
+  const std::string& log = (which == 1 ? s->pol_k : s->obs_k).code->log;
+  info[0] = remark_value(log, "VGPRs:");
+  info[1] = remark_value(log, "AGPRs:");
+  info[2] = remark_value(log, "SGPRs:");
+  info[3] = remark_value(log, "ScratchSize [bytes/lane]:");
+  info[4] = 64;
+  info[5] = which == 1 ? 16 * s->pol.cb() : 64;
   return 0;
 }
 

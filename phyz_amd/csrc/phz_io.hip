@@ -42,6 +42,13 @@ __global__ void seed_worlds(uint64_t* __restrict__ rng, uint64_t seed, int nworl
   rng[w] = z ? z : 1;
 }
 
+// dst[i] = src[i], 4-byte words (state snapshots; a kernel rather than a
+// memcpy node so that a captured rollout holds only kernel nodes).
+__global__ void copy_words(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
 constexpr int kBlock = 256;
 inline int blocks(size_t n) { return (int)((n + kBlock - 1) / kBlock); }
 
@@ -68,6 +75,13 @@ hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
   const size_t n = bytes / 4;
   hipLaunchKernelGGL(fill_zero<uint32_t>, dim3(blocks(n)), dim3(kBlock), 0, s, (uint32_t*)dst, n);
+  return hipGetLastError();
+}
+
+hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  const size_t n = bytes / 4;
+  hipLaunchKernelGGL(copy_words, dim3(blocks(n)), dim3(kBlock), 0, s, (uint32_t*)dst, (const uint32_t*)src, n);
   return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@ import numpy as np
 
 from . import _lib
 from .model import Model, PdDof, pack_bodies, pack_geometries, pack_pd_dofs
+from .policy import XF_STRIDE, PolicySpec, pack_obs_ops
 
 F32, F64 = 0, 1
 NOISE_NORMAL, NOISE_UNIFORM = 0, 1
@@ -192,6 +193,106 @@ class BatchSim:
         ms = np.zeros(reps)
         self._check(self._L.phz_time_step_many(self._h, int(n), int(reps), _dp(ms)))
         return ms
+
+    # ── device-resident control loop (mod.rs:1004-1376) ──
+    def enable_kinematics(self):
+        self._check(self._L.phz_enable_kinematics(self._h))
+
+    def compute_kinematics(self):
+        self._check(self._L.phz_compute_kinematics(self._h))
+
+    def readback_kinematics(self) -> np.ndarray:
+        """[nworld][nb][18]: rotation world->body (row-major), origin, omega, v (body frame)."""
+        rows = np.zeros((self.nworld, self.nb, XF_STRIDE))
+        self._check(self._L.phz_readback_kinematics(self._h, _dp(rows)))
+        return rows
+
+    def enable_policy(self, spec: PolicySpec):
+        spec.check_lengths()
+        table, aux = pack_obs_ops(spec.obs)
+        table = np.ascontiguousarray(table)
+        aux = np.ascontiguousarray(aux)
+        noise = np.ascontiguousarray(np.asarray(spec.input_noise, dtype=np.float64))
+        slots = (C.c_uint32 * max(spec.n_out(), 1))(*[int(s) for s in spec.act_slots])
+        cs = None if spec.act_clamp_slots is None else np.ascontiguousarray(np.asarray(spec.act_clamp_slots, dtype=np.float64))
+        self._check(self._L.phz_enable_policy(self._h, _dp(table) if len(table) else None, spec.n_in(),
+                                              _dp(aux) if len(aux) else None, len(aux), int(spec.hidden), slots,
+                                              spec.n_out(), float(spec.act_clamp), _dp(cs), float(spec.noise_rho),
+                                              _dp(noise) if len(noise) else None, int(spec.history_steps)))
+        self._policy = spec
+
+    def set_policy_weights(self, weights):
+        w = np.ascontiguousarray(np.asarray(weights, dtype=np.float64).ravel())
+        self._check(self._L.phz_set_policy_weights(self._h, _dp(w), w.size))
+
+    def set_policy_std(self, std):
+        s = np.ascontiguousarray(np.asarray(std, dtype=np.float64).ravel())
+        self._check(self._L.phz_set_policy_std(self._h, _dp(s), s.size))
+
+    def set_policy_base_targets(self, rows):
+        self._check(self._L.phz_set_policy_base_targets(self._h, _dp(_rows(rows, self.nworld, self._npd, "base targets"))))
+
+    def seed_policy(self, seed: int):
+        self._check(self._L.phz_seed_policy(self._h, int(seed)))
+
+    def run_policy(self, step: int):
+        self._check(self._L.phz_run_policy(self._h, int(step)))
+
+    def readback_policy_history(self, start: int, end: int):
+        """(obs [n][nworld][n_in], out [n][nworld][n_out + 1]) for control steps [start, end)."""
+        spec = self._policy_spec()
+        n = max(int(end) - int(start), 0)
+        obs = np.zeros((n, self.nworld, spec.n_in()))
+        out = np.zeros((n, self.nworld, spec.n_out() + 1))
+        self._check(self._L.phz_readback_policy_history(self._h, int(start), int(end), _dp(obs), _dp(out)))
+        return obs, out
+
+    def readback_targets(self) -> np.ndarray:
+        rows = np.zeros((self.nworld, max(self._npd, 1)))
+        self._check(self._L.phz_readback_targets(self._h, _dp(rows)))
+        return rows[:, :self._npd]
+
+    def enable_state_history(self, slots: int):
+        self._check(self._L.phz_enable_state_history(self._h, int(slots)))
+
+    def record_state(self, slot: int):
+        self._check(self._L.phz_record_state(self._h, int(slot)))
+
+    def readback_state_history(self, start: int, end: int):
+        """(q [n][nworld][nq], v [n][nworld][nv]) for history slots [start, end)."""
+        n = max(int(end) - int(start), 0)
+        q = np.zeros((n, self.nworld, self.nq))
+        v = np.zeros((n, self.nworld, self.nv))
+        self._check(self._L.phz_readback_state_history(self._h, int(start), int(end), _dp(q), _dp(v)))
+        return q, v
+
+    def rollout(self, first_step: int, n_control: int, control_every: int, record_states: bool = False):
+        self._check(self._L.phz_rollout(self._h, int(first_step), int(n_control), int(control_every),
+                                        1 if record_states else 0))
+
+    def time_rollout(self, first_step: int, n_control: int, control_every: int, record_states: bool,
+                     reps: int) -> np.ndarray:
+        ms = np.zeros(reps)
+        self._check(self._L.phz_time_rollout(self._h, int(first_step), int(n_control), int(control_every),
+                                             1 if record_states else 0, int(reps), _dp(ms)))
+        return ms
+
+    def time_control_kernel(self, which: str, step: int, reps: int) -> np.ndarray:
+        ms = np.zeros(reps)
+        self._check(self._L.phz_time_control_kernel(self._h, {"obs": 0, "policy": 1}[which], int(step), int(reps), _dp(ms)))
+        return ms
+
+    def control_kernel_info(self, which: str) -> dict:
+        info = (C.c_int64 * 6)()
+        self._check(self._L.phz_control_kernel_info(self._h, {"obs": 0, "policy": 1}[which], info))
+        keys = ("vgpr", "agpr", "sgpr", "scratch_bytes", "block", "worlds_per_block")
+        return dict(zip(keys, [int(x) for x in info]))
+
+    def _policy_spec(self) -> PolicySpec:
+        spec = getattr(self, "_policy", None)
+        if spec is None:
+            raise PhzError("policy pass not enabled")
+        return spec
 
 
 def from_workload(w, precision: str, nworld: Optional[int] = None, device: int = 0) -> BatchSim:

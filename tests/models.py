@@ -105,3 +105,16 @@ def random_tree(seed, njoints=8, with_free_root=True):
                   spring_ref=0.1, armature=float(rng.uniform(0, 0.1)))
         b.add_body(f"b{i}", parent, j, rinertia())
     return b.build()
+
+
+def trunk_and_two_feet():
+    """Free trunk with two hinged feet, offset centres of mass (cuda_vs_cpu.rs:1418-1443)."""
+    def off(m, c):
+        return SpatialInertia.new(m, c, np.diag([0.1, 0.1, 0.1]))
+    return (ModelBuilder().gravity([0, 0, -9.81]).dt(0.001)
+            .add_body("trunk", -1, Joint(FREE, SpatialTransform.identity(), np.zeros(3)), off(8.0, [0.02, 0.0, 0.15]))
+            .add_revolute_body("left_foot", 0, SpatialTransform.from_translation([0.0, 0.12, -0.6]),
+                               off(1.5, [0.03, 0.0, -0.02]))
+            .add_revolute_body("right_foot", 0, SpatialTransform.from_translation([0.0, -0.12, -0.6]),
+                               off(1.5, [-0.03, 0.01, -0.02]))
+            .build())

@@ -144,3 +144,77 @@ def test_workload_shapes(idx, nb, nv):
         assert sum(1 for b in w.model.bodies if b.joint.jtype == 0) == 21
     if idx == 5:
         assert tg.shape == (16, 24) and len(w.pd) == 24
+
+
+def _limb_spec(**kw):
+    from phyz_amd import policy as P
+    base = dict(obs=[P.V(0)], hidden=8, act_slots=[0], act_clamp=0.5, input_noise=[0.0], history_steps=2)
+    base.update(kw)
+    return P.PolicySpec(**base)
+
+
+def test_policy_errors_match_reference():
+    """PolicySpec::validate / ObsOp::check (policy_pipeline.rs:153-183, 357-416) and
+    the BatchSim guards (mod.rs:1004-1376), through the C ABI."""
+    from phyz_amd import policy as P
+    m = TM.free_base_with_limb()
+    s = host_sim(m)
+    with pytest.raises(PhzError, match="policy pass needs PD control"):
+        s.enable_policy(_limb_spec())
+    with pytest.raises(PhzError, match="policy pass not enabled"):
+        s.set_policy_weights([0.0])
+    with pytest.raises(PhzError, match="kinematics not enabled"):
+        s.compute_kinematics()
+    s.enable_pd_control([PdDof(6, 6, 20.0, 1.0, 10.0)])
+    cases = [
+        (dict(obs=[], input_noise=[]), "policy input width 0 not in 1..=128"),
+        (dict(hidden=0), "policy hidden width 0 not in 1..=256"),
+        (dict(hidden=257), "policy hidden width 257 not in 1..=256"),
+        (dict(act_slots=[]), "policy output width 0 not in 1..=32"),
+        (dict(history_steps=0), "policy history_steps must be at least 1"),
+        (dict(obs=[P.QMinus(7, 0.0)]), r"observation op QMinus\(7, 0\) out of range \(nq 7, nv 7, nbodies 2\)"),
+        (dict(obs=[P.V(7)]), r"observation op V\(7\) out of range"),
+        (dict(obs=[P.BodyPitch(2)]), r"observation op BodyPitch\(2\) out of range"),
+        (dict(obs=[P.BodyPos(1, 3)]), r"observation op BodyPos \{ body: 1, axis: 3 \} out of range"),
+        (dict(obs=[P.ComOverSupport([(5, [0, 0, 0])], None, 0)]), "observation op ComOverSupport.* out of range"),
+        (dict(obs=[P.ComOverSupport([(1, [0, 0, 0])], 2, 0)]), r"heading_body: Some\(2\).* out of range"),
+        (dict(act_slots=[1]), "action slot 1 exceeds the 1 registered PD servos"),
+    ]
+    for kw, msg in cases:
+        with pytest.raises(PhzError, match=msg):
+            s.enable_policy(_limb_spec(**kw))
+    with pytest.raises(ValueError, match="input_noise has 2 entries for 1 inputs"):
+        s.enable_policy(_limb_spec(input_noise=[0.0, 0.0]))
+    s.enable_policy(_limb_spec())
+    with pytest.raises(PhzError, match="policy expects 97 weights, got 3"):
+        s.set_policy_weights([0.0, 0.0, 0.0])
+    with pytest.raises(PhzError, match="policy has 1 actions, got 2 stds"):
+        s.set_policy_std([1.0, 1.0])
+    with pytest.raises(PhzError, match="host-only"):
+        s.run_policy(0)
+    with pytest.raises(PhzError, match="state history needs at least one slot"):
+        s.enable_state_history(0)
+    with pytest.raises(PhzError, match="state history not enabled"):
+        s.record_state(0)
+    s.enable_state_history(2)
+    with pytest.raises(PhzError, match="history slot 2 exceeds 2 slots"):
+        s.record_state(2)
+
+
+def test_host_only_sim_compiles_control_kernels():
+    """The FK/observation and MFMA policy kernels compile for gfx950 without
+    scratch at the largest widths the reference accepts (128 in, 256 hidden, 32 out)."""
+    from phyz_amd import policy as P
+    w = W.config(4)
+    s = BatchSim(w.model, 64, "f32", device=-1)
+    s.enable_pd_control([PdDof(6 + k, 6 + k, 20.0, 1.0, 10.0) for k in range(21)])
+    obs = [P.V(i % 27) for i in range(120)] + [P.BodyPitch(0), P.BodyRoll(0), P.BodyYawError(0, 0.0), P.BodyPosZ(3),
+                                                P.BodyPos(5, 1), P.QMinus(7, 0.1), P.Const(1.0),
+                                                P.ComOverSupport([(9, [0, 0, -0.1]), (12, [0, 0, -0.1])], 0, 1)]
+    s.enable_policy(P.PolicySpec(obs=obs, hidden=256, act_slots=[k % 21 for k in range(32)], act_clamp=0.4,
+                                 input_noise=[0.01] * len(obs), history_steps=1))
+    s.compile()
+    for k in ("obs", "policy"):
+        info = s.control_kernel_info(k)
+        assert info["vgpr"] > 0 and info["scratch_bytes"] == 0, (k, info)
+    assert s.control_kernel_info("policy")["worlds_per_block"] == 32
