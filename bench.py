@@ -161,6 +161,105 @@ def cpu_baseline(w, sim, prec, budget_s=20.0):
     }, {"worlds_checked": len(idx), "qdd_rel_err_max": err}
 
 
+def run_control_loop(prec: str, reps: int, with_cpu: bool):
+    """The ant driven by the on-device policy (phyz_amd.workloads.control_loop):
+    a rollout of n_control control steps, each FK + observation, the MLP policy,
+    control_every physics steps and a state snapshot, as one captured graph."""
+    from phyz_amd import workloads as W
+    from phyz_amd.sim import from_control_loop
+    cl = W.control_loop()
+    n, nc, every = cl.nworld, cl.n_control, cl.control_every
+    log(f"[bench] control loop {cl.name}: {n} worlds, {nc} control steps x {every} physics steps, "
+        f"MLP {cl.spec.n_in()}-{cl.spec.hidden}-{cl.spec.hidden}-{cl.spec.n_out()}")
+    sim = from_control_loop(cl, prec)
+    q, v, _, _ = cl.base.initial_state()
+    sim.load_states(q, v)
+    sim.compile()
+    sim.rollout(0, nc, every, True)  # builds the kernels and captures the rollout graph
+    sim.synchronize()
+    ev = []
+    for _ in range(reps):
+        sim.load_states(q, v)
+        sim.seed_policy(cl.seed)
+        ev.extend(sim.time_rollout(0, nc, every, True, 1))
+    t_roll = float(np.median(ev))
+    t_obs = float(np.median(sim.time_control_kernel("obs", 0, 20)))
+    t_pol = float(np.median(sim.time_control_kernel("policy", 0, 20)))
+    t_phys = float(np.median(sim.time_step_many(nc * every, 3)))
+    m = cl.base.model
+    obs_bytes = n * 4 * ((m.nq + m.nv) + 18 * m.nbodies + cl.spec.n_in())
+    pol_flops = cl.flops_per_world() * n
+    out = {
+        "workload": cl.name, "nworld": n, "n_control": nc, "control_every": every, "dtype": prec,
+        "mlp": [cl.spec.n_in(), cl.spec.hidden, cl.spec.hidden, cl.spec.n_out()],
+        "rollout_ms": {"median": round(t_roll, 4), "min": round(float(min(ev)), 4), "max": round(float(max(ev)), 4)},
+        "world_steps_per_s": round(n * nc * every / (t_roll / 1e3), 1),
+        "control_steps_per_s": round(n * nc / (t_roll / 1e3), 1),
+        "physics_only_ms": round(t_phys, 4),
+        "policy_roofline": {"bound": "mfma", "achieved": round(pol_flops / (t_pol / 1e3) / 1e12, 3), "peak": 157.3,
+                            "unit": "TFLOP/s", "frac": round(pol_flops / (t_pol / 1e3) / 1e12 / 157.3, 4),
+                            "launch_ms": round(t_pol, 5), "flops_per_world": cl.flops_per_world(),
+                            "kernel": sim.control_kernel_info("policy")},
+        "obs_roofline": {"bound": "hbm", "achieved": round(obs_bytes / (t_obs / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(obs_bytes / (t_obs / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "launch_ms": round(t_obs, 5), "bytes_per_world": obs_bytes // n},
+    }
+    log(f"[bench] control loop: {out['world_steps_per_s']:.4g} world-steps/s, rollout {t_roll:.3f} ms "
+        f"(physics alone {t_phys:.3f} ms), policy {t_pol:.4f} ms = {out['policy_roofline']['achieved']} TFLOP/s, "
+        f"obs {t_obs:.4f} ms = {out['obs_roofline']['achieved']} GB/s")
+    # Parity: one control step of sampled worlds against the oracle, exact stream replay.
+    from oracle import policy_ref as PR
+    from oracle.oracle import Oracle
+    from phyz_amd.model import pack_geometries, pack_pd_dofs
+    sim.load_states(q, v)
+    sim.seed_policy(cl.seed)
+    sim.run_policy(0)
+    dq, dv = sim.readback_states()
+    obs_h, out_h = sim.readback_policy_history(0, 1)
+    tgt = sim.readback_targets()
+    g, _ = pack_geometries(m, cl.base.contact.stiffness, cl.base.contact.damping)
+    orc = Oracle(m, contact=(g, cl.base.contact.ground_height, cl.base.contact.friction), pd=pack_pd_dofs(cl.pd))
+    idx = np.linspace(0, n - 1, 32).astype(int)
+    base = cl.base_targets(n)
+    err = {"obs": 0.0, "act": 0.0, "logp": 0.0, "targets": 0.0}
+    for k in idx:
+        o = np.array(PR.observe_reference(m, orc, dq[k], dv[k], cl.spec.obs))
+        z = np.zeros(cl.spec.n_out())
+        t = np.zeros(len(cl.pd))
+        a, lp = PR.policy_reference(cl.spec, cl.weights, cl.std, PR.KernelRng.for_world(cl.seed, int(k)), o, z, base[k], t)
+        err["obs"] = max(err["obs"], float(np.abs(obs_h[0, k] - o).max()))
+        err["act"] = max(err["act"], float(np.abs(out_h[0, k, :-1] - a).max()))
+        err["logp"] = max(err["logp"], abs(float(out_h[0, k, -1]) - lp))
+        err["targets"] = max(err["targets"], float(np.abs(tgt[k] - t).max()))
+    out["parity"] = {"worlds_checked": len(idx), **{k: float(f"{e:.3g}") for k, e in err.items()}}
+    if with_cpu:
+        out["cpu_baseline"] = control_cpu_baseline(cl, orc)
+    return out
+
+
+def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
+    """The oracle's rollout (observe + policy per world, then the f64 physics
+    steps) on a bounded sample, single-threaded Python/C++."""
+    from oracle import policy_ref as PR
+    m = cl.base.model
+    q, v, c, _ = cl.base.initial_state(nworld)
+    base = cl.base_targets(nworld)
+    rngs = [PR.KernelRng.for_world(cl.seed, w) for w in range(nworld)]
+    zs = np.zeros((nworld, cl.spec.n_out()))
+    tg = np.zeros((nworld, len(cl.pd)))
+    t0 = time.perf_counter()
+    for _ in range(n_control):
+        for w in range(nworld):
+            o = np.array(PR.observe_reference(m, orc, q[w], v[w], cl.spec.obs))
+            PR.policy_reference(cl.spec, cl.weights, cl.std, rngs[w], o, zs[w], base[w], tg[w])
+        orc.step_batch(q, v, c, cl.control_every, targets=tg, threads=1)
+    dt = time.perf_counter() - t0
+    return {"value": round(nworld * n_control * cl.control_every / dt, 1), "unit": "world-steps/s", "cores": 1,
+            "kind": "port", "sample": f"{nworld} worlds x {n_control} control steps x {cl.control_every} physics steps, "
+                                      f"f64 oracle (Python observation/policy, C++ physics), {dt:.1f} s",
+            "control_steps_per_s": round(nworld * n_control / dt, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +268,8 @@ def main():
     ap.add_argument("--workload", type=int, default=2)
     ap.add_argument("--reps", type=int, default=7)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-control", action="store_true", help="skip the on-device control-loop measurement")
+    ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
     ap.add_argument("--precision", choices=["f32", "f64"], default=None, help="run one precision only")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (HBM counter calibration)")
@@ -187,6 +288,10 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (worlds are independent: "
               "a multi-GPU run is N disjoint world ranges, one per GPU).", file=sys.stderr)
         sys.exit(2)
+
+    if args.control_only:
+        print(json.dumps(run_control_loop("f32", args.reps, not args.no_cpu)), flush=True)
+        return
 
     from phyz_amd import workloads as W
     w = W.config(args.workload)
@@ -256,6 +361,8 @@ def main():
             line[prec] = results[prec]
     if parity:
         line["parity"] = parity
+    if not args.no_control:
+        line["control_loop"] = run_control_loop("f32", min(args.reps, 5), not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -178,7 +178,9 @@ int phz_readback_state_history(phz_sim* sim, uint32_t start, uint32_t end, doubl
  * run_policy(first + c); step_many(control_every); if record_states,
  * record_state(first + c). Captured into one hipGraph when graphs are enabled. */
 int phz_rollout(phz_sim* sim, uint32_t first_step, uint32_t n_control, uint32_t control_every, int record_states);
-/* Measurement: reps rollouts (as phz_rollout), each bracketed by hipEvents. */
+/* Measurement: reps rollouts (as phz_rollout), each bracketed by hipEvents.
+ * The first rollout of a new shape captures its graph: warm up with
+ * phz_rollout first to keep capture out of the timed region. */
 int phz_time_rollout(phz_sim* sim, uint32_t first_step, uint32_t n_control, uint32_t control_every,
                      int record_states, uint32_t reps, double* ms_per_rep);
 /* Measurement: reps launches of one control-loop kernel (0 = FK/observation,

@@ -196,9 +196,9 @@ template <class M, class O, class T> __device__ __forceinline__ void obs_world(c
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct PolicyArgs {
-  const float* w1;     // [NHB][KS1][64] fragments of W1 (host re-layout, zero padded)
-  const f32x4* w2;     // [NHB][NHB][64] x 4 fragments of W2
-  const f32x4* w3;     // [NOB][NHB][64] x 4 fragments of W3
+  const f32x4* w1;     // [KU][NHB][64] x 4 fragments of W1 (host re-layout, zero padded)
+  const f32x4* w2;     // [NHB][NHB][64] x 4 fragments of W2, input block major
+  const f32x4* w3;     // [NHB][NOB][64] x 4 fragments of W3, input block major
   const float* bias;   // b1[NHB*16] b2[NHB*16] b3[NOB*16], zero padded
   const float* stdv;   // [NO]
   float* obs;          // [NI][stride], this control step's history row (noised in place)
@@ -225,16 +225,77 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// tanh without branches, from tanh|x| = (1 - t) / (1 + t), t = e^(-2|x|) = 2^(-2|x| log2 e)
+// (hardware exp2 and reciprocal, about 1 ulp each), and the odd series
+// x - x^3/3 + 2x^5/15 - 17x^7/315 below |x| = 1/16, where 1 - t cancels; the
+// series' first omitted term is under 1e-12 relative there. Absolute error
+// stays near 2e-7 over the whole range; NaN propagates.
+__device__ __forceinline__ float tanh_mlp(float x) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_exp2f(-2.88539008177792681f * ax);
+  const float big = (1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t);
+  const float x2 = x * x;
+  const float small = ax * (1.0f + x2 * (-0.333333333333f + x2 * (0.133333333333f + x2 * -0.0539682539683f)));
+  return copysignf(ax < 0.0625f ? small : big, x);
+}
+
+template <int NB_, int CB> __device__ __forceinline__ void bias_tiles(const float* bias, int g, f32x4 (&acc)[NB_][CB]) {
+#pragma unroll
+  for (int ob = 0; ob < NB_; ob++) {
+    f32x4 b0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) b0[j] = bias[ob * 16 + 4 * g + j];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) acc[ob][cb] = b0;
+  }
+}
+
+template <int NB_, int CB> __device__ __forceinline__ void tanh_tiles(f32x4 (&h)[NB_][CB]) {
+#pragma unroll
+  for (int ob = 0; ob < NB_; ob++)
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) h[ob][cb][j] = tanh_mlp(h[ob][cb][j]);
+}
+
+// acc[ob][cb] += sum over k of W[ob block][k] B[k][cb block]. The weights are
+// fragments [kb][ob][lane] x 4 (component s = k-step s of input block kb), read
+// in that order as one contiguous stream with PF fragments in flight; the
+// sched_barrier keeps the compiler from sinking the prefetches to their use,
+// which would expose a full L2 round trip per fragment. bfrag(kb, s, cb) is
+// the B operand (this lane's input value) of k-step s of block kb for world
+// block cb.
+template <int NKB, int NOB_, int CB, class BF>
+__device__ __forceinline__ void mfma_layer(const f32x4* __restrict__ w, int lane, f32x4 (&acc)[NOB_][CB], BF bfrag) {
+  constexpr int NT = NKB * NOB_;
+  constexpr int PF = NT < 6 ? NT : 6;
+  f32x4 ring[PF];
+#pragma unroll
+  for (int t = 0; t < PF; t++) ring[t] = w[t * 64 + lane];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int kb = t / NOB_, ob = t % NOB_;
+    const f32x4 wa = ring[t % PF];
+    if (t + PF < NT) ring[t % PF] = w[(t + PF) * 64 + lane];
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++) acc[ob][cb] = mfma4(wa[s], bfrag(kb, s, cb), acc[ob][cb]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // v_mfma_f32_16x16x4f32 lane layout: A[i][k] in lane i + 16 k, B[k][j] in
 // lane j + 16 k, D[i][j] in lane j + 16 (i / 4), register i % 4.
 // Layer l computes H_l^T = tanh(W_l H_{l-1}^T + b_l): rows are neurons, columns
-// worlds. For the next layer, k-step s of input block hb uses register s of
-// the previous output tile, i.e. lane j + 16 g supplies neuron 16 hb + 4 g + s
+// worlds. For the next layer, k-step s of input block kb uses register s of
+// the previous output tile, i.e. lane j + 16 g supplies neuron 16 kb + 4 g + s
 // of world j; the host lays W out to match (phz_host.cpp, policy_fragments).
 template <class P, class T> __device__ __forceinline__ void policy_wave(const PolicyArgs& a, float* lds) {
-  constexpr int NI = P::NI, NO = P::NO, CB = P::CB, NHB = P::NHB, NOB = P::NOB, KS1 = P::KS1, NPD = P::NPD;
+  constexpr int NI = P::NI, NO = P::NO, CB = P::CB, NHB = P::NHB, NOB = P::NOB, KU = P::KU, NPD = P::NPD;
   constexpr int WPW = 16 * CB;     // worlds per wave
-  constexpr int XS = 4 * KS1 + 1;  // LDS row stride of the input tile (floats)
+  constexpr int XS = 16 * KU + 1;  // LDS row stride of the input tile (floats)
   constexpr int MS = 16 * NOB + 1; // LDS row stride of the output tile
   const int lane = threadIdx.x & 63;
   const int w0 = blockIdx.x * WPW;
@@ -248,7 +309,7 @@ template <class P, class T> __device__ __forceinline__ void policy_wave(const Po
   if (lane < WPW) {
     if (own) rs = a.rng[my];
 #pragma unroll
-    for (int i = 0; i < 4 * KS1; i++) {
+    for (int i = 0; i < 16 * KU; i++) {
       float x = 0.0f;
       if (i < NI && own) {
         x = a.obs[(size_t)i * S + my];
@@ -263,86 +324,21 @@ template <class P, class T> __device__ __forceinline__ void policy_wave(const Po
   __syncthreads();
 
   const int r = lane & 15, g = lane >> 4;
-  // Layer 1: [NHB x CB] tiles, K = inputs in steps of 4.
+  // Layer 1: B = the input tile in LDS; k-step s of input group u is inputs
+  // 16 u + 4 s + g in lane group g.
   f32x4 h[NHB][CB];
-#pragma unroll
-  for (int hb = 0; hb < NHB; hb++) {
-    f32x4 b0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) b0[j] = a.bias[hb * 16 + 4 * g + j];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) h[hb][cb] = b0;
-  }
-  // One k-step per iteration (not unrolled): at 128 inputs a fully unrolled
-  // loop lets the scheduler hoist hundreds of weight loads and spill.
-#pragma unroll 1
-  for (int s = 0; s < KS1; s++) {
-    float xb[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) xb[cb] = lds[(cb * 16 + r) * XS + 4 * s + g];
-#pragma unroll
-    for (int hb = 0; hb < NHB; hb++) {
-      const float wa = a.w1[(hb * KS1 + s) * 64 + lane];
-#pragma unroll
-      for (int cb = 0; cb < CB; cb++) h[hb][cb] = mfma4(wa, xb[cb], h[hb][cb]);
-    }
-  }
-#pragma unroll
-  for (int hb = 0; hb < NHB; hb++)
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) h[hb][cb][j] = tanhf(h[hb][cb][j]);
-
-  // Layer 2.
+  bias_tiles<NHB, CB>(a.bias, g, h);
+  mfma_layer<KU, NHB, CB>(a.w1, lane, h, [&](int kb, int s, int cb) { return lds[(cb * 16 + r) * XS + 16 * kb + 4 * s + g]; });
+  tanh_tiles<NHB, CB>(h);
+  // Layer 2: B = layer 1's output tiles, straight from registers.
   f32x4 h2[NHB][CB];
-#pragma unroll
-  for (int hb = 0; hb < NHB; hb++) {
-    f32x4 b0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) b0[j] = a.bias[16 * NHB + hb * 16 + 4 * g + j];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) h2[hb][cb] = b0;
-  }
-#pragma unroll
-  for (int kb = 0; kb < NHB; kb++) {
-#pragma unroll
-    for (int hb = 0; hb < NHB; hb++) {
-      const f32x4 wa = a.w2[(hb * NHB + kb) * 64 + lane];
-#pragma unroll
-      for (int s = 0; s < 4; s++)
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) h2[hb][cb] = mfma4(wa[s], h[kb][cb][s], h2[hb][cb]);
-    }
-  }
-#pragma unroll
-  for (int hb = 0; hb < NHB; hb++)
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) h2[hb][cb][j] = tanhf(h2[hb][cb][j]);
-
+  bias_tiles<NHB, CB>(a.bias + 16 * NHB, g, h2);
+  mfma_layer<NHB, NHB, CB>(a.w2, lane, h2, [&](int kb, int s, int cb) { return h[kb][cb][s]; });
+  tanh_tiles<NHB, CB>(h2);
   // Layer 3: the action means.
   f32x4 m[NOB][CB];
-#pragma unroll
-  for (int ob = 0; ob < NOB; ob++) {
-    f32x4 b0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) b0[j] = a.bias[32 * NHB + ob * 16 + 4 * g + j];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) m[ob][cb] = b0;
-  }
-#pragma unroll
-  for (int kb = 0; kb < NHB; kb++) {
-#pragma unroll
-    for (int ob = 0; ob < NOB; ob++) {
-      const f32x4 wa = a.w3[(ob * NHB + kb) * 64 + lane];
-#pragma unroll
-      for (int s = 0; s < 4; s++)
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) m[ob][cb] = mfma4(wa[s], h2[kb][cb][s], m[ob][cb]);
-    }
-  }
+  bias_tiles<NOB, CB>(a.bias + 32 * NHB, g, m);
+  mfma_layer<NHB, NOB, CB>(a.w3, lane, m, [&](int kb, int s, int cb) { return h2[kb][cb][s]; });
   // Means to LDS, world-major, for the per-world epilogue.
   __syncthreads();
 #pragma unroll

@@ -581,7 +581,7 @@ struct PolicyD {
   double rho = 0;
   int nhb() const { return (hidden + 15) / 16; }
   int nob() const { return (n_out + 15) / 16; }
-  int ks1() const { return (n_in + 3) / 4; }
+  int ku() const { return (n_in + 15) / 16; }  // 16-input groups of layer 1
   // Worlds per wave = 16 * cb: as many 16-world column blocks as keep both
   // hidden layers' tiles (2 x nhb x cb x 4 floats per lane) within ~290 registers.
   int cb() const { return std::max(1, std::min(4, 36 / nhb())); }
@@ -589,10 +589,12 @@ struct PolicyD {
     const size_t i = n_in, h = hidden, o = n_out;
     return i * h + h + h * h + h + h * o + o;
   }
-  // Fragment buffer (floats): W1 [nhb][ks1][64], W2 [nhb][nhb][64][4], W3 [nob][nhb][64][4], biases.
-  size_t off_w2() const { return (size_t)nhb() * ks1() * 64; }
+  // Fragment buffer (floats): W1 [ku][nhb][64][4], W2 [nhb][nhb][64][4],
+  // W3 [nhb][nob][64][4] (input block major, the order the kernel streams
+  // them), then the biases.
+  size_t off_w2() const { return (size_t)ku() * nhb() * 256; }
   size_t off_w3() const { return off_w2() + (size_t)nhb() * nhb() * 256; }
-  size_t off_bias() const { return off_w3() + (size_t)nob() * nhb() * 256; }
+  size_t off_bias() const { return off_w3() + (size_t)nhb() * nob() * 256; }
   size_t frag_floats() const { return off_bias() + 16 * (size_t)(2 * nhb() + nob()); }
   bool same_shape(const PolicyD& o) const {
     return n_in == o.n_in && hidden == o.hidden && n_out == o.n_out && history == o.history;
@@ -603,7 +605,7 @@ struct PolicyD {
 // policy_wave in phz_control.h). Input order is the reference's flat
 // W1 b1 W2 b2 W3 b3 with each W row-major [out][in] (policy_pipeline.rs:460-481).
 void policy_fragments(const PolicyD& p, const double* w, std::vector<float>& out) {
-  const int NI = p.n_in, NH = p.hidden, NO = p.n_out, NHB = p.nhb(), NOB = p.nob(), KS1 = p.ks1();
+  const int NI = p.n_in, NH = p.hidden, NO = p.n_out, NHB = p.nhb(), NOB = p.nob(), KU = p.ku();
   const double* W1 = w;
   const double* b1 = W1 + (size_t)NH * NI;
   const double* W2 = b1 + NH;
@@ -611,25 +613,28 @@ void policy_fragments(const PolicyD& p, const double* w, std::vector<float>& out
   const double* W3 = b2 + NH;
   const double* b3 = W3 + (size_t)NO * NH;
   out.assign(p.frag_floats(), 0.0f);
-  for (int hb = 0; hb < NHB; hb++)
-    for (int s = 0; s < KS1; s++)
-      for (int l = 0; l < 64; l++) {
-        const int n = hb * 16 + (l & 15), i = 4 * s + (l >> 4);
-        if (n < NH && i < NI) out[((size_t)hb * KS1 + s) * 64 + l] = (float)W1[(size_t)n * NI + i];
-      }
-  for (int hb = 0; hb < NHB; hb++)
-    for (int kb = 0; kb < NHB; kb++)
+  // Layer 1: component s of fragment (u, hb), lane l = W1[16 hb + l%16][16 u + 4 s + l/16].
+  for (int u = 0; u < KU; u++)
+    for (int hb = 0; hb < NHB; hb++)
+      for (int l = 0; l < 64; l++)
+        for (int s = 0; s < 4; s++) {
+          const int n = hb * 16 + (l & 15), i = 16 * u + 4 * s + (l >> 4);
+          if (n < NH && i < NI) out[(((size_t)u * NHB + hb) * 64 + l) * 4 + s] = (float)W1[(size_t)n * NI + i];
+        }
+  // Layers 2 and 3: component s of fragment (kb, ob), lane l = W[16 ob + l%16][16 kb + 4 (l/16) + s].
+  for (int kb = 0; kb < NHB; kb++)
+    for (int hb = 0; hb < NHB; hb++)
       for (int l = 0; l < 64; l++)
         for (int s = 0; s < 4; s++) {
           const int n2 = hb * 16 + (l & 15), n1 = kb * 16 + 4 * (l >> 4) + s;
-          if (n2 < NH && n1 < NH) out[p.off_w2() + (((size_t)hb * NHB + kb) * 64 + l) * 4 + s] = (float)W2[(size_t)n2 * NH + n1];
+          if (n2 < NH && n1 < NH) out[p.off_w2() + (((size_t)kb * NHB + hb) * 64 + l) * 4 + s] = (float)W2[(size_t)n2 * NH + n1];
         }
-  for (int ob = 0; ob < NOB; ob++)
-    for (int kb = 0; kb < NHB; kb++)
+  for (int kb = 0; kb < NHB; kb++)
+    for (int ob = 0; ob < NOB; ob++)
       for (int l = 0; l < 64; l++)
         for (int s = 0; s < 4; s++) {
           const int k = ob * 16 + (l & 15), n = kb * 16 + 4 * (l >> 4) + s;
-          if (k < NO && n < NH) out[p.off_w3() + (((size_t)ob * NHB + kb) * 64 + l) * 4 + s] = (float)W3[(size_t)k * NH + n];
+          if (k < NO && n < NH) out[p.off_w3() + (((size_t)kb * NOB + ob) * 64 + l) * 4 + s] = (float)W3[(size_t)k * NH + n];
         }
   for (int n = 0; n < NH; n++) {
     out[p.off_bias() + n] = (float)b1[n];
@@ -740,11 +745,11 @@ std::string gen_policy_source(const PolicyD& p, int npd, bool f64) {
   s += "\n";
   s += kControlSrc;
   const int cb = p.cb();
-  const int lds = 16 * cb * std::max(4 * p.ks1() + 1, 16 * p.nob() + 1);
+  const int lds = 16 * cb * std::max(16 * p.ku() + 1, 16 * p.nob() + 1);
   std::ostringstream o;
   o << "\n// ---- policy shape ----\nstruct Pol {\n";
   o << "  static constexpr int NI = " << p.n_in << ", NH = " << p.hidden << ", NO = " << p.n_out << ", NHB = " << p.nhb()
-    << ", NOB = " << p.nob() << ", KS1 = " << p.ks1() << ", CB = " << cb << ", NPD = " << npd << ", LDS = " << lds << ";\n";
+    << ", NOB = " << p.nob() << ", KU = " << p.ku() << ", CB = " << cb << ", NPD = " << npd << ", LDS = " << lds << ";\n";
   o << "  static constexpr double rho = " << num(p.rho) << ";\n";
   o << "  static constexpr double noise[" << p.n_in << "] = " << arr1(p.n_in, [&](int k) { return num(p.noise[k]); }) << ";\n";
   o << "  static constexpr double clamp[" << p.n_out << "] = " << arr1(p.n_out, [&](int k) { return num(p.clamp[k]); }) << ";\n";
@@ -769,7 +774,7 @@ struct ObsArgs {  // must match phz::ObsArgs in phz_control.h
 };
 
 struct PolicyArgs {  // must match phz::PolicyArgs in phz_control.h
-  const float* w1;
+  const void* w1;
   const void* w2;
   const void* w3;
   const float* bias;
@@ -1644,8 +1649,6 @@ int phz_time_rollout(phz_sim* s, uint32_t first_step, uint32_t n_control, uint32
                      uint32_t reps, double* ms_per_rep) {
   if (!s || !ms_per_rep) return 1;
   if (!set_device(s)) return 1;
-  // Build and capture outside the timed region.
-  if (!s->rollout(first_step, n_control, control_every, record_states != 0)) return 1;
   return time_reps(s, reps, ms_per_rep, [&] { return s->rollout(first_step, n_control, control_every, record_states != 0); });
 }
 

@@ -306,3 +306,22 @@ def from_workload(w, precision: str, nworld: Optional[int] = None, device: int =
     if w.noise is not None:
         sim.enable_control_noise(w.noise.seed, w.noise.dist, w.noise.a, w.noise.b, w.noise.dofs)
     return sim
+
+
+def from_control_loop(cl, precision: str = "f32", nworld: Optional[int] = None, device: int = 0) -> BatchSim:
+    """A BatchSim running a phyz_amd.workloads.ControlLoop: contact, PD servos, the
+    policy with its weights, std, base targets and seed, and a state history of
+    one slot per control step."""
+    n = cl.nworld if nworld is None else nworld
+    w = cl.base
+    sim = BatchSim(w.model, n, precision, device)
+    sim.enable_ground_contact(w.contact.ground_height, w.contact.stiffness, w.contact.damping, w.contact.friction)
+    sim.enable_pd_control(cl.pd)
+    sim.enable_policy(cl.spec)
+    if device >= 0:
+        sim.set_policy_weights(cl.weights)
+        sim.set_policy_std(cl.std)
+        sim.set_policy_base_targets(cl.base_targets(n))
+        sim.seed_policy(cl.seed)
+    sim.enable_state_history(cl.spec.history_steps)
+    return sim

@@ -302,3 +302,59 @@ def config(index: int) -> Workload:
 
 
 ALL = (1, 2, 3, 4, 5)
+
+
+# ── control loop: the ant driven by an on-device policy ─────────────────────
+@dataclasses.dataclass
+class ControlLoop:
+    """An RL collector's rollout on the ant (workload 3's model and contact, no
+    control-noise torques): every `control_every` physics steps, FK, a 29-feature
+    observation row, a 29-256-256-8 tanh MLP with an AR(1) Gaussian sample, and
+    the clamped actions onto hip/knee PD targets; the state is recorded after
+    each control step (docs/design/cuda-backend.md section 7 of the reference)."""
+    name: str
+    base: Workload
+    pd: List[PdDof]
+    spec: object
+    weights: np.ndarray
+    std: np.ndarray
+    seed: int
+    n_control: int
+    control_every: int
+
+    @property
+    def nworld(self) -> int:
+        return self.base.nworld
+
+    def base_targets(self, n: Optional[int] = None) -> np.ndarray:
+        """Standing pose: hips 0, knees 0.5 rad, every world."""
+        n = self.nworld if n is None else n
+        row = np.array([0.0, 0.5] * 4)
+        return np.tile(row, (n, 1))
+
+    def flops_per_world(self) -> int:
+        """MLP multiply-adds x 2 per world and control step (biases, tanh and the
+        sample not counted)."""
+        i, h, o = self.spec.n_in(), self.spec.hidden, self.spec.n_out()
+        return 2 * (i * h + h * h + h * o)
+
+
+def control_loop(hidden: int = 256) -> ControlLoop:
+    from .policy import BodyPitch, BodyPos, BodyPosZ, BodyRoll, BodyYawError, ComOverSupport, PolicySpec, QMinus, V
+    base = config(3)
+    m = base.model
+    base = dataclasses.replace(base, name="ant_control", noise=None)
+    pd = [PdDof(6 + k, 6 + k, 20.0, 1.0, 10.0) for k in range(8)]
+    feet = [(2 + 2 * k, [0.0, 0.0, 0.0]) for k in range(4)]
+    obs = ([BodyPitch(0), BodyRoll(0), BodyYawError(0, 0.0), BodyPosZ(0), BodyPos(0, 0)]
+           + [QMinus(6 + k, 0.5 if k % 2 else 0.0) for k in range(8)] + [V(j) for j in range(14)]
+           + [ComOverSupport(feet, 0, 0), ComOverSupport(feet, 0, 1)])
+    spec = PolicySpec(obs=obs, hidden=hidden, act_slots=list(range(8)), act_clamp=0.5, noise_rho=0.5,
+                      input_noise=[0.01] * len(obs), history_steps=50)
+    rng = np.random.default_rng(0xC0)
+    n_in, h, n_out = spec.n_in(), hidden, spec.n_out()
+    weights = np.concatenate([rng.normal(size=h * n_in) / math.sqrt(n_in), np.zeros(h),
+                              rng.normal(size=h * h) / math.sqrt(h), np.zeros(h),
+                              0.1 * rng.normal(size=n_out * h) / math.sqrt(h), np.zeros(n_out)])
+    return ControlLoop("ant_control", base, pd, spec, weights, np.full(n_out, 0.2), seed=0xC0DE,
+                       n_control=50, control_every=5)
