@@ -56,7 +56,9 @@ def lib():
         L.orc_world_seed.restype = C.c_uint64
         L.orc_world_seed.argtypes = [C.c_uint64, C.c_uint64]
         L.orc_quat_exp_log.argtypes = [dp, dp, dp]
-        L.orc_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, dp, dp, dp, u64p, dp, dp, C.c_int, C.c_int]
+        L.orc_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, dp, dp, dp, u64p, dp, dp, C.c_int, C.c_int, dp, dp]
+        L.orc_set_contact_cfg.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, C.c_int, dp, C.c_int, C.c_int, dp, dp]
+        L.orc_contact_pass.argtypes = [C.c_void_p, dp, dp, dp, dp, dp]
         L.orc_count_ops.argtypes = [C.c_void_p, dp, dp, dp, dp, C.c_uint64, C.c_int, u64p]
         _lib = L
     return _lib
@@ -76,8 +78,12 @@ COUNTERS = ("add", "mul", "div", "sqrt", "trans", "other")
 class Oracle:
     """f64 CPU restatement of one model's step (see oracle/phz_oracle.hpp)."""
 
-    def __init__(self, model=None, contact=None, pd=None, noise=None, tables=None):
-        """From a phyz_amd.model.Model, or from raw tables=(body_table, nq, nv, gravity, dt)."""
+    def __init__(self, model=None, contact=None, pd=None, noise=None, tables=None, contact_cfg=None):
+        """From a phyz_amd.model.Model, or from raw tables=(body_table, nq, nv, gravity, dt).
+
+        contact = (geometry table, ground height, friction); contact_cfg (a
+        ContactCfg) adds impulse mode, the body-attached plane and heightfield
+        terrain to it."""
         L = lib()
         if tables is not None:
             table, nq, nv, gravity, dt = tables
@@ -109,6 +115,9 @@ class Oracle:
             arr = (C.c_int * len(dofs))(*dofs)
             L.orc_set_noise(self._h, int(seed), int(dist), float(a), float(b), arr, len(dofs))
             self.noise = noise
+        self.cfg = contact_cfg
+        if contact_cfg is not None:
+            contact_cfg.apply(L, self._h)
 
     def __del__(self):
         if getattr(self, "_h", None) is not None and _lib is not None:
@@ -187,8 +196,21 @@ class Oracle:
         seed = int(self.noise[0])
         return np.array([lib().orc_world_seed(seed, w) for w in range(nworld)], dtype=np.uint64)
 
-    def step_batch(self, q, v, ctrl, nsteps, targets=None, rng=None, threads=1, dense=False, want_contacts=False):
-        """Advance world-major (q, v, ctrl) in place by nsteps. Returns (qdd_last, contact_rows|None)."""
+    def contact_pass(self, q, v, cs=None):
+        """One contact pass at velocity v (the free velocity in impulse mode).
+        cs: nb x 56 solver state, updated in place. Returns (ext, rows)."""
+        ext = np.zeros((self.nb, 6))
+        rows = np.zeros((self.nb, 8))
+        if cs is not None:
+            assert cs.dtype == np.float64 and cs.flags.c_contiguous and cs.size == self.nb * 56
+        lib().orc_contact_pass(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)),
+                               _d(np.ascontiguousarray(v, dtype=np.float64)), _d(ext), _d(cs), _d(rows))
+        return ext, rows
+
+    def step_batch(self, q, v, ctrl, nsteps, targets=None, rng=None, threads=1, dense=False, want_contacts=False,
+                   ext_state=None, cs_state=None):
+        """Advance world-major (q, v, ctrl) in place by nsteps. Returns (qdd_last, contact_rows|None).
+        ext_state [nworld][nb][6] / cs_state [nworld][nb][56]: impulse-mode solver state, in and out."""
         nworld = q.shape[0]
         assert q.dtype == np.float64 and q.flags.c_contiguous
         qdd = np.zeros((nworld, self.nv))
@@ -200,8 +222,11 @@ class Oracle:
         if rng is not None:
             assert rng.dtype == np.uint64 and rng.flags.c_contiguous
             rp = rng.ctypes.data_as(u64p)
+        for a in (ext_state, cs_state):
+            if a is not None:
+                assert a.dtype == np.float64 and a.flags.c_contiguous
         lib().orc_step_batch(self._h, nworld, int(nsteps), _d(q), _d(v), _d(ctrl), _d(tg), rp, _d(qdd),
-                             _d(rows), int(threads), 1 if dense else 0)
+                             _d(rows), int(threads), 1 if dense else 0, _d(ext_state), _d(cs_state))
         return qdd, rows
 
     def count_ops(self, q, v, ctrl, targets=None, rng_state=1, dense=False):
@@ -224,3 +249,33 @@ def quat_exp_log(w):
     l = np.zeros(3)
     lib().orc_quat_exp_log(_d(np.ascontiguousarray(w, dtype=np.float64)), _d(q), _d(l))
     return q, l
+
+
+class ContactCfg:
+    """Impulse mode, body-attached plane and heightfield terrain for the oracle
+    (ContactParams, crates/phyz-gpu/src/contact_pipeline.rs:17-100; defaults of
+    GroundContactParams::default, 197-222)."""
+
+    def __init__(self, solve_mode=0, sweeps=16, restitution=0.0, restitution_threshold=0.05,
+                 erp=0.001 / (2.0 * 0.02 + 0.001), margin=0.001, solimp=(0.9, 0.95, 0.001, 0.5, 2.0), plane=None,
+                 heightfield=None):
+        """plane: (body, offset, max_depth, half_x, half_y); heightfield: (nx, ny, ox, oy, oz, cell, heights)."""
+        self.solve_mode, self.sweeps = int(solve_mode), int(sweeps)
+        self.prm = np.array([restitution, restitution_threshold, erp, margin, *solimp], dtype=np.float64)
+        self.plane = plane
+        self.heightfield = heightfield
+
+    def apply(self, L, h):
+        pb, pl = -1, np.zeros(4)
+        if self.plane is not None:
+            pb = int(self.plane[0])
+            pl = np.array(self.plane[1:5], dtype=np.float64)
+        nx = ny = 0
+        hf = np.zeros(4)
+        heights = None
+        if self.heightfield is not None:
+            nx, ny, ox, oy, oz, cell, hh = self.heightfield
+            hf = np.array([ox, oy, oz, cell], dtype=np.float64)
+            heights = np.ascontiguousarray(np.asarray(hh, dtype=np.float64).ravel())
+        L.orc_set_contact_cfg(h, self.solve_mode, self.sweeps, _d(self.prm), pb, _d(pl), int(nx), int(ny), _d(hf),
+                              _d(heights))

@@ -42,6 +42,32 @@ int orc_set_contact(orc_model* o, const double* geom, double ground_h, double mu
   o->m.mu = mu;
   return 0;
 }
+// Impulse mode, body-attached plane and heightfield (ContactParams,
+// contact_pipeline.rs:17-100). prm: restitution, restitution_threshold, erp,
+// margin, solimp dmin, dmax, width, midpoint, power. plane: offset, max_depth,
+// half_x, half_y. hf: origin x, y, z, cell; heights [ny][nx] (nullable when
+// hf_nx == 0). Geometry slot 7 carries the per-body plane exclusion.
+int orc_set_contact_cfg(orc_model* o, int solve_mode, int sweeps, const double* prm, int plane_body,
+                        const double* plane, int hf_nx, int hf_ny, const double* hf, const double* heights) {
+  ContactCfg& c = o->m.cc;
+  c.solve_mode = solve_mode;
+  c.sweeps = sweeps;
+  c.restitution = prm[0]; c.restitution_threshold = prm[1]; c.erp = prm[2]; c.margin = prm[3];
+  c.solimp_dmin = prm[4]; c.solimp_dmax = prm[5]; c.solimp_width = prm[6]; c.solimp_mid = prm[7]; c.solimp_power = prm[8];
+  c.plane_body = plane_body;
+  if (plane_body >= 0) {
+    c.plane_offset = plane[0]; c.plane_max_depth = plane[1]; c.plane_half_x = plane[2]; c.plane_half_y = plane[3];
+  }
+  c.hf_nx = hf_nx;
+  c.hf_ny = hf_ny;
+  if (hf_nx > 0) {
+    c.hf_ox = hf[0]; c.hf_oy = hf[1]; c.hf_oz = hf[2]; c.hf_cell = hf[3];
+    c.hf.assign(heights, heights + (size_t)hf_nx * hf_ny);
+  } else {
+    c.hf.clear();
+  }
+  return 0;
+}
 int orc_set_pd(orc_model* o, const double* dofs, int n) {
   o->m.pd.clear();
   for (int i = 0; i < n; i++) {
@@ -134,6 +160,18 @@ int orc_contact(orc_model* o, const double* q, const double* v, double* ext_out,
   for (int i = 0; i < o->m.nb; i++) for (int k = 0; k < 6; k++) ext_out[i * 6 + k] = ext[i].get(k);
   return 0;
 }
+// One contact pass from (q, v) with the solver state cs (nb x 56, read and
+// written; nullable in penalty mode). v is the velocity the pass sees: the
+// free velocity v + dt qdd in impulse mode.
+int orc_contact_pass(orc_model* o, const double* q, const double* v, double* ext_out, double* cs, double* rows_out) {
+  if (!o->m.contact) return 1;
+  std::vector<FK<double>> fk(o->m.nb);
+  std::vector<SV<double>> ext(o->m.nb);
+  forward_kinematics<double>(o->m, q, v, fk.data());
+  contact_pass<double>(o->m, fk.data(), ext.data(), cs, rows_out);
+  for (int i = 0; i < o->m.nb; i++) for (int k = 0; k < 6; k++) ext_out[i * 6 + k] = ext[i].get(k);
+  return 0;
+}
 int orc_integrate(orc_model* o, double* q, double* v, const double* qdd) {
   integrate<double>(o->m, q, v, qdd);
   return 0;
@@ -152,8 +190,11 @@ int orc_quat_exp_log(const double* w, double* quat_out, double* log_out) {
 // (nullable when noise is off). targets: [nworld][n_pd]. qdd_last:
 // [nworld][nv] (nullable). contact_rows: [nworld][nb][8] of the last step
 // (nullable). threads <= 0 uses hardware concurrency. mode 0 struct, 1 dense.
+// ext_state [nworld][nb][6] and cs_state [nworld][nb][56]: impulse-mode solver
+// state carried from step to step (nullable: start from zero, not returned).
 int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, double* ctrl, const double* targets,
-                   uint64_t* rng, double* qdd_last, double* contact_rows, int threads, int mode) {
+                   uint64_t* rng, double* qdd_last, double* contact_rows, int threads, int mode, double* ext_state,
+                   double* cs_state) {
   const Model& m = o->m;
   if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
   threads = std::min(threads, std::max(1, nworld));
@@ -167,10 +208,17 @@ int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, d
       double* cw = ctrl + (size_t)w * m.nv;
       const double* tw = npd ? targets + (size_t)w * npd : nullptr;
       uint64_t* rw = rng ? rng + w : nullptr;
+      ws.reset(m);
+      double* ew = ext_state ? ext_state + (size_t)w * m.nb * 6 : nullptr;
+      double* sw = cs_state ? cs_state + (size_t)w * m.nb * CS_STRIDE : nullptr;
+      if (ew) for (int i = 0; i < m.nb; i++) for (int k = 0; k < 6; k++) ws.ext[i].set(k, ew[i * 6 + k]);
+      if (sw) std::memcpy(ws.cs.data(), sw, sizeof(double) * m.nb * CS_STRIDE);
       for (int s = 0; s < nsteps; s++) {
         double* cr = (contact_rows && s == nsteps - 1) ? contact_rows + (size_t)w * m.nb * CONTACT_ROW : nullptr;
         step_world<double>(m, qw, vw, cw, tw, rw, ws, cr, mode == 1);
       }
+      if (ew) for (int i = 0; i < m.nb; i++) for (int k = 0; k < 6; k++) ew[i * 6 + k] = ws.ext[i].get(k);
+      if (sw) std::memcpy(sw, ws.cs.data(), sizeof(double) * m.nb * CS_STRIDE);
       if (qdd_last && nsteps > 0) std::memcpy(qdd_last + (size_t)w * m.nv, ws.qdd.data(), sizeof(double) * m.nv);
     }
   };
@@ -202,8 +250,8 @@ int orc_count_ops(orc_model* o, const double* q0, const double* v0, const double
   OpCount last;
   auto hook = [&](int phase) {
     uint64_t* out = counts + phase * 6;
-    out[0] = c.add - last.add; out[1] = c.mul - last.mul; out[2] = c.div - last.div;
-    out[3] = c.sqrt - last.sqrt; out[4] = c.trans - last.trans; out[5] = c.other - last.other;
+    out[0] += c.add - last.add; out[1] += c.mul - last.mul; out[2] += c.div - last.div;
+    out[3] += c.sqrt - last.sqrt; out[4] += c.trans - last.trans; out[5] += c.other - last.other;
     last = c;
   };
   WorldScratch<OpScalar> ws;

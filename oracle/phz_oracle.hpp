@@ -392,9 +392,28 @@ struct Body {
 struct Geom {
   int type;
   double p[6];            // [1..7): shape parameters / mesh AABB
+  bool skip_plane;        // [7]: never contacts the body-attached plane
   double k, d;            // per-body penalty gains
   double o_pos[3], o_rot[9];
 };
+// Contact configuration beyond the flat-ground penalty law: the fields of
+// ContactParams (crates/phyz-gpu/src/contact_pipeline.rs:17-100) with the
+// defaults of GroundContactParams::default (197-222).
+struct ContactCfg {
+  int solve_mode = 0;  // 0 penalty, 1 velocity-level impulse solve
+  int sweeps = 16;     // [contact, ABA] sweeps per step in impulse mode (DEFAULT_CONTACT_SWEEPS)
+  double restitution = 0.0, restitution_threshold = 0.05;
+  double erp = 0.001 / (2.0 * 0.02 + 0.001), margin = 0.001;
+  double solimp_dmin = 0.9, solimp_dmax = 0.95, solimp_width = 0.001, solimp_mid = 0.5, solimp_power = 2.0;
+  int plane_body = -1;  // body-attached contact plane (contact_pipeline.rs:300-353)
+  double plane_offset = 0.0, plane_max_depth = 0.0, plane_half_x = 0.0, plane_half_y = 0.0;
+  int hf_nx = 0, hf_ny = 0;  // heightfield terrain; nx == 0 is the flat plane at ground_h
+  double hf_ox = 0.0, hf_oy = 0.0, hf_oz = 0.0, hf_cell = 1.0;
+  std::vector<double> hf;  // heights[iy * nx + ix]
+};
+constexpr int CS_STRIDE = 56;      // contact state per body: 8 readback + 24 ground + 24 plane impulses
+constexpr int CS_IMPULSE_OFF = 8;
+constexpr int CS_PLANE_OFF = 32;
 struct PdDof { int q_index, v_index; double kp, kd, max_force; };
 enum NoiseDist { NOISE_NORMAL = 0, NOISE_UNIFORM = 1 };
 
@@ -407,6 +426,7 @@ struct Model {
   bool contact = false;
   double ground_h = 0.0, mu = 0.0;
   std::vector<Geom> geoms;
+  ContactCfg cc;
   // PD servos
   std::vector<PdDof> pd;
   // per-step control noise (the synthetic torque stream of the benchmark workloads)
@@ -449,6 +469,7 @@ inline void geoms_from_table(Model& m, const double* t) {
     Geom& g = m.geoms[i];
     g.type = (int)r[0];
     for (int k = 0; k < 6; k++) g.p[k] = r[1 + k];
+    g.skip_plane = r[7] != 0.0;
     g.k = r[8]; g.d = r[9];
     for (int k = 0; k < 3; k++) g.o_pos[k] = r[10 + k];
     for (int k = 0; k < 9; k++) g.o_rot[k] = r[13 + k];
@@ -1061,32 +1082,168 @@ template <class S> V3<S> box_corner(const Geom& g, int c) {
   return cv3<S>(g.o_pos) + tmul(cm3<S>(g.o_rot), corner);
 }
 
-// Per-body contact readback row: touching, deepest penetration, point (x, y, h),
-// summed world force (layout.rs:68-81 slots 0..8).
-template <class S> void ground_contact(const Model& m, const FK<S>* fk, SV<S>* ext, S* rows /* nb x 8, nullable */) {
-  const double dt = m.dt;
-  for (int i = 0; i < m.nb; i++) {
-    ext[i] = SV<S>();
+template <class S> inline S s_pow(const S& x, double p) {
+  if constexpr (std::is_same<S, OpScalar>::value) {
+    if (x.k) return OpScalar(std::pow(x.v, p));
+    count_trans();
+    return OpScalar::state(std::pow(x.v, p));
+  } else return S(std::pow(x, S(p)));
+}
+template <class S> V3<S> normalize3(const V3<S>& a) {
+  S l = norm(a);
+  return l > S(0.0) ? a * (S(1.0) / l) : a;
+}
+
+// Terrain height and unit normal at world (x, y): the flat plane at ground_h,
+// or the bilinear heightfield with its cell-wise gradient (phyz_kernels.cu:641-664;
+// crates/phyz-model/src/heightfield.rs).
+template <class S> S terrain(const Model& m, const S& px, const S& py, V3<S>& n_out) {
+  const ContactCfg& c = m.cc;
+  if (c.hf_nx == 0) { n_out = V3<S>{S(0.0), S(0.0), S(1.0)}; return S(m.ground_h); }
+  auto locate = [&](const S& w, double o, int n, int& i, S& t) {
+    if (n < 2) { i = 0; t = S(0.0); return; }
+    S u = s_clamp((w - S(o)) / S(c.hf_cell), S(0.0), S(double(n - 1)));
+    int ii = (int)s_val(u);
+    if (ii > n - 2) ii = n - 2;
+    i = ii;
+    t = u - S(double(ii));
+  };
+  int ix, iy;
+  S tx, ty;
+  locate(px, c.hf_ox, c.hf_nx, ix, tx);
+  locate(py, c.hf_oy, c.hf_ny, iy, ty);
+  const int ix1 = std::min(ix + 1, c.hf_nx - 1), iy1 = std::min(iy + 1, c.hf_ny - 1);
+  auto node = [&](int x, int y) { return S(c.hf_oz + c.hf[(size_t)y * c.hf_nx + x]); };
+  const S h00 = node(ix, iy), h10 = node(ix1, iy), h01 = node(ix, iy1), h11 = node(ix1, iy1);
+  const S one(1.0);
+  S h = (h00 * (one - tx) + h10 * tx) * (one - ty) + (h01 * (one - tx) + h11 * tx) * ty;
+  S dhdx(0.0), dhdy(0.0);
+  const double span_x = double(c.hf_nx - 1) * c.hf_cell, span_y = double(c.hf_ny - 1) * c.hf_cell;
+  if (c.hf_nx >= 2 && s_val(px) >= c.hf_ox && s_val(px) <= c.hf_ox + span_x)
+    dhdx = ((h10 - h00) * (one - ty) + (h11 - h01) * ty) / S(c.hf_cell);
+  if (c.hf_ny >= 2 && s_val(py) >= c.hf_oy && s_val(py) <= c.hf_oy + span_y)
+    dhdy = ((h01 - h00) * (one - tx) + (h11 - h10) * tx) / S(c.hf_cell);
+  n_out = normalize3(V3<S>{-dhdx, -dhdy, one});
+  return h;
+}
+
+// SolImp impedance and its margin taper, smoothstep restitution, contact
+// tangents (phyz_kernels.cu:581-633; phyz_contact's material and cone frame).
+template <class S> S solimp_impedance(const ContactCfg& c, const S& r) {
+  const double dmin = std::clamp(c.solimp_dmin, 1e-4, 1.0 - 1e-9), dmax = std::clamp(c.solimp_dmax, 1e-4, 1.0 - 1e-9);
+  if (c.solimp_width <= 0.0) return S(dmax);
+  S x = s_clamp(s_abs(r) / S(c.solimp_width), S(0.0), S(1.0));
+  const double mid = std::clamp(c.solimp_mid, 1e-6, 1.0 - 1e-6), pw = std::max(c.solimp_power, 1.0);
+  S y = x <= S(mid) ? s_pow(x, pw) / S(std::pow(mid, pw - 1.0))
+                    : S(1.0) - s_pow(S(1.0) - x, pw) / S(std::pow(1.0 - mid, pw - 1.0));
+  return S(dmin) + y * S(dmax - dmin);
+}
+template <class S> S impedance_at(const ContactCfg& c, const S& depth) {
+  if (depth >= S(0.0)) return solimp_impedance(c, depth);
+  S gap = -depth;
+  if (c.margin <= 0.0 || gap >= S(c.margin)) return S(0.0);
+  S sc = S(1.0) - gap / S(c.margin);
+  return sc * sc * (S(3.0) - S(2.0) * sc) * solimp_impedance(c, S(0.0));
+}
+template <class S> S effective_restitution(const ContactCfg& c, double e, const S& approach) {
+  const double vr = c.restitution_threshold;
+  if (vr <= 0.0) return S(e);
+  S sp = s_abs(approach);
+  if (sp <= S(vr)) return S(0.0);
+  if (sp >= S(2.0 * vr)) return S(e);
+  S t = (sp - S(vr)) / S(vr);
+  return S(e) * t * t * (S(3.0) - S(2.0) * t);
+}
+template <class S> void contact_tangents(const V3<S>& n, V3<S>& u, V3<S>& w) {
+  V3<S> a{S(1.0), S(0.0), S(0.0)};
+  if (s_abs(n.x) > S(0.9)) a = V3<S>{S(0.0), S(1.0), S(0.0)};
+  u = normalize3(cross(n, a));
+  w = cross(n, u);
+}
+
+// One contact pass over a world (phyz_kernels.cu:804-1132): ground or terrain
+// contacts per body, then the body-attached plane. Penalty mode applies the
+// bounded Kelvin-Voigt law; impulse mode makes one warm-started Coulomb update
+// per contact slot, from the velocities in `fk` (the free velocity v + dt qdd).
+// ext is overwritten (body-frame spatial forces). cs (nb x 56: readback row,
+// ground impulses, plane impulses) is read and written in impulse mode and may
+// be null in penalty mode; rows (nb x 8) receives the readback rows.
+template <class S> void contact_pass(const Model& m, const FK<S>* fk, SV<S>* ext, S* cs, S* rows) {
+  const ContactCfg& c = m.cc;
+  const bool imp = c.solve_mode == 1;
+  const double dt = m.dt, dtc = std::max(dt, 1e-9);
+  for (int i = 0; i < m.nb; i++) ext[i] = SV<S>();
+  auto zero_body = [&](int i) {
+    if (cs) for (int k = 0; k < CS_STRIDE; k++) cs[i * CS_STRIDE + k] = S(0.0);
     if (rows) for (int k = 0; k < CONTACT_ROW; k++) rows[i * CONTACT_ROW + k] = S(0.0);
+  };
+  for (int i = 0; i < m.nb; i++) {
     const Geom& g = m.geoms[i];
-    if (g.type == G_NONE) continue;
+    if (g.type == G_NONE) { zero_body(i); continue; }
     const Body& b = m.bodies[i];
     const M3<S>& R = fk[i].w_rot;
     V3<S> z_body{R.m[2][0], R.m[2][1], R.m[2][2]};  // R^T z
-    int npts = g.type == G_BOX ? 8 : 1;
-    double pt_scale = g.type == G_BOX ? 0.25 : 1.0;
-    V3<S> f_total;
-    S deepest = S(0.0);
-    V3<S> deepest_w;
+    const int npts = g.type == G_BOX ? 8 : 1;
+    const double pt_scale = g.type == G_BOX ? 0.25 : 1.0;
+    auto point = [&](int cp) { return g.type == G_BOX ? box_corner<S>(g, cp) : support_point<S>(g, z_body); };
+    int n_active = 0;
+    if (imp) {
+      for (int cq = 0; cq < npts; cq++) {
+        V3<S> sq_w = fk[i].w_pos + R * point(cq);
+        V3<S> tn;
+        S th = terrain(m, sq_w.x, sq_w.y, tn);
+        if (tn.z * (th - sq_w.z) > S(-c.margin)) n_active++;
+      }
+      if (n_active < 1) n_active = 1;
+    }
+    V3<S> f_total, deepest_w;
+    S deepest(0.0);
     bool any = false;
     for (int cp = 0; cp < npts; cp++) {
-      V3<S> sup = g.type == G_BOX ? box_corner<S>(g, cp) : support_point<S>(g, z_body);
+      V3<S> sup = point(cp);
       V3<S> sup_w = fk[i].w_pos + R * sup;
-      S pen = S(m.ground_h) - sup_w.z;
-      if (!(pen > S(0.0))) continue;
-      const V3<S>& n_body = z_body;
+      V3<S> n_w;
+      S terr_h = terrain(m, sup_w.x, sup_w.y, n_w);
+      S pen = n_w.z * (terr_h - sup_w.z);
+      const bool in = imp ? pen > S(-c.margin) : pen > S(0.0);
+      if (!in) {
+        if (imp && cs) for (int k = 0; k < 3; k++) cs[i * CS_STRIDE + CS_IMPULSE_OFF + cp * 3 + k] = S(0.0);
+        continue;
+      }
+      V3<S> n_body = tmul(R, n_w);
       V3<S> v_pt = fk[i].vel.lin + cross(fk[i].vel.ang, sup);
       S v_n = dot(v_pt, n_body);
+      if (imp) {
+        S* slot = cs + i * CS_STRIDE + CS_IMPULSE_OFF + cp * 3;
+        V3<S> tu, tw;
+        contact_tangents(n_body, tu, tw);
+        S b_u = dot(v_pt, tu), b_w = dot(v_pt, tw);
+        S m_n = contact_eff_mass<S>(b, sup, n_body) / S(double(n_active));
+        S a_nn = S(1.0) / s_max(m_n, S(1e-9));
+        S bias = impedance_at(c, pen) * S(c.erp) * s_max(pen, S(0.0)) / S(dtc);
+        S e = effective_restitution(c, c.restitution, s_min(v_n, S(0.0)));
+        S r_n = v_n * (S(1.0) + e) - a_nn * slot[0];
+        S fn = s_max((bias - r_n) / a_nn, S(0.0));
+        S a_uu = S(double(n_active)) / s_max(contact_eff_mass<S>(b, sup, tu), S(1e-9));
+        S a_ww = S(double(n_active)) / s_max(contact_eff_mass<S>(b, sup, tw), S(1e-9));
+        S ftu = -(b_u - a_uu * slot[1]) / a_uu;
+        S ftw = -(b_w - a_ww * slot[2]) / a_ww;
+        S limit = S(m.mu) * fn;
+        S tn = s_sqrt(ftu * ftu + ftw * ftw);
+        if (tn > limit) {
+          S scl = tn > S(0.0) ? limit / tn : S(0.0);
+          ftu = ftu * scl;
+          ftw = ftw * scl;
+        }
+        slot[0] = fn; slot[1] = ftu; slot[2] = ftw;
+        V3<S> fb = (n_body * fn + tu * ftu + tw * ftw) * (S(1.0) / S(dtc));
+        ext[i].ang = ext[i].ang + cross(sup, fb);
+        ext[i].lin = ext[i].lin + fb;
+        f_total = f_total + R * fb;
+        any = true;
+        if (pen > deepest) { deepest = pen; deepest_w = sup_w; }
+        continue;
+      }
       S m_n = contact_eff_mass<S>(b, sup, n_body);
       S k_b = s_min(S(pt_scale * g.k), max_stiffness(m_n, dt));
       S d_b = s_min(S(pt_scale * g.d), max_damping(m_n, dt));
@@ -1104,15 +1261,123 @@ template <class S> void ground_contact(const Model& m, const FK<S>* fk, SV<S>* e
       ext[i].lin = ext[i].lin + fb;
       f_total = f_total + R * fb;
       any = true;
-      if (pen > deepest) { deepest = pen; deepest_w = V3<S>{sup_w.x, sup_w.y, S(m.ground_h)}; }
+      if (pen > deepest) { deepest = pen; deepest_w = V3<S>{sup_w.x, sup_w.y, terr_h}; }
     }
-    if (any && rows) {
-      S* r = rows + i * CONTACT_ROW;
-      r[0] = S(1.0); r[1] = deepest;
-      r[2] = deepest_w.x; r[3] = deepest_w.y; r[4] = deepest_w.z;
-      r[5] = f_total.x; r[6] = f_total.y; r[7] = f_total.z;
+    if (!any) { zero_body(i); continue; }
+    S row[CONTACT_ROW] = {S(1.0), deepest, deepest_w.x, deepest_w.y, deepest_w.z, f_total.x, f_total.y, f_total.z};
+    for (int k = 0; k < CONTACT_ROW; k++) {
+      if (cs) cs[i * CS_STRIDE + k] = row[k];
+      if (rows) rows[i * CONTACT_ROW + k] = row[k];
     }
   }
+
+  // Body-attached plane: the plane body's local +Z face at plane_offset,
+  // acting on every other collidable body not excluded, forces on both.
+  if (c.plane_body < 0) return;
+  const int pb = c.plane_body;
+  const M3<S>& Rp = fk[pb].w_rot;
+  const V3<S> Pp = fk[pb].w_pos;
+  const V3<S> n_w = Rp * V3<S>{S(0.0), S(0.0), S(1.0)};
+  const V3<S> p0_w = Pp + Rp * V3<S>{S(0.0), S(0.0), S(c.plane_offset)};
+  const Body& bp = m.bodies[pb];
+  for (int i = 0; i < m.nb; i++) {
+    if (i == pb) continue;
+    const Geom& g = m.geoms[i];
+    if (g.type == G_NONE || g.skip_plane) continue;
+    const Body& b = m.bodies[i];
+    const M3<S>& R = fk[i].w_rot;
+    const V3<S> n_body = tmul(R, n_w);
+    const int npts = g.type == G_BOX ? 8 : 1;
+    const double pt_scale = g.type == G_BOX ? 0.25 : 1.0;
+    auto point = [&](int cp) { return g.type == G_BOX ? box_corner<S>(g, cp) : support_point<S>(g, n_body); };
+    S lo_x(1e30), lo_y(1e30), hi_x(-1e30), hi_y(-1e30);
+    for (int cp = 0; cp < npts; cp++) {
+      V3<S> rp = tmul(Rp, fk[i].w_pos + R * point(cp) - Pp);
+      lo_x = s_min(lo_x, rp.x); lo_y = s_min(lo_y, rp.y);
+      hi_x = s_max(hi_x, rp.x); hi_y = s_max(hi_y, rp.y);
+    }
+    const S ov_lo_x = s_max(lo_x, S(-c.plane_half_x)), ov_lo_y = s_max(lo_y, S(-c.plane_half_y));
+    const S ov_hi_x = s_min(hi_x, S(c.plane_half_x)), ov_hi_y = s_min(hi_y, S(c.plane_half_y));
+    if (ov_lo_x > ov_hi_x || ov_lo_y > ov_hi_y) continue;
+    int n_act = 1;
+    if (imp) {
+      int cnt = 0;
+      for (int cq = 0; cq < npts; cq++) {
+        S d = -dot(fk[i].w_pos + R * point(cq) - p0_w, n_w);
+        if (d > S(0.0) && d <= S(c.plane_max_depth)) cnt++;
+      }
+      n_act = cnt > 1 ? cnt : 1;
+    }
+    for (int cp = 0; cp < npts; cp++) {
+      V3<S> sup_w0 = fk[i].w_pos + R * point(cp);
+      S pen = -dot(sup_w0 - p0_w, n_w);
+      if (pen <= S(0.0) || pen > S(c.plane_max_depth)) {
+        if (imp && cs) for (int k = 0; k < 3; k++) cs[i * CS_STRIDE + CS_PLANE_OFF + cp * 3 + k] = S(0.0);
+        continue;
+      }
+      V3<S> r_p = tmul(Rp, sup_w0 - Pp);
+      r_p.x = s_clamp(r_p.x, ov_lo_x, ov_hi_x);
+      r_p.y = s_clamp(r_p.y, ov_lo_y, ov_hi_y);
+      V3<S> sup_w = Pp + Rp * r_p;
+      V3<S> sup_c = tmul(R, sup_w - fk[i].w_pos);
+      V3<S> v_i_w = R * (fk[i].vel.lin + cross(fk[i].vel.ang, sup_c));
+      V3<S> v_p_w = Rp * (fk[pb].vel.lin + cross(fk[pb].vel.ang, r_p));
+      V3<S> v_rel = v_i_w - v_p_w;
+      S v_n = dot(v_rel, n_w);
+      auto series = [&](const V3<S>& d_w) {
+        return S(1.0) / (S(1.0) / contact_eff_mass<S>(b, sup_c, tmul(R, d_w)) +
+                         S(1.0) / contact_eff_mass<S>(bp, r_p, tmul(Rp, d_w)));
+      };
+      S m_n = series(n_w);
+      V3<S> f_w;
+      if (imp) {
+        S* slot = cs + i * CS_STRIDE + CS_PLANE_OFF + cp * 3;
+        V3<S> pu, pw;
+        contact_tangents(n_w, pu, pw);
+        S bu = dot(v_rel, pu), bw = dot(v_rel, pw);
+        S ann = S(double(n_act)) / s_max(m_n, S(1e-9));
+        S bias = impedance_at(c, pen) * S(c.erp) * s_max(pen, S(0.0)) / S(dtc);
+        S ee = effective_restitution(c, c.restitution, s_min(v_n, S(0.0)));
+        S nf = s_max((bias - (v_n * (S(1.0) + ee) - ann * slot[0])) / ann, S(0.0));
+        S auu = S(double(n_act)) / s_max(series(pu), S(1e-9));
+        S aww = S(double(n_act)) / s_max(series(pw), S(1e-9));
+        S ptu = -(bu - auu * slot[1]) / auu;
+        S ptw = -(bw - aww * slot[2]) / aww;
+        S plim = S(m.mu) * nf;
+        S ptn = s_sqrt(ptu * ptu + ptw * ptw);
+        if (ptn > plim) {
+          S psc = ptn > S(0.0) ? plim / ptn : S(0.0);
+          ptu = ptu * psc;
+          ptw = ptw * psc;
+        }
+        slot[0] = nf; slot[1] = ptu; slot[2] = ptw;
+        f_w = (n_w * nf + pu * ptu + pw * ptw) * (S(1.0) / S(dtc));
+      } else {
+        S k_b = s_min(S(pt_scale * g.k), max_stiffness(m_n, dt));
+        S d_b = s_min(S(pt_scale * g.d), max_damping(m_n, dt));
+        S f_n = s_max(k_b * pen - d_b * v_n, S(0.0));
+        V3<S> v_tan = v_rel - n_w * v_n;
+        S vt = norm(v_tan);
+        f_w = n_w * f_n;
+        if (vt > S(1e-6)) {
+          V3<S> t_dir = v_tan * (S(1.0) / vt);
+          S f_t = s_min(S(m.mu) * f_n * s_min(S(1.0), vt / S(1e-3)), max_damping(series(t_dir), dt) * vt);
+          f_w = f_w - t_dir * f_t;
+        }
+      }
+      V3<S> f_i = tmul(R, f_w);
+      ext[i].ang = ext[i].ang + cross(sup_c, f_i);
+      ext[i].lin = ext[i].lin + f_i;
+      V3<S> f_p = tmul(Rp, -f_w);
+      ext[pb].ang = ext[pb].ang + cross(r_p, f_p);
+      ext[pb].lin = ext[pb].lin + f_p;
+    }
+  }
+}
+
+// Penalty-mode contact of one world (no persistent solver state).
+template <class S> void ground_contact(const Model& m, const FK<S>* fk, SV<S>* ext, S* rows /* nb x 8, nullable */) {
+  contact_pass<S>(m, fk, ext, nullptr, rows);
 }
 
 // ─────────────────────────────────────────────────────────────────────────────
@@ -1190,10 +1455,20 @@ template <class S> void noise_apply(const Model& m, uint64_t& s, S* ctrl) {
 // ─────────────────────────────────────────────────────────────────────────────
 template <class S> struct WorldScratch {
   std::vector<FK<S>> fk;
-  std::vector<SV<S>> ext;
+  std::vector<SV<S>> ext;  // impulse mode: persists from step to step (the leading ABA reads it)
   std::vector<S> qdd;
+  std::vector<S> cs;       // impulse mode: nb x 56 contact state with warm-start impulses, persistent
+  std::vector<S> vfree;
+  void reset(const Model& m) {
+    fk.assign(m.nb, FK<S>());
+    ext.assign(m.nb, SV<S>());
+    qdd.assign(m.nv, S(0.0));
+    cs.assign((size_t)m.nb * CS_STRIDE, S(0.0));
+    vfree.assign(m.nv, S(0.0));
+  }
 };
-// Phase hooks let the op counter attribute work to each phase.
+// Phase hooks let the op counter attribute work to each phase; a phase may
+// report more than once per step (impulse sweeps), so counts accumulate.
 struct NoHooks { void operator()(int) const {} };
 enum Phase { PH_NOISE = 0, PH_PD = 1, PH_CONTACT = 2, PH_ABA = 3, PH_INTEGRATE = 4 };
 template <class S, class Hooks = NoHooks>
@@ -1207,19 +1482,36 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
     ctrl[p.v_index] = s_clamp(tau, S(-p.max_force), S(p.max_force));
   }
   hook(PH_PD);
-  ws.qdd.resize(m.nv);
-  const SV<S>* ext = nullptr;
-  if (m.contact) {
-    ws.fk.resize(m.nb);
-    ws.ext.resize(m.nb);
-    forward_kinematics(m, q, v, ws.fk.data());
-    ground_contact(m, ws.fk.data(), ws.ext.data(), contact_rows);
-    ext = ws.ext.data();
+  if (ws.qdd.size() != (size_t)m.nv) ws.reset(m);
+  auto aba = [&](const SV<S>* ext) {
+    if (dense) aba_dense(m, q, v, ctrl, ext, ws.qdd.data());
+    else aba_struct(m, q, v, ctrl, ext, ws.qdd.data());
+  };
+  if (m.contact && m.cc.solve_mode == 1) {
+    // Impulse mode (mod.rs:899-928): a leading ABA with the previous step's
+    // contact forces, then `sweeps` x [contact at the free velocity
+    // v + dt qdd, ABA]; each contact pass warm-starts from the last.
+    aba(ws.ext.data());
+    hook(PH_ABA);
+    for (int sw = 0; sw < m.cc.sweeps; sw++) {
+      for (int k = 0; k < m.nv; k++) ws.vfree[k] = v[k] + S(m.dt) * ws.qdd[k];
+      forward_kinematics(m, q, ws.vfree.data(), ws.fk.data());
+      contact_pass(m, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
+      hook(PH_CONTACT);
+      aba(ws.ext.data());
+      hook(PH_ABA);
+    }
+  } else {
+    const SV<S>* ext = nullptr;
+    if (m.contact) {
+      forward_kinematics(m, q, v, ws.fk.data());
+      contact_pass(m, ws.fk.data(), ws.ext.data(), (S*)nullptr, contact_rows);
+      ext = ws.ext.data();
+    }
+    hook(PH_CONTACT);
+    aba(ext);
+    hook(PH_ABA);
   }
-  hook(PH_CONTACT);
-  if (dense) aba_dense(m, q, v, ctrl, ext, ws.qdd.data());
-  else aba_struct(m, q, v, ctrl, ext, ws.qdd.data());
-  hook(PH_ABA);
   integrate(m, q, v, ws.qdd.data());
   hook(PH_INTEGRATE);
 }

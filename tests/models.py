@@ -118,3 +118,30 @@ def trunk_and_two_feet():
             .add_revolute_body("right_foot", 0, SpatialTransform.from_translation([0.0, -0.12, -0.6]),
                                off(1.5, [-0.03, 0.01, -0.02]))
             .build())
+
+
+def deck_and_feet():
+    """A free box deck on the ground with a free sphere foot and a free box foot
+    standing on it (the skateboard case of contact_pipeline.rs:300-353): plane
+    body 0, face at its local +Z half-thickness."""
+    def box_inertia(m, h):
+        hx, hy, hz = h
+        return SpatialInertia.new(m, np.zeros(3), np.diag([m * (hy * hy + hz * hz) / 3, m * (hx * hx + hz * hz) / 3,
+                                                           m * (hx * hx + hy * hy) / 3]))
+    free = lambda: Joint(FREE, SpatialTransform.identity(), np.zeros(3))
+    return (ModelBuilder().gravity([0, 0, -G]).dt(0.001)
+            .add_body("deck", -1, free(), box_inertia(2.0, (0.4, 0.1, 0.02)), Geometry.box([0.4, 0.1, 0.02]))
+            .add_body("foot_sphere", -1, free(), SpatialInertia.sphere(0.5, 0.05), Geometry.sphere(0.05))
+            .add_body("foot_box", -1, free(), box_inertia(0.4, (0.05, 0.03, 0.02)), Geometry.box([0.05, 0.03, 0.02]))
+            .build())
+
+
+DECK_PLANE = (0, 0.02, 0.05, 0.4, 0.1)  # body, offset, max_depth, half_x, half_y
+
+
+def bumpy_heightfield(nx=9, ny=9, cell=0.25, amp=0.08):
+    """(nx, ny, ox, oy, oz, cell, heights) centred on the origin: smooth bumps."""
+    xs = (np.arange(nx) - (nx - 1) / 2) * cell
+    ys = (np.arange(ny) - (ny - 1) / 2) * cell
+    h = amp * np.sin(2.1 * xs)[None, :] * np.cos(1.7 * ys)[:, None] + 0.03 * ys[:, None]
+    return (nx, ny, float(xs[0]), float(ys[0]), 0.01, cell, np.asarray(h, dtype=np.float32).astype(np.float64))

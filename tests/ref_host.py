@@ -7,7 +7,8 @@ phyz_host_{pd,contact,aba,integrate} (phyz_kernels.cu:1779-1802) walk the grid
 serially. This module packs buffers exactly as crates/phyz-gpu/src/layout.rs
 and crates/phyz-gpu/src/contact_pipeline.rs:60-100 do (f32, integer slots
 bit-cast) and runs the reference step order of
-crates/phyz-gpu/src/cuda/mod.rs:879-945 (PD, contact, ABA, integrate).
+crates/phyz-gpu/src/cuda/mod.rs:879-945 (PD, contact, ABA, integrate; in
+impulse mode PD, ABA, then [contact, ABA] x sweeps, integrate).
 """
 from __future__ import annotations
 
@@ -61,8 +62,22 @@ def pack_bodies_f32(table64: np.ndarray) -> np.ndarray:
     return t
 
 
-def pack_cparams(nworld, nb, nv, ground_h, dt, mu) -> np.ndarray:
-    """ContactParams::pack (contact_pipeline.rs:60-100), penalty mode, flat ground, defaults."""
+def pack_cparams(nworld, nb, nv, ground_h, dt, mu, cfg=None) -> np.ndarray:
+    """ContactParams::pack (contact_pipeline.rs:60-100). Without cfg: penalty mode,
+    flat ground, defaults; cfg (oracle.oracle.ContactCfg) sets the solve mode,
+    solver parameters, body-attached plane and heightfield header."""
+    if cfg is not None:
+        p = pack_cparams(nworld, nb, nv, ground_h, dt, mu)
+        if cfg.plane is not None:
+            p[6] = _bits_i32(int(cfg.plane[0]))
+            p[7:11] = cfg.plane[1:5]
+        if cfg.heightfield is not None:
+            nx, ny, ox, oy, oz, cell, _ = cfg.heightfield
+            p[11], p[12] = _bits_u32(nx), _bits_u32(ny)
+            p[13:17] = [ox, oy, oz, cell]
+        p[17] = _bits_u32(cfg.solve_mode)
+        p[19:28] = cfg.prm
+        return p
     p = np.zeros(32, dtype=np.float32)
     p[0] = _bits_u32(nworld)
     p[1] = _bits_u32(nb)
@@ -85,7 +100,7 @@ def pack_cparams(nworld, nb, nv, ground_h, dt, mu) -> np.ndarray:
 class RefStepper:
     """Reference f32 kernels on the host for `nworld` worlds of one model."""
 
-    def __init__(self, table64, nq, nv, gravity, dt, nworld, geom64=None, ground_h=0.0, mu=0.0, pd64=None):
+    def __init__(self, table64, nq, nv, gravity, dt, nworld, geom64=None, ground_h=0.0, mu=0.0, pd64=None, cfg=None):
         self.L = lib()
         self.nb = table64.shape[0]
         self.nq, self.nv, self.nworld = nq, nv, nworld
@@ -95,12 +110,18 @@ class RefStepper:
         self.contact = geom64 is not None
         if self.contact:
             self.geom = np.ascontiguousarray(np.asarray(geom64, dtype=np.float32).reshape(-1))
-            self.cparams = pack_cparams(nworld, self.nb, nv, ground_h, dt, mu)
+            self.cparams = pack_cparams(nworld, self.nb, nv, ground_h, dt, mu, cfg)
         self.pd = None if pd64 is None else np.ascontiguousarray(np.asarray(pd64, dtype=np.float32).reshape(-1))
         self.npd = 0 if pd64 is None else len(pd64)
         self.ext = np.zeros(nworld * self.nb * 6, dtype=np.float32)
         self.cstate = np.zeros(nworld * self.nb * 56, dtype=np.float32)
         self.hf = np.zeros(1, dtype=np.float32)
+        self.sweeps = 0
+        if cfg is not None:
+            if cfg.heightfield is not None:
+                self.hf = np.ascontiguousarray(np.asarray(cfg.heightfield[6], dtype=np.float32).ravel())
+            if cfg.solve_mode == 1:
+                self.sweeps = cfg.sweeps
         self.qdd = np.zeros(nworld * nv, dtype=np.float32)
 
     @staticmethod
@@ -113,12 +134,26 @@ class RefStepper:
         n = self.nworld
         if self.npd:
             L.phyz_host_pd(n * self.npd, n, self.nq, self.nv, self.npd, P(self.pd), P(q), P(v), P(targets), P(ctrl))
-        if self.contact:
+        g = self.gravity
+
+        def contact():
             L.phyz_host_contact(n, P(self.cparams), P(self.bodies), P(self.geom), P(q), P(v), P(self.ext),
                                 P(self.cstate), P(self.hf), P(self.qdd))
-        g = self.gravity
-        L.phyz_host_aba(n, n, self.nv, self.dt, self.nb, float(g[0]), float(g[1]), float(g[2]), P(self.bodies), P(q),
-                        P(v), P(ctrl), P(self.qdd), P(self.ext))
+
+        def aba():
+            L.phyz_host_aba(n, n, self.nv, self.dt, self.nb, float(g[0]), float(g[1]), float(g[2]), P(self.bodies),
+                            P(q), P(v), P(ctrl), P(self.qdd), P(self.ext))
+
+        if self.contact and self.sweeps > 0:
+            # Impulse mode (mod.rs:899-928): leading ABA, then [contact, ABA] x sweeps.
+            aba()
+            for _ in range(self.sweeps):
+                contact()
+                aba()
+        else:
+            if self.contact:
+                contact()
+            aba()
         L.phyz_host_integrate(n * self.nb, n, self.nv, self.dt, self.nb, P(q), P(v), P(self.qdd), P(self.bodies))
         rows = self.cstate.reshape(n, self.nb, 56)[:, :, :8].copy()
         return self.qdd.reshape(n, self.nv).copy(), self.ext.reshape(n, self.nb, 6).copy(), rows
