@@ -63,6 +63,41 @@ int phz_enable_ground_contact(phz_sim* sim, double ground_height, double stiffne
 /* BatchSim::enable_ground_contact_per_body (mod.rs:630-640): gains nb x 2 (k, d). */
 int phz_enable_ground_contact_per_body(phz_sim* sim, double ground_height, double friction, const double* gains,
                                        const double* geom_table, uint32_t* collidable_out);
+/* BatchSim::enable_ground_contact_with_plane / enable_contact_terrain
+ * (mod.rs:642-680): per-body gains (nb x 2: k, d) over the flat ground or a
+ * heightfield, with an optional body-attached plane.
+ *   plane         NULL, or [body, offset, max_depth, half_x, half_y] (BodyPlane,
+ *                 contact_pipeline.rs:300-353); plane_exclude lists bodies that
+ *                 never touch it (the plane body never does)
+ *   hf, heights   NULL, or [nx, ny, origin x, origin y, origin z, cell] and the
+ *                 ny x nx heights, row-major (phyz_model::Heightfield); the node
+ *                 buffer is sized to this first field
+ * Writes the collidable-body count; errors when it is zero. */
+int phz_enable_contact_terrain(phz_sim* sim, double ground_height, double friction, const double* gains,
+                               const double* geom_table, const double* plane, const uint32_t* plane_exclude,
+                               uint32_t n_exclude, const double* hf, const double* heights, uint32_t* collidable_out);
+/* BatchSim::enable_contact_impulse (mod.rs:680-701): the velocity-level impulse
+ * solve, contact_sweeps x [contact, ABA] per step, warm-started from the last.
+ * Same arguments as phz_enable_contact_terrain, plus solver: NULL for the
+ * reference's values (restitution 0, threshold 0.05, solref erp from
+ * timeconst 0.02 / dampratio 1 at the model's dt, margin 0.001, SolImp
+ * 0.9 / 0.95 / 0.001 / 0.5 / 2), or those 9 numbers in that order (extension). */
+int phz_enable_contact_impulse(phz_sim* sim, double ground_height, double friction, const double* gains,
+                               const double* geom_table, const double* plane, const uint32_t* plane_exclude,
+                               uint32_t n_exclude, const double* hf, const double* heights, const double* solver,
+                               uint32_t* collidable_out);
+/* BatchSim::set_heightfield (mod.rs:743-760): new terrain up to the node count
+ * contact was enabled with. */
+int phz_set_heightfield(phz_sim* sim, const double* hf, const double* heights);
+/* BatchSim::contact_sweeps, a public field (mod.rs:450-451); default 16. */
+int phz_set_contact_sweeps(phz_sim* sim, uint32_t sweeps);
+int phz_contact_sweeps(const phz_sim* sim);
+/* Extensions for checking and checkpointing the contact solver: the whole
+ * contact state, [nworld][nb][56] (layout.rs:68-81: readback row, ground
+ * impulses, plane impulses), and the per-body contact forces [nworld][nb][6]
+ * the next impulse-mode step starts from (ext may be NULL). */
+int phz_readback_contact_state(phz_sim* sim, double* cs, double* ext);
+int phz_load_contact_state(phz_sim* sim, const double* cs, const double* ext);
 /* BatchSim::enable_pd_control (mod.rs:765-786): dofs n x 8 (PD_DOF_STRIDE slots). */
 int phz_enable_pd_control(phz_sim* sim, const double* dofs, uint32_t n);
 /* BatchSim::set_position_targets (mod.rs:789-796): rows [nworld][n]. */

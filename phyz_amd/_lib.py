@@ -48,6 +48,14 @@ SIGNATURES = {
     "phz_compile": (C.c_int, [SIM]),
     "phz_time_step_many": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp]),
     "phz_kernel_info": (C.c_int, [SIM, i64p]),
+    "phz_enable_contact_terrain": (C.c_int, [SIM, C.c_double, C.c_double, dp, dp, dp, u32p, C.c_uint32, dp, dp, u32p]),
+    "phz_enable_contact_impulse": (C.c_int, [SIM, C.c_double, C.c_double, dp, dp, dp, u32p, C.c_uint32, dp, dp, dp,
+                                             u32p]),
+    "phz_set_heightfield": (C.c_int, [SIM, dp, dp]),
+    "phz_set_contact_sweeps": (C.c_int, [SIM, C.c_uint32]),
+    "phz_contact_sweeps": (C.c_int, [SIM]),
+    "phz_readback_contact_state": (C.c_int, [SIM, dp, dp]),
+    "phz_load_contact_state": (C.c_int, [SIM, dp, dp]),
     "phz_enable_kinematics": (C.c_int, [SIM]),
     "phz_compute_kinematics": (C.c_int, [SIM]),
     "phz_readback_kinematics": (C.c_int, [SIM, dp]),

@@ -56,6 +56,8 @@ __device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double dlog(double x) { return log(x); }
 __device__ __forceinline__ float dlog(float x) { return logf(x); }
 __device__ __forceinline__ double datan2(double y, double x) { return atan2(y, x); }
+__device__ __forceinline__ double dpow(double x, double y) { return pow(x, y); }
+__device__ __forceinline__ float dpow(float x, float y) { return powf(x, y); }
 __device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x); }
 template <class T> __device__ __forceinline__ T dmax(T a, T b) { return a > b ? a : b; }
 template <class T> __device__ __forceinline__ T dmin(T a, T b) { return a < b ? a : b; }
@@ -76,6 +78,11 @@ template <class T> __device__ __forceinline__ V3<T> operator*(V3<T> a, T s) { re
 template <class T> __device__ __forceinline__ T dot(V3<T> a, V3<T> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 template <class T> __device__ __forceinline__ V3<T> cross(V3<T> a, V3<T> b) {
   return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+// Component-wise select: a struct-valued ?: can become a select between two
+// stack addresses, which keeps the operands out of registers.
+template <class T> __device__ __forceinline__ V3<T> sel(bool c, V3<T> a, V3<T> b) {
+  return {c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z};
 }
 template <class T> struct SV { V3<T> a, l; };  // [angular; linear]
 template <class T> __device__ __forceinline__ SV<T> operator+(SV<T> x, SV<T> y) { return {x.a + y.a, x.l + y.l}; }
@@ -275,6 +282,11 @@ struct StepArgs {
   const void* targets; // [npd][stride]
   u64* rng;            // [stride]
   void* contact_rows;  // [nb * 8][stride], last step's contact readback
+  void* ext;           // [nb * 6][stride], contact forces carried between steps (impulse mode)
+  void* imp;           // [nb * 48][stride], warm-start impulses: 24 ground, 24 plane per body (impulse mode)
+  const void* hf;      // heightfield nodes [ny][nx] in T
+  double hf_ox, hf_oy, hf_oz, hf_cell;
+  int hf_nx, hf_ny;
   int nworld;
   int stride;
   int nsteps;
@@ -323,13 +335,163 @@ template <class M, class T, int i> __device__ __forceinline__ T eff_mass(V3<T> r
   }
 }
 
+// Heightfield terrain: nodes h[iy * nx + ix] and the header, uniform over a launch.
+template <class T> struct Terrain {
+  const T* h;
+  T ox, oy, oz, cell;
+  int nx, ny;
+};
+
+// Cell and fraction along one axis, clamped to the grid (NaN lands on cell 0).
+template <class T> __device__ __forceinline__ void hf_locate(T w, T o, int n, T cell, int& i, T& t) {
+  if (n < 2) { i = 0; t = T(0); return; }
+  const T u = dmin(dmax((w - o) / cell, T(0)), T(n - 1));
+  int ii = (int)u;
+  ii = ii > n - 2 ? n - 2 : ii;
+  i = ii;
+  t = u - T(ii);
+}
+
+// Terrain height and unit normal at world (x, y): the flat ground, or the
+// bilinear heightfield with its cell-wise gradient (phyz_kernels.cu:641-664).
+template <class M, class T> __device__ __forceinline__ T terrain_at(const Terrain<T>& tr, T px, T py, V3<T>& n) {
+  if constexpr (!M::HAS_HF) {
+    n = v3(T(0), T(0), T(1));
+    return T(M::ground_h);
+  } else {
+    int ix, iy;
+    T tx, ty;
+    hf_locate(px, tr.ox, tr.nx, tr.cell, ix, tx);
+    hf_locate(py, tr.oy, tr.ny, tr.cell, iy, ty);
+    const int ix1 = ix + 1 < tr.nx - 1 ? ix + 1 : tr.nx - 1;
+    const int iy1 = iy + 1 < tr.ny - 1 ? iy + 1 : tr.ny - 1;
+    const T h00 = tr.oz + tr.h[iy * tr.nx + ix], h10 = tr.oz + tr.h[iy * tr.nx + ix1];
+    const T h01 = tr.oz + tr.h[iy1 * tr.nx + ix], h11 = tr.oz + tr.h[iy1 * tr.nx + ix1];
+    const T h = (h00 * (T(1) - tx) + h10 * tx) * (T(1) - ty) + (h01 * (T(1) - tx) + h11 * tx) * ty;
+    T dhdx = T(0), dhdy = T(0);
+    if (tr.nx >= 2 && px >= tr.ox && px <= tr.ox + T(tr.nx - 1) * tr.cell)
+      dhdx = ((h10 - h00) * (T(1) - ty) + (h11 - h01) * ty) / tr.cell;
+    if (tr.ny >= 2 && py >= tr.oy && py <= tr.oy + T(tr.ny - 1) * tr.cell)
+      dhdy = ((h01 - h00) * (T(1) - tx) + (h11 - h10) * tx) / tr.cell;
+    const V3<T> g = v3(-dhdx, -dhdy, T(1));
+    n = g * (T(1) / dsqrt(dot(g, g)));
+    return h;
+  }
+}
+
+// Contact point cp of body i's shape, body frame: a box corner, or the
+// support point against body-frame direction d (phyz_kernels.cu:667-730).
+template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_point(int cp, V3<T> d) {
+  constexpr int gt = M::gtype[i];
+  const R3<T> oR = R3<T>{{T(M::gorot[i][0]), T(M::gorot[i][1]), T(M::gorot[i][2]), T(M::gorot[i][3]), T(M::gorot[i][4]),
+                          T(M::gorot[i][5]), T(M::gorot[i][6]), T(M::gorot[i][7]), T(M::gorot[i][8])}};
+  const V3<T> oP = v3(T(M::gopos[i][0]), T(M::gopos[i][1]), T(M::gopos[i][2]));
+  if constexpr (gt == G_BOX) {
+    V3<T> corner = v3(T(M::gp[i][0] * ((cp & 1) ? 1.0 : -1.0)), T(M::gp[i][1] * ((cp & 2) ? 1.0 : -1.0)),
+                      T(M::gp[i][2] * ((cp & 4) ? 1.0 : -1.0)));
+    return oP + tmul(oR, corner);
+  } else {
+    V3<T> n = mul(oR, d);
+    V3<T> sp;
+    if constexpr (gt == G_SPHERE) {
+      sp = n * T(-M::gp[i][0]);
+    } else if constexpr (gt == G_CAPSULE) {
+      sp = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
+    } else if constexpr (gt == G_CYLINDER) {
+      T rl = dsqrt(n.x * n.x + n.y * n.y);
+      T f = rl > T(1e-6) ? T(M::gp[i][0]) / rl : T(0);
+      sp = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
+    } else {  // mesh AABB
+      sp = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
+              T(0.5 * (M::gp[i][1] + M::gp[i][4])) - T(0.5 * (M::gp[i][4] - M::gp[i][1])) * dsign(n.y),
+              T(0.5 * (M::gp[i][2] + M::gp[i][5])) - T(0.5 * (M::gp[i][5] - M::gp[i][2])) * dsign(n.z));
+    }
+    return oP + tmul(oR, sp);
+  }
+}
+
+// SolImp impedance with the margin taper, smoothstep restitution, and the
+// contact tangent frame (phyz_kernels.cu:581-633), constants from the model.
+template <class M, class T> __device__ __forceinline__ T solimp_pow(T x) {
+  if constexpr (M::c_power == 1.0) return x;
+  else if constexpr (M::c_power == 2.0) return x * x;
+  else if constexpr (M::c_power == 3.0) return x * x * x;
+  else return dpow(x, T(M::c_power));
+}
+// Model constants arrive clamped as SolImp clamps them: c_dmin, c_dmax in
+// [1e-4, 1 - 1e-9], c_mid in [1e-6, 1 - 1e-6], c_power >= 1, and
+// c_mid_pow = mid^(power-1), c_omid_pow = (1-mid)^(power-1).
+template <class M, class T> __device__ __forceinline__ T solimp_at(T r) {
+  if constexpr (M::c_width <= 0.0) {
+    return T(M::c_dmax);
+  } else {
+    const T x = dmin(dmax(dabs(r) / T(M::c_width), T(0)), T(1));
+    const T lo = solimp_pow<M, T>(x) / T(M::c_mid_pow);
+    const T hi = T(1) - solimp_pow<M, T>(T(1) - x) / T(M::c_omid_pow);
+    const T y = x <= T(M::c_mid) ? lo : hi;
+    return T(M::c_dmin) + y * T(M::c_dmax - M::c_dmin);
+  }
+}
+template <class M, class T> __device__ __forceinline__ T impedance_at(T depth) {
+  if (depth >= T(0)) return solimp_at<M, T>(depth);
+  if constexpr (M::c_margin <= 0.0) {
+    return T(0);
+  } else {
+    const T gap = -depth;
+    const T sc = T(1) - gap / T(M::c_margin);
+    const T val = sc * sc * (T(3) - T(2) * sc) * solimp_at<M, T>(T(0));
+    return gap >= T(M::c_margin) ? T(0) : val;
+  }
+}
+template <class M, class T> __device__ __forceinline__ T restitution_at(T approach) {
+  if constexpr (M::c_rest_v <= 0.0) {
+    return T(M::c_rest);
+  } else {
+    const T sp = dabs(approach);
+    const T t = (sp - T(M::c_rest_v)) / T(M::c_rest_v);
+    const T ramp = T(M::c_rest) * t * t * (T(3) - T(2) * t);
+    return sp <= T(M::c_rest_v) ? T(0) : (sp >= T(2.0 * M::c_rest_v) ? T(M::c_rest) : ramp);
+  }
+}
+template <class T> __device__ __forceinline__ void tangent_frame(V3<T> n, V3<T>& u, V3<T>& w) {
+  const bool ax = dabs(n.x) > T(0.9);
+  const V3<T> a = v3(ax ? T(0) : T(1), ax ? T(1) : T(0), T(0));
+  const V3<T> c = cross(n, a);
+  const T l = dsqrt(dot(c, c));
+  u = sel(l > T(0), c * (T(1) / l), c);
+  w = cross(n, u);
+}
+
+// One warm-started Coulomb update of a contact slot (impulse mode,
+// phyz_kernels.cu:874-937 and 1058-1096): normal response with SolImp/solref
+// bias and restitution, tangential response clipped to the friction cone.
+// a_* are the Delassus diagonals, b_* the free contact velocity components;
+// slot holds (normal, tangent u, tangent w) impulses in and out.
+template <class M, class T>
+__device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_nn, T a_uu, T a_ww, T* slot) {
+  const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
+  const T bias = impedance_at<M, T>(pen) * T(M::c_erp) * dmax(pen, T(0)) / T(dtc);
+  const T e = restitution_at<M, T>(dmin(b_n, T(0)));
+  const T r_n = b_n * (T(1) + e) - a_nn * slot[0];
+  const T fn = dmax((bias - r_n) / a_nn, T(0));
+  T tu = -(b_u - a_uu * slot[1]) / a_uu;
+  T tw = -(b_w - a_ww * slot[2]) / a_ww;
+  const T limit = T(M::mu) * fn;
+  const T tn = dsqrt(tu * tu + tw * tw);
+  const T sc = tn > limit ? (tn > T(0) ? limit / tn : T(0)) : T(1);
+  slot[0] = fn;
+  slot[1] = tu * sc;
+  slot[2] = tw * sc;
+}
+
 // Ground penalty contact of body i (crates/phyz-gpu/cuda/phyz_kernels.cu:804-980,
 // penalty branch 939-965). Rw: body->world rotation, pw: body origin in world,
 // vel: body-frame spatial velocity. Returns the body-frame spatial force. When
 // `write` is set, stores the readback row (touching, deepest penetration,
 // point (x, y, h), summed world force) at out[k * S], k = 8 i .. 8 i + 7.
 template <class M, class T, int i>
-__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, T* out, int S, bool write) {
+__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const Terrain<T>& tr, T* out,
+                                              int S, bool write) {
   constexpr int gt = M::gtype[i];
   constexpr int npts = gt == G_BOX ? 8 : 1;
   constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
@@ -338,46 +500,24 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
   SV<T> ext = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
   V3<T> ftot = v3(T(0), T(0), T(0));
   T deepest = T(0);
-  T dx = T(0), dy = T(0);
+  T dx = T(0), dy = T(0), dz = T(0);
   bool any = false;
-  const R3<T> oR = R3<T>{{T(M::gorot[i][0]), T(M::gorot[i][1]), T(M::gorot[i][2]), T(M::gorot[i][3]), T(M::gorot[i][4]),
-                          T(M::gorot[i][5]), T(M::gorot[i][6]), T(M::gorot[i][7]), T(M::gorot[i][8])}};
-  const V3<T> oP = v3(T(M::gopos[i][0]), T(M::gopos[i][1]), T(M::gopos[i][2]));
 #pragma unroll
   for (int cp = 0; cp < npts; cp++) {
-    V3<T> sup;
-    if constexpr (gt == G_BOX) {
-      V3<T> corner = v3(T(M::gp[i][0] * ((cp & 1) ? 1.0 : -1.0)), T(M::gp[i][1] * ((cp & 2) ? 1.0 : -1.0)),
-                        T(M::gp[i][2] * ((cp & 4) ? 1.0 : -1.0)));
-      sup = oP + tmul(oR, corner);
-    } else {
-      V3<T> n = mul(oR, zb);
-      V3<T> s;
-      if constexpr (gt == G_SPHERE) {
-        s = n * T(-M::gp[i][0]);
-      } else if constexpr (gt == G_CAPSULE) {
-        s = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
-      } else if constexpr (gt == G_CYLINDER) {
-        T rl = dsqrt(n.x * n.x + n.y * n.y);
-        T f = rl > T(1e-6) ? T(M::gp[i][0]) / rl : T(0);
-        s = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
-      } else {  // mesh AABB
-        s = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
-               T(0.5 * (M::gp[i][1] + M::gp[i][4])) - T(0.5 * (M::gp[i][4] - M::gp[i][1])) * dsign(n.y),
-               T(0.5 * (M::gp[i][2] + M::gp[i][5])) - T(0.5 * (M::gp[i][5] - M::gp[i][2])) * dsign(n.z));
-      }
-      sup = oP + tmul(oR, s);
-    }
+    const V3<T> sup = contact_point<M, T, i>(cp, zb);
     V3<T> supw = pw + mul(Rw, sup);
-    T pen = T(M::ground_h) - supw.z;
+    V3<T> nw;
+    const T th = terrain_at<M, T>(tr, supw.x, supw.y, nw);
+    T pen = nw.z * (th - supw.z);
+    const V3<T> nb = M::HAS_HF ? tmul(Rw, nw) : zb;
     const bool in = pen > T(0);
     V3<T> vpt = vel.l + cross(vel.a, sup);
-    T vn = dot(vpt, zb);
-    T mn = eff_mass<M, T, i>(sup, zb);
+    T vn = dot(vpt, nb);
+    T mn = eff_mass<M, T, i>(sup, nb);
     T kb = dmin(T(sc * M::gk[i]), T(4.0 / (dtc * dtc)) * mn);
     T db = dmin(T(sc * M::gd[i]), T(1.0 / dtc) * mn);
     T fn = dmax(kb * pen - db * vn, T(0));
-    V3<T> vt3 = vpt - zb * vn;
+    V3<T> vt3 = vpt - nb * vn;
     T vt = dsqrt(dot(vt3, vt3));
     const bool slip = vt > T(1e-6);
     T ivt = slip ? T(1) / vt : T(0);
@@ -385,7 +525,7 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     T coul = T(M::mu) * fn * dmin(T(1), vt * T(1e3));
     T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i>(sup, td) * vt);
     ft = slip ? ft : T(0);
-    V3<T> fb = zb * fn - td * ft;
+    V3<T> fb = nb * fn - td * ft;
     fb = in ? fb : v3(T(0), T(0), T(0));
     ext.a = ext.a + cross(sup, fb);
     ext.l = ext.l + fb;
@@ -395,6 +535,7 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
       deepest = deeper ? pen : deepest;
       dx = deeper ? supw.x : dx;
       dy = deeper ? supw.y : dy;
+      dz = deeper ? th : dz;
       any = any || in;
     }
   }
@@ -404,12 +545,168 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     o[S] = any ? deepest : T(0);
     o[2 * S] = any ? dx : T(0);
     o[3 * S] = any ? dy : T(0);
-    o[4 * S] = any ? T(M::ground_h) : T(0);
+    o[4 * S] = any ? dz : T(0);
     o[5 * S] = any ? ftot.x : T(0);
     o[6 * S] = any ? ftot.y : T(0);
     o[7 * S] = any ? ftot.z : T(0);
   }
   return ext;
+}
+
+// Impulse-mode ground/terrain contact of body i (phyz_kernels.cu:845-937): one
+// warm-started update per contact point from the free velocity `vel`. slot
+// holds this body's ground impulses (3 per point); pslot its plane impulses,
+// cleared with the rest of the contact state when the body is off the ground.
+// Returns the body-frame spatial force; writes the readback row when `write`.
+template <class M, class T, int i>
+__device__ __forceinline__ SV<T> contact_body_imp(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const Terrain<T>& tr,
+                                                  T* slot, T* pslot, T* out, int S, bool write) {
+  constexpr int gt = M::gtype[i];
+  constexpr int npts = gt == G_BOX ? 8 : 1;
+  const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
+  const V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);
+  V3<T> sup[npts], supw[npts], nw[npts];
+  T pen[npts];
+  int nact = 0;
+#pragma unroll
+  for (int cp = 0; cp < npts; cp++) {
+    sup[cp] = contact_point<M, T, i>(cp, zb);
+    supw[cp] = pw + mul(Rw, sup[cp]);
+    const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw[cp]);
+    pen[cp] = nw[cp].z * (th - supw[cp].z);
+    nact += pen[cp] > T(-M::c_margin) ? 1 : 0;
+  }
+  const T na = T(nact < 1 ? 1 : nact);
+  SV<T> ext = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  V3<T> ftot = v3(T(0), T(0), T(0));
+  T deepest = T(0);
+  V3<T> dw = v3(T(0), T(0), T(0));
+  bool any = false;
+#pragma unroll
+  for (int cp = 0; cp < npts; cp++) {
+    const bool in = pen[cp] > T(-M::c_margin);
+    const V3<T> nb = tmul(Rw, nw[cp]);
+    const V3<T> vpt = vel.l + cross(vel.a, sup[cp]);
+    V3<T> tu, tw;
+    tangent_frame(nb, tu, tw);
+    T* sl = slot + 3 * cp;
+    const T a_nn = T(1) / dmax(eff_mass<M, T, i>(sup[cp], nb) / na, T(1e-9));
+    const T a_uu = na / dmax(eff_mass<M, T, i>(sup[cp], tu), T(1e-9));
+    const T a_ww = na / dmax(eff_mass<M, T, i>(sup[cp], tw), T(1e-9));
+    T upd[3] = {sl[0], sl[1], sl[2]};
+    impulse_update<M, T>(pen[cp], dot(vpt, nb), dot(vpt, tu), dot(vpt, tw), a_nn, a_uu, a_ww, upd);
+#pragma unroll
+    for (int k = 0; k < 3; k++) sl[k] = in ? upd[k] : T(0);
+    const V3<T> fb = (nb * sl[0] + tu * sl[1] + tw * sl[2]) * T(1.0 / dtc);
+    ext.a = ext.a + cross(sup[cp], fb);
+    ext.l = ext.l + fb;
+    ftot = ftot + mul(Rw, fb);
+    any = any || in;
+    const bool deeper = in && pen[cp] > deepest;
+    deepest = deeper ? pen[cp] : deepest;
+    dw = sel(deeper, supw[cp], dw);
+  }
+  if (!any) {
+#pragma unroll
+    for (int k = 0; k < 3 * npts; k++) pslot[k] = T(0);
+  }
+  if (write) {
+    T* o = out + 8 * i * S;
+    o[0] = any ? T(1) : T(0);
+    o[S] = any ? deepest : T(0);
+    o[2 * S] = any ? dw.x : T(0);
+    o[3 * S] = any ? dw.y : T(0);
+    o[4 * S] = any ? dw.z : T(0);
+    o[5 * S] = any ? ftot.x : T(0);
+    o[6 * S] = any ? ftot.y : T(0);
+    o[7 * S] = any ? ftot.z : T(0);
+  }
+  return ext;
+}
+
+// Contacts on the body-attached plane (phyz_kernels.cu:982-1132): the plane
+// body's local +Z face at plane_offset, finite in x and y, against every other
+// collidable body not excluded. Forces land on both bodies (added to f). In
+// impulse mode pslot[i] holds body i's plane impulses.
+template <class M, class T, bool IMP>
+__device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw, const SV<T>* vel, T (*pslot)[24],
+                                               SV<T>* f) {
+  constexpr int pb = M::PLANE;
+  const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
+  const V3<T> nw = v3(Rw[pb].m[2], Rw[pb].m[5], Rw[pb].m[8]);  // the face normal, world
+  const V3<T> p0 = Pw[pb] + nw * T(M::plane_offset);
+  sfor<0, M::NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    if constexpr (i != pb && M::gtype[i] != G_NONE && !M::gskip[i]) {
+      constexpr int gt = M::gtype[i];
+      constexpr int npts = gt == G_BOX ? 8 : 1;
+      constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
+      const V3<T> nbi = tmul(Rw[i], nw);
+      V3<T> spw[npts];
+      T lox = T(1e30), loy = T(1e30), hix = T(-1e30), hiy = T(-1e30);
+      int cnt = 0;
+#pragma unroll
+      for (int cp = 0; cp < npts; cp++) {
+        spw[cp] = Pw[i] + mul(Rw[i], contact_point<M, T, i>(cp, nbi));
+        const V3<T> rp = tmul(Rw[pb], spw[cp] - Pw[pb]);
+        lox = dmin(lox, rp.x); loy = dmin(loy, rp.y);
+        hix = dmax(hix, rp.x); hiy = dmax(hiy, rp.y);
+        const T d = -dot(spw[cp] - p0, nw);
+        cnt += (d > T(0) && d <= T(M::plane_depth)) ? 1 : 0;
+      }
+      const T olx = dmax(lox, T(-M::plane_hx)), oly = dmax(loy, T(-M::plane_hy));
+      const T ohx = dmin(hix, T(M::plane_hx)), ohy = dmin(hiy, T(M::plane_hy));
+      if (!(olx > ohx || oly > ohy)) {
+        const T na = T(cnt > 1 ? cnt : 1);
+#pragma unroll
+        for (int cp = 0; cp < npts; cp++) {
+          const T pen = -dot(spw[cp] - p0, nw);
+          const bool in = pen > T(0) && pen <= T(M::plane_depth);
+          V3<T> rpp = tmul(Rw[pb], spw[cp] - Pw[pb]);
+          rpp.x = dmin(dmax(rpp.x, olx), ohx);
+          rpp.y = dmin(dmax(rpp.y, oly), ohy);
+          const V3<T> sw = Pw[pb] + mul(Rw[pb], rpp);
+          const V3<T> sc_i = tmul(Rw[i], sw - Pw[i]);
+          const V3<T> vrel = mul(Rw[i], vel[i].l + cross(vel[i].a, sc_i)) - mul(Rw[pb], vel[pb].l + cross(vel[pb].a, rpp));
+          const T vn = dot(vrel, nw);
+          auto series = [&](V3<T> d) {
+            return T(1) / (T(1) / eff_mass<M, T, i>(sc_i, tmul(Rw[i], d)) + T(1) / eff_mass<M, T, pb>(rpp, tmul(Rw[pb], d)));
+          };
+          V3<T> fw;
+          if constexpr (IMP) {
+            V3<T> pu, pwv;
+            tangent_frame(nw, pu, pwv);
+            T* sl = pslot[i] + 3 * cp;
+            T upd[3] = {sl[0], sl[1], sl[2]};
+            impulse_update<M, T>(pen, vn, dot(vrel, pu), dot(vrel, pwv), na / dmax(series(nw), T(1e-9)),
+                                 na / dmax(series(pu), T(1e-9)), na / dmax(series(pwv), T(1e-9)), upd);
+#pragma unroll
+            for (int k = 0; k < 3; k++) sl[k] = in ? upd[k] : T(0);
+            fw = (nw * sl[0] + pu * sl[1] + pwv * sl[2]) * T(1.0 / dtc);
+          } else {
+            const T mn = series(nw);
+            const T kb = dmin(T(sc * M::gk[i]), T(4.0 / (dtc * dtc)) * mn);
+            const T db = dmin(T(sc * M::gd[i]), T(1.0 / dtc) * mn);
+            const T fn = dmax(kb * pen - db * vn, T(0));
+            const V3<T> vt3 = vrel - nw * vn;
+            const T vt = dsqrt(dot(vt3, vt3));
+            const bool slip = vt > T(1e-6);
+            const V3<T> td = vt3 * (slip ? T(1) / vt : T(0));
+            T ft = dmin(T(M::mu) * fn * dmin(T(1), vt * T(1e3)), T(1.0 / dtc) * series(td) * vt);
+            ft = slip ? ft : T(0);
+            fw = nw * fn - td * ft;
+            fw = sel(in, fw, v3(T(0), T(0), T(0)));
+          }
+          const V3<T> fi = tmul(Rw[i], fw);
+          f[i].a = f[i].a + cross(sc_i, fi);
+          f[i].l = f[i].l + fi;
+          const V3<T> fp = tmul(Rw[pb], v3(T(0), T(0), T(0)) - fw);
+          f[pb].a = f[pb].a + cross(rpp, fp);
+          f[pb].l = f[pb].l + fp;
+        }
+      }
+    }
+  });
 }
 
 // ── per-world step, organised by body groups ────────────────────────────────
@@ -482,7 +779,7 @@ __device__ __forceinline__ void joint_xf(const T* q, const T* v, Xf<T>& X, SV<T>
 
 template <class M, class T, int i>
 __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v, T* rows, int S, bool write_rows,
-                                           bool do_contact) {
+                                           bool do_contact, const Terrain<T>& tr) {
   constexpr int p = M::parent[i];
   Xf<T>& X = ws.X[i];
   SV<T> vj;
@@ -506,7 +803,7 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
   }
   if constexpr (M::gtype[i] != G_NONE) {
     if (do_contact) {
-      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], rows, S, write_rows);
+      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], tr, rows, S, write_rows);
       ws.pA[i] = ws.pA[i] - f;
     }
   }
@@ -709,15 +1006,10 @@ template <class T> __device__ __forceinline__ void add_sym(const T* lds, int s, 
   p.l = p.l + v3(lds_get(lds, s + 24, lane), lds_get(lds, s + 25, lane), lds_get(lds, s + 26, lane));
 }
 
-// One step of group G for one world (lane). State arrays are in registers; a
-// group reads and writes only the DOFs of its own bodies (plus the trunk's).
+// Control noise and PD servos of group G's DOFs, before the dynamics.
 template <class M, class T, int G>
-__device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
-                                           const T* tgt, u64& rng, T* rows, int S, bool write_rows, T* lds, int lane) {
-  constexpr int NB = M::NB;
-  constexpr int NL = M::glen[G];
-  constexpr int NT = M::NTRUNK;
-  constexpr bool FLOAT = M::PMODE == 2;
+__device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)[M::NV], T (&ctrl)[M::NV], const T* tgt,
+                                               u64& rng) {
   // ── control noise: every group advances the whole stream; values only for its DOFs ──
   if constexpr (M::NNOISE > 0) {
     if constexpr (M::noise_dist == 1) {
@@ -753,16 +1045,37 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
     }
   });
 
+}
+
+// One step of group G for one world (lane). State arrays are in registers; a
+// group reads and writes only the DOFs of its own bodies (plus the trunk's).
+template <class M, class T, int G>
+__device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+                                           const T* tgt, u64& rng, T* rows, int S, bool write_rows, T* lds, int lane,
+                                           const Terrain<T>& tr) {
+  constexpr int NB = M::NB;
+  constexpr int NL = M::glen[G];
+  constexpr int NT = M::NTRUNK;
+  constexpr bool FLOAT = M::PMODE == 2;
+  apply_controls<M, T, G>(q, v, ctrl, tgt, rng);
+
   WS<M, T> ws;
   // ── pass 1: trunk (every group), then own bodies ──
   sfor<0, NT>([&](auto K) {
     constexpr int i = M::tlist[decltype(K)::value];
-    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, G == 0);
+    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, G == 0, tr);
   });
   sfor<0, NL>([&](auto K) {
     constexpr int i = M::glist[G][decltype(K)::value];
-    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, true);
+    body_pass1<M, T, i>(ws, q, v, rows, S, write_rows, true, tr);
   });
+  if constexpr (M::HAS_CONTACT && M::PLANE >= 0) {
+    // Body-attached plane, penalty law (one group owns every body here).
+    SV<T> fp[NB];
+    sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; fp[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))}; });
+    plane_contacts<M, T, false>(ws.Rw, ws.Pw, ws.vel, (T(*)[24]) nullptr, fp);
+    sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; ws.pA[i] = ws.pA[i] - fp[i]; });
+  }
   // ── pass 2: own bodies, leaves first ──
   sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; ws.IA[i] = rigid_inertia<M, T, i>(); });
   rfor<NL>([&](auto K) {
@@ -867,6 +1180,145 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
   });
 }
 
+// Force-dependent half of body i's pass 2 after the contact forces change
+// (impulse sweeps): u = tau - S^T p_A and p_a = p_A + I_a c + U D^-1 u, with
+// U, D^-1 and I_a c kept from the step's full pass 2 (q and v do not change
+// between sweeps, so neither do the articulated inertias).
+template <class M, class T, int i>
+__device__ __forceinline__ void body_bias(WS<M, T>& ws, const T* q, const T* v, const T* ctrl, const SV<T>& iac, SV<T>& pa) {
+  constexpr int nd = ndof_of(M::jtype[i]);
+  constexpr int p = M::parent[i];
+  constexpr int vo = M::voff[i], qo = M::qoff[i];
+  constexpr int MAXD = M::MAXD;
+  pa = ws.pA[i];
+  if constexpr (nd > 0) {
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
+      if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
+      ws.uu[i][k] = tau - dot(subspace<M, T, i>(k), ws.pA[i]);
+    }
+    if constexpr (p >= 0) {
+      // U D^-1 u: solve L D L^T y = u, then U y.
+      T y[MAXD];
+#pragma unroll
+      for (int k = 0; k < nd; k++) {
+        y[k] = ws.uu[i][k];
+#pragma unroll
+        for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
+      }
+#pragma unroll
+      for (int k = 0; k < nd; k++) y[k] = y[k] * ws.Dinv[i][k];
+#pragma unroll
+      for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+        for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
+      SV<T> wu = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+#pragma unroll
+      for (int k = 0; k < nd; k++) {
+        const SV<T> uk = {v3(ws.U[i][k][0], ws.U[i][k][1], ws.U[i][k][2]), v3(ws.U[i][k][3], ws.U[i][k][4], ws.U[i][k][5])};
+        wu = wu + uk * y[k];
+      }
+      pa = pa + iac + wu;
+    }
+  }
+}
+
+template <class M> struct HasExt {
+  template <int i> static constexpr bool at() { return M::gtype[i] != G_NONE || i == M::PLANE; }
+};
+
+// One impulse-mode step of one world (crates/phyz-gpu/src/cuda/mod.rs:899-928):
+// controls; FK, velocities and bias forces once; a full ABA against the
+// contact forces carried from the previous step; then SWEEPS x [contact at the
+// free velocity v + dt qdd (warm-started), force-only ABA re-solve]; integrate.
+// ext, impg (ground) and impp (plane) persist between steps.
+template <class M, class T>
+__device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+                                             const T* tgt, u64& rng, SV<T> (&ext)[M::NB], T (&impg)[M::NB][24],
+                                             T (&impp)[M::NB][24], const Terrain<T>& tr, T* rows, int S,
+                                             bool write_rows) {
+  constexpr int NB = M::NB;
+  apply_controls<M, T, 0>(q, v, ctrl, tgt, rng);
+  WS<M, T> ws;
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    body_pass1<M, T, i>(ws, q, v, rows, S, false, false, tr);
+  });
+  SV<T> pA0[NB], iac[NB];
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    pA0[i] = ws.pA[i];
+    if constexpr (HasExt<M>::template at<i>()) ws.pA[i] = ws.pA[i] - ext[i];
+    ws.IA[i] = rigid_inertia<M, T, i>();
+  });
+  rfor<NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int p = M::parent[i];
+    Sym<T> Ia;
+    SV<T> pa;
+    body_solve<M, T, i>(ws, q, v, ctrl, Ia, pa);
+    iac[i] = (ndof_of(M::jtype[i]) > 0 && p >= 0) ? sym_mul(Ia, ws.cb[i]) : SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+    if constexpr (p >= 0) {
+      if (ws.ok[i]) {
+        Sym<T> dI;
+        SV<T> dp;
+        propagate<M, T, i>(ws, Ia, pa, dI, dp);
+        sym_add(ws.IA[p], dI);
+        ws.pA[p] = ws.pA[p] + dp;
+      }
+    }
+  });
+  sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
+  // A plain loop: compact, spill-free, and exact at every sweep count. Left to
+  // the compiler's own unrolling choice, the f64 kernel of an 8-corner box gave
+  // wrong impulses from the fourth sweep on (checked across sweep counts in
+  // tests/test_gpu_contact_modes.py).
+#pragma unroll 1
+  for (int sw = 0; sw < M::SWEEPS; sw++) {
+    // Body velocities at the free joint velocity v + dt qdd.
+    T vv[M::NV];
+#pragma unroll
+    for (int j = 0; j < M::NV; j++) vv[j] = v[j] + T(M::dt) * qdd[j];
+    SV<T> vf[NB];
+    sfor<0, NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int p = M::parent[i];
+      Xf<T> Xd;
+      SV<T> vj;
+      joint_xf<M, T, i>(q, vv, Xd, vj);
+      if constexpr (p < 0) vf[i] = vj;
+      else vf[i] = apply_motion(ws.X[i], vf[p]) + vj;
+    });
+    const bool wr = write_rows && sw == M::SWEEPS - 1;
+    sfor<0, NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (M::gtype[i] != G_NONE) {
+        ext[i] = contact_body_imp<M, T, i>(ws.Rw[i], ws.Pw[i], vf[i], tr, impg[i], impp[i], rows, S, wr);
+      } else if constexpr (i == M::PLANE) {
+        ext[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+      }
+    });
+    if constexpr (M::PLANE >= 0) plane_contacts<M, T, true>(ws.Rw, ws.Pw, vf, impp, ext);
+    sfor<0, NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      ws.pA[i] = pA0[i];
+      if constexpr (HasExt<M>::template at<i>()) ws.pA[i] = ws.pA[i] - ext[i];
+    });
+    rfor<NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int p = M::parent[i];
+      SV<T> pa;
+      body_bias<M, T, i>(ws, q, v, ctrl, iac[i], pa);
+      if constexpr (p >= 0) {
+        if (ws.ok[i]) ws.pA[p] = ws.pA[p] + inv_apply_force(ws.X[i], pa);
+      }
+    });
+    sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
+  }
+  sfor<0, NB>([&](auto I) { body_integrate<M, T, decltype(I)::value>(q, v, qdd); });
+}
+
 // Kernel body for group G: load the world's state, run nsteps, store. A group
 // loads the DOFs it owns and the trunk's; it stores only the DOFs it owns
 // (group 0 also stores the trunk's and the RNG state).
@@ -902,10 +1354,57 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
   u64 rng = 0;
   if constexpr (M::NNOISE > 0) rng = a.rng[wl];
   T* rows = M::HAS_CONTACT ? (T*)a.contact_rows + wl : nullptr;
+  const Terrain<T> tr{(const T*)a.hf, T(a.hf_ox), T(a.hf_oy), T(a.hf_oz), T(a.hf_cell), a.hf_nx, a.hf_ny};
   const int n = a.nsteps;
-  for (int s = 0; s < n; s++) {
-    const bool last = (s == n - 1) && a.write_contacts && live;
-    step_group<M, T, G>(q, v, ctrl, qdd, tgt, rng, rows, S, last, lds, lane);
+  if constexpr (M::HAS_CONTACT && M::CMODE == 1) {
+    // Impulse mode: one group (checked on the host); the solver state persists.
+    SV<T> ext[M::NB];
+    T impg[M::NB][24], impp[M::NB][24];
+    const T* ge = (const T*)a.ext;
+    const T* gi = (const T*)a.imp;
+    sfor<0, M::NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int np3 = 3 * (M::gtype[i] == G_BOX ? 8 : 1);
+      if constexpr (HasExt<M>::template at<i>()) {
+        ext[i] = SV<T>{v3(ge[(6 * i) * S + wl], ge[(6 * i + 1) * S + wl], ge[(6 * i + 2) * S + wl]),
+                       v3(ge[(6 * i + 3) * S + wl], ge[(6 * i + 4) * S + wl], ge[(6 * i + 5) * S + wl])};
+      }
+      if constexpr (M::gtype[i] != G_NONE) {
+#pragma unroll
+        for (int k = 0; k < np3; k++) {
+          impg[i][k] = gi[(48 * i + k) * S + wl];
+          impp[i][k] = M::PLANE >= 0 ? gi[(48 * i + 24 + k) * S + wl] : T(0);
+        }
+      }
+    });
+    for (int s = 0; s < n; s++) {
+      const bool last = (s == n - 1) && a.write_contacts && live;
+      step_impulse<M, T>(q, v, ctrl, qdd, tgt, rng, ext, impg, impp, tr, rows, S, last);
+    }
+    if (live) {
+      T* he = (T*)a.ext;
+      T* hi = (T*)a.imp;
+      sfor<0, M::NB>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        constexpr int np3 = 3 * (M::gtype[i] == G_BOX ? 8 : 1);
+        if constexpr (HasExt<M>::template at<i>()) {
+          he[(6 * i) * S + w] = ext[i].a.x; he[(6 * i + 1) * S + w] = ext[i].a.y; he[(6 * i + 2) * S + w] = ext[i].a.z;
+          he[(6 * i + 3) * S + w] = ext[i].l.x; he[(6 * i + 4) * S + w] = ext[i].l.y; he[(6 * i + 5) * S + w] = ext[i].l.z;
+        }
+        if constexpr (M::gtype[i] != G_NONE) {
+#pragma unroll
+          for (int k = 0; k < np3; k++) {
+            hi[(48 * i + k) * S + w] = impg[i][k];
+            if constexpr (M::PLANE >= 0) hi[(48 * i + 24 + k) * S + w] = impp[i][k];
+          }
+        }
+      });
+    }
+  } else {
+    for (int s = 0; s < n; s++) {
+      const bool last = (s == n - 1) && a.write_contacts && live;
+      step_group<M, T, G>(q, v, ctrl, qdd, tgt, rng, rows, S, last, lds, lane, tr);
+    }
   }
   if (!live) return;
   sfor<0, M::NQ>([&](auto J) {

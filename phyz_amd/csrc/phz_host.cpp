@@ -143,8 +143,16 @@ bool parse_model(const double* t, uint32_t nb, uint32_t nq, uint32_t nv, const d
 struct Features {
   bool contact = false;
   double ground_h = 0, mu = 0;
-  std::vector<double> geom;  // nb x 24
+  std::vector<double> geom;  // nb x 24 (slot 7: excluded from the body-attached plane)
   int collidable = 0;
+  // Contact solver and terrain (ContactParams, crates/phyz-gpu/src/contact_pipeline.rs:17-100).
+  int cmode = 0;             // 0 penalty, 1 velocity-level impulse solve
+  int sweeps = 16;           // [contact, ABA] sweeps per step in impulse mode (DEFAULT_CONTACT_SWEEPS)
+  double prm[9] = {0.0, 0.05, 0.001 / (2.0 * 0.02 + 0.001), 0.001, 0.9, 0.95, 0.001, 0.5, 2.0};
+  int plane_body = -1;       // body-attached plane: body, offset, max depth, half x, half y
+  double plane[4] = {0, 0, 0, 0};
+  int hf_nx = 0, hf_ny = 0;  // heightfield header; the nodes live in a device buffer
+  double hf_o[3] = {0, 0, 0}, hf_cell = 1.0;
   int npd = 0;
   std::vector<double> pd;  // npd x 8
   bool noise = false;
@@ -186,7 +194,7 @@ struct Plan {
   std::vector<std::vector<int>> groups;  // bodies owned by each wave, topological order
 };
 
-Plan plan_partition(const ModelD& m) {
+Plan plan_partition(const ModelD& m, const Features& f) {
   const int nb = m.nb;
   Plan pl;
   std::vector<int> all(nb);
@@ -195,6 +203,9 @@ Plan plan_partition(const ModelD& m) {
   const std::string want = env ? env : "auto";
   auto lane_per_world = [&]() { pl = Plan{}; pl.groups.push_back(all); return pl; };
   if (want == "0") return lane_per_world();
+  // Impulse sweeps and the body-attached plane couple bodies across subtrees
+  // every sweep: they run one lane per world.
+  if (f.contact && (f.cmode == 1 || f.plane_body >= 0)) return lane_per_world();
   std::vector<std::vector<int>> kids(nb);
   for (int i = 0; i < nb; i++) if (m.b[i].parent >= 0) kids[m.b[i].parent].push_back(i);
   std::vector<int> size(nb, 1);
@@ -306,12 +317,15 @@ std::string gen_model(const ModelD& m, const Features& f) {
     ptj_id[i] = 1;
     for (int k = 0; k < 9; k++) if (b.ptj_rot[k] != id[k]) ptj_id[i] = 0;
   }
-  if (f.contact)
+  if (f.contact) {
     for (int i = 0; i < nb; i++)
       if ((int)f.geom[i * kGeomStride] != 0)
         for (int j = i; j >= 0; j = m.b[j].parent) need_world[j] = 1;
+    if (f.plane_body >= 0)
+      for (int j = f.plane_body; j >= 0; j = m.b[j].parent) need_world[j] = 1;
+  }
 
-  const Plan pl = plan_partition(m);
+  const Plan pl = plan_partition(m, f);
   const int ng = (int)pl.groups.size();
   int maxg = 1;
   for (auto& g : pl.groups) maxg = std::max(maxg, (int)g.size());
@@ -365,6 +379,22 @@ std::string gen_model(const ModelD& m, const Features& f) {
   o << "  static constexpr int tdof[" << m.nv << "] = " << arr1(m.nv, [&](int j) { return std::to_string(tdof[j]); })
     << ";\n";
   o << "  static constexpr bool HAS_CONTACT = " << (f.contact ? "true" : "false") << ";\n";
+  o << "  static constexpr int CMODE = " << (f.contact ? f.cmode : 0) << ", SWEEPS = " << f.sweeps
+    << ", PLANE = " << (f.contact ? f.plane_body : -1) << ";\n";
+  o << "  static constexpr bool HAS_HF = " << (f.contact && f.hf_nx > 0 ? "true" : "false") << ";\n";
+  o << "  static constexpr double c_rest = " << num(f.prm[0]) << ", c_rest_v = " << num(f.prm[1]) << ", c_erp = "
+    << num(f.prm[2]) << ", c_margin = " << num(f.prm[3]) << ";\n";
+  {
+    // SolImp's clamps (phyz_kernels.cu:595-607), evaluated once here.
+    const double dmin = std::clamp(f.prm[4], 1e-4, 1.0 - 1e-9), dmax = std::clamp(f.prm[5], 1e-4, 1.0 - 1e-9);
+    const double mid = std::clamp(f.prm[7], 1e-6, 1.0 - 1e-6), pw = std::max(f.prm[8], 1.0);
+    o << "  static constexpr double c_dmin = " << num(dmin) << ", c_dmax = " << num(dmax) << ", c_width = "
+      << num(f.prm[6]) << ", c_mid = " << num(mid) << ", c_power = " << num(pw) << ";\n";
+    o << "  static constexpr double c_mid_pow = " << num(std::pow(mid, pw - 1.0)) << ", c_omid_pow = "
+      << num(std::pow(1.0 - mid, pw - 1.0)) << ";\n";
+  }
+  o << "  static constexpr double plane_offset = " << num(f.plane[0]) << ", plane_depth = " << num(f.plane[1])
+    << ", plane_hx = " << num(f.plane[2]) << ", plane_hy = " << num(f.plane[3]) << ";\n";
   o << "  static constexpr int NPD = " << npd << ", NNOISE = " << nn << ", noise_dist = " << f.dist << ";\n";
   o << "  static constexpr double dt = " << num(m.dt) << ";\n";
   o << "  static constexpr double gravity[3] = " << arr1(3, [&](int k) { return num(m.g[k]); }) << ";\n";
@@ -415,6 +445,7 @@ std::string gen_model(const ModelD& m, const Features& f) {
   db("gd", [&](int i) { return g(i, 9); });
   d2("gopos", 3, [&](int i, int k) { return g(i, 10 + k); });
   d2("gorot", 9, [&](int i, int k) { return f.contact ? g(i, 13 + k) : (k % 4 == 0 ? 1.0 : 0.0); });
+  bb("gskip", [&](int i) { return f.contact && g(i, 7) != 0.0; });
   const int npa = std::max(npd, 1), nna = std::max(nn, 1);
   auto pdv = [&](int d, int s) { return npd ? f.pd[d * kPdStride + s] : 0.0; };
   o << "  static constexpr int pd_q[" << npa << "] = " << arr1(npa, [&](int d) { return std::to_string((int)pdv(d, 0)); }) << ";\n";
@@ -430,7 +461,7 @@ std::string gen_model(const ModelD& m, const Features& f) {
 
 // One workgroup = NG waves over the same 64 worlds; wave g runs group g.
 std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups) {
-  const int ng = (int)plan_partition(m).groups.size();
+  const int ng = (int)plan_partition(m, f).groups.size();
   *ngroups = ng;
   const std::string T = f64 ? "double" : "float";
   std::string s = kDeviceSrc;
@@ -558,6 +589,11 @@ struct StepArgs {  // must match phz::StepArgs in phz_device.h
   const void* targets;
   uint64_t* rng;
   void* contact_rows;
+  void* ext;
+  void* imp;
+  const void* hf;
+  double hf_ox, hf_oy, hf_oz, hf_cell;
+  int hf_nx, hf_ny;
   int nworld;
   int stride;
   int nsteps;
@@ -816,6 +852,8 @@ struct phz_sim {
   int max_steps = 1000;
   hipStream_t stream = nullptr;
   void *q = nullptr, *v = nullptr, *ctrl = nullptr, *qdd = nullptr, *targets = nullptr, *rows = nullptr;
+  void *ext_buf = nullptr, *imp_buf = nullptr, *hf_buf = nullptr;  // impulse solver state; heightfield nodes (T)
+  size_t hf_cap = 0;                                                // node capacity of hf_buf
   uint64_t* rng = nullptr;
   double* staging = nullptr;
   size_t staging_bytes = 0;
@@ -877,6 +915,8 @@ struct phz_sim {
   }
   bool ensure_staging(size_t bytes) {
     if (bytes <= staging_bytes) return true;
+    // A pack or unpack kernel queued on the stream may still read the old buffer.
+    if (staging && !hip_ok(hipStreamSynchronize(stream), "staging sync")) return false;
     if (staging) hipFree(staging);
     staging = nullptr;
     staging_bytes = 0;
@@ -924,7 +964,9 @@ struct phz_sim {
     return hip_ok(hipModuleGetFunction(&fn, module, "phz_step"), "hipModuleGetFunction");
   }
   bool launch(int nsteps) {
-    StepArgs a{q, v, ctrl, qdd, targets, rng, rows, nworld, stride, nsteps, feat.contact ? 1 : 0};
+    StepArgs a{q,       v,       ctrl,    qdd,          targets,          rng,        rows,       ext_buf, imp_buf,
+               hf_buf,  feat.hf_o[0], feat.hf_o[1], feat.hf_o[2], feat.hf_cell, feat.hf_nx, feat.hf_ny, nworld,
+               stride,  nsteps,  feat.contact ? 1 : 0};
     void* params[] = {&a};
     const unsigned grid = (unsigned)((nworld + 63) / 64);
     return hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
@@ -940,6 +982,10 @@ struct phz_sim {
   }
   bool step_many(uint32_t n) {
     if (!has_device()) { err = "host-only sim (device_ordinal -1) cannot step"; return false; }
+    if (feat.contact && feat.cmode == 1 && feat.sweeps < 1) {
+      err = "impulse contact needs at least one contact sweep per step";
+      return false;
+    }
     if (n == 0) return true;
     if (nworld == 0) return true;
     if (!load_kernel()) return false;
@@ -1089,7 +1135,7 @@ struct phz_sim {
       obs_k.reset();
       pol_k.reset();
       free_policy_buffers();
-      for (void* p : {q, v, ctrl, qdd, targets, rows, (void*)rng, (void*)staging, kin, hq, hv})
+      for (void* p : {q, v, ctrl, qdd, targets, rows, (void*)rng, (void*)staging, kin, hq, hv, ext_buf, imp_buf, hf_buf})
         if (p) hipFree(p);
       if (stream) hipStreamDestroy(stream);
     }
@@ -1117,33 +1163,120 @@ template <class F> int time_reps(phz_sim* s, uint32_t reps, double* ms_per_rep, 
   return ok ? 0 : 1;
 }
 
-int set_contact(phz_sim* s, double ground_h, double friction, const double* geom, const double* gains, double k,
-                double d, uint32_t* collidable_out) {
-  if (!geom) return s->fail("null geometry table");
-  if (!(std::isfinite(ground_h) && std::isfinite(friction))) return s->fail("ground height and friction must be finite");
+// Everything enable_contact takes (crates/phyz-gpu/src/cuda/mod.rs:704-733):
+// ground or terrain, penalty or impulse, an optional body-attached plane.
+struct ContactSpec {
+  double ground_h = 0, friction = 0;
+  const double* geom = nullptr;
+  const double* gains = nullptr;  // nb x 2 (k, d), or the global k, d below
+  double k = 0, d = 0;
+  int cmode = 0;
+  const double* solver = nullptr;  // 9 solver parameters, or the defaults
+  const double* plane = nullptr;   // body, offset, max depth, half x, half y
+  const uint32_t* exclude = nullptr;
+  uint32_t n_exclude = 0;
+  const double* hf = nullptr;      // nx, ny, origin x, y, z, cell
+  const double* heights = nullptr; // [ny][nx]
+};
+
+// validate_heightfield (crates/phyz-gpu/src/contact_pipeline.rs:652-671).
+bool check_heightfield(phz_sim* s, const double* hf, const double* heights, int& nx, int& ny) {
+  if (!hf) return true;
+  if (!(is_int(hf[0]) && is_int(hf[1])) || hf[0] < 1 || hf[1] < 1 || hf[0] > (1 << 15) || hf[1] > (1 << 15)) {
+    s->err = "heightfield needs at least one node per axis";
+    return false;
+  }
+  if (!(std::isfinite(hf[5]) && hf[5] > 0.0)) { s->err = fmt("heightfield cell must be positive, got %g", hf[5]); return false; }
+  for (int k = 2; k < 5; k++)
+    if (!std::isfinite(hf[k])) { s->err = "heightfield origin must be finite"; return false; }
+  if (!heights) { s->err = "null heightfield heights"; return false; }
+  nx = (int)hf[0];
+  ny = (int)hf[1];
+  for (size_t k = 0; k < (size_t)nx * ny; k++)
+    if (!std::isfinite(heights[k])) { s->err = "heightfield heights must be finite"; return false; }
+  return true;
+}
+
+bool upload_heightfield(phz_sim* s, const double* heights, size_t n) {
+  if (!s->has_device()) return true;
+  const size_t E = s->esize();
+  std::vector<char> buf(n * E);
+  for (size_t k = 0; k < n; k++) {
+    if (s->f64) ((double*)buf.data())[k] = heights[k];
+    else ((float*)buf.data())[k] = (float)heights[k];
+  }
+  if (!s->hip_ok(hipMemcpyAsync(s->hf_buf, buf.data(), n * E, hipMemcpyHostToDevice, s->stream), "upload heightfield"))
+    return false;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "upload heightfield");
+}
+
+int set_contact(phz_sim* s, const ContactSpec& cs, uint32_t* collidable_out) {
+  if (!cs.geom) return s->fail("null geometry table");
+  if (!(std::isfinite(cs.ground_h) && std::isfinite(cs.friction))) return s->fail("ground height and friction must be finite");
   const int nb = s->model.nb;
-  std::vector<double> g(geom, geom + (size_t)nb * kGeomStride);
+  if (cs.plane) {
+    if (!is_int(cs.plane[0]) || cs.plane[0] < 0 || cs.plane[0] >= nb)
+      return s->fail(fmt("plane body %g out of range for a model with %d bodies", cs.plane[0], nb));
+    for (int k = 1; k < 5; k++) if (!std::isfinite(cs.plane[k])) return s->fail("plane parameters must be finite");
+    for (uint32_t k = 0; k < cs.n_exclude; k++)
+      if (cs.exclude[k] >= (uint32_t)nb) return s->fail(fmt("plane exclude body %u out of range", cs.exclude[k]));
+  }
+  int nx = 0, ny = 0;
+  if (!check_heightfield(s, cs.hf, cs.heights, nx, ny)) return 1;
+  if (cs.solver)
+    for (int k = 0; k < 9; k++) if (!std::isfinite(cs.solver[k])) return s->fail("contact solver parameters must be finite");
+  std::vector<double> g(cs.geom, cs.geom + (size_t)nb * kGeomStride);
   int collidable = 0;
   for (int i = 0; i < nb; i++) {
     double* r = &g[(size_t)i * kGeomStride];
     if (!is_int(r[0]) || r[0] < 0 || r[0] > 5) return s->fail(fmt("body %d: unknown geometry type %g", i, r[0]));
-    if (gains) { r[8] = gains[i * 2]; r[9] = gains[i * 2 + 1]; }
-    else { r[8] = k; r[9] = d; }
+    if (cs.gains) { r[8] = cs.gains[i * 2]; r[9] = cs.gains[i * 2 + 1]; }
+    else { r[8] = cs.k; r[9] = cs.d; }
+    r[7] = 0.0;
     for (int q = 1; q < 22; q++)
       if (!std::isfinite(r[q])) return s->fail(fmt("body %d: non-finite geometry slot %d", i, q));
     if ((int)r[0] != 0) collidable++;
+  }
+  if (cs.plane) {  // pack_contact_geometry: the plane body and the excluded bodies never touch the plane
+    g[(size_t)cs.plane[0] * kGeomStride + 7] = 1.0;
+    for (uint32_t k = 0; k < cs.n_exclude; k++) g[(size_t)cs.exclude[k] * kGeomStride + 7] = 1.0;
   }
   if (collidable == 0)
     return s->fail("ground contact enabled but no body has GPU-collidable geometry "
                    "(supported: sphere, box, capsule, cylinder, mesh)");
   if (!set_device(s)) return 1;
-  s->feat.contact = true;
-  s->feat.ground_h = ground_h;
-  s->feat.mu = friction;
-  s->feat.geom = std::move(g);
-  s->feat.collidable = collidable;
-  if (s->has_device() && !s->rows) {
-    if (!s->alloc(&s->rows, (size_t)nb * 8 * s->stride * s->esize(), "contact rows alloc")) return 1;
+  Features& f = s->feat;
+  f.contact = true;
+  f.ground_h = cs.ground_h;
+  f.mu = cs.friction;
+  f.geom = std::move(g);
+  f.collidable = collidable;
+  f.cmode = cs.cmode;
+  const double dt = s->model.dt;
+  const double defaults[9] = {0.0, 0.05, cs.cmode == 1 ? dt / (2.0 * 0.02 * 1.0 + dt) : 0.001 / (2.0 * 0.02 + 0.001),
+                              0.001, 0.9, 0.95, 0.001, 0.5, 2.0};
+  for (int k = 0; k < 9; k++) f.prm[k] = cs.solver ? cs.solver[k] : defaults[k];
+  f.plane_body = cs.plane ? (int)cs.plane[0] : -1;
+  for (int k = 0; k < 4; k++) f.plane[k] = cs.plane ? cs.plane[1 + k] : 0.0;
+  f.hf_nx = nx;
+  f.hf_ny = ny;
+  for (int k = 0; k < 3; k++) f.hf_o[k] = cs.hf ? cs.hf[2 + k] : 0.0;
+  f.hf_cell = cs.hf ? cs.hf[5] : 1.0;
+  if (s->has_device()) {
+    const size_t E = s->esize(), S = s->stride;
+    if (!s->rows && !s->alloc(&s->rows, (size_t)nb * 8 * S * E, "contact rows alloc")) return 1;
+    if (cs.cmode == 1) {
+      if (!s->ext_buf && !s->alloc(&s->ext_buf, (size_t)nb * 6 * S * E, "contact force state alloc")) return 1;
+      if (!s->imp_buf && !s->alloc(&s->imp_buf, (size_t)nb * 48 * S * E, "impulse state alloc")) return 1;
+    }
+    // Node buffer sized to this first field (set_heightfield may shrink, not grow, it).
+    const size_t nodes = (size_t)std::max(nx, 1) * std::max(ny, 1);
+    if (s->hf_buf) { s->invalidate(); hipFree(s->hf_buf); s->hf_buf = nullptr; }
+    if (!s->alloc(&s->hf_buf, nodes * E, "heightfield alloc")) return 1;
+    s->hf_cap = nx > 0 ? nodes : 0;
+    if (nx > 0 && !upload_heightfield(s, cs.heights, nodes)) return 1;
+  } else {
+    s->hf_cap = (size_t)nx * ny;
   }
   s->invalidate();
   if (collidable_out) *collidable_out = (uint32_t)collidable;
@@ -1215,14 +1348,150 @@ int phz_enable_ground_contact(phz_sim* s, double ground_height, double stiffness
                               const double* geom_table, uint32_t* collidable_out) {
   if (!s) return 1;
   if (!(std::isfinite(stiffness) && std::isfinite(damping))) return s->fail("stiffness and damping must be finite");
-  return set_contact(s, ground_height, friction, geom_table, nullptr, stiffness, damping, collidable_out);
+  ContactSpec cs;
+  cs.ground_h = ground_height;
+  cs.friction = friction;
+  cs.geom = geom_table;
+  cs.k = stiffness;
+  cs.d = damping;
+  return set_contact(s, cs, collidable_out);
 }
 
 int phz_enable_ground_contact_per_body(phz_sim* s, double ground_height, double friction, const double* gains,
                                        const double* geom_table, uint32_t* collidable_out) {
   if (!s) return 1;
   if (!gains) return s->fail("null gains table");
-  return set_contact(s, ground_height, friction, geom_table, gains, 0.0, 0.0, collidable_out);
+  ContactSpec cs;
+  cs.ground_h = ground_height;
+  cs.friction = friction;
+  cs.geom = geom_table;
+  cs.gains = gains;
+  return set_contact(s, cs, collidable_out);
+}
+
+namespace {
+int enable_contact_with(phz_sim* s, int cmode, double ground_height, double friction, const double* gains,
+                        const double* geom_table, const double* plane, const uint32_t* plane_exclude, uint32_t n_exclude,
+                        const double* hf, const double* heights, const double* solver, uint32_t* collidable_out) {
+  if (!gains) return s->fail("null gains table");
+  if (n_exclude && !plane_exclude) return s->fail("null plane exclude list");
+  ContactSpec cs;
+  cs.ground_h = ground_height;
+  cs.friction = friction;
+  cs.geom = geom_table;
+  cs.gains = gains;
+  cs.cmode = cmode;
+  cs.solver = solver;
+  cs.plane = plane;
+  cs.exclude = plane_exclude;
+  cs.n_exclude = plane ? n_exclude : 0;
+  cs.hf = hf;
+  cs.heights = heights;
+  return set_contact(s, cs, collidable_out);
+}
+}  // namespace
+
+int phz_enable_contact_terrain(phz_sim* s, double ground_height, double friction, const double* gains,
+                               const double* geom_table, const double* plane, const uint32_t* plane_exclude,
+                               uint32_t n_exclude, const double* hf, const double* heights, uint32_t* collidable_out) {
+  if (!s) return 1;
+  return enable_contact_with(s, 0, ground_height, friction, gains, geom_table, plane, plane_exclude, n_exclude, hf,
+                             heights, nullptr, collidable_out);
+}
+
+int phz_enable_contact_impulse(phz_sim* s, double ground_height, double friction, const double* gains,
+                               const double* geom_table, const double* plane, const uint32_t* plane_exclude,
+                               uint32_t n_exclude, const double* hf, const double* heights, const double* solver,
+                               uint32_t* collidable_out) {
+  if (!s) return 1;
+  return enable_contact_with(s, 1, ground_height, friction, gains, geom_table, plane, plane_exclude, n_exclude, hf,
+                             heights, solver, collidable_out);
+}
+
+int phz_set_heightfield(phz_sim* s, const double* hf, const double* heights) {
+  if (!s) return 1;
+  if (!s->feat.contact) return s->fail("contact not enabled — call enable_contact_terrain first");
+  if (!hf) return s->fail("null heightfield");
+  int nx = 0, ny = 0;
+  if (!check_heightfield(s, hf, heights, nx, ny)) return 1;
+  const size_t nodes = (size_t)nx * ny;
+  if (s->feat.hf_nx == 0)
+    return s->fail("contact was enabled without a heightfield; enable contact with one to use terrain");
+  if (nodes > s->hf_cap)
+    return s->fail(fmt("heightfield has %zu nodes but the buffer was sized for %zu; enable contact with the largest "
+                       "grid first", nodes, s->hf_cap));
+  if (!set_device(s)) return 1;
+  if (s->stream) hipStreamSynchronize(s->stream);
+  s->feat.hf_nx = nx;
+  s->feat.hf_ny = ny;
+  for (int k = 0; k < 3; k++) s->feat.hf_o[k] = hf[2 + k];
+  s->feat.hf_cell = hf[5];
+  s->drop_graph();  // the header is a launch argument: re-capture
+  return upload_heightfield(s, heights, nodes) ? 0 : 1;
+}
+
+int phz_set_contact_sweeps(phz_sim* s, uint32_t sweeps) {
+  if (!s) return 1;
+  if (sweeps > 1024) return s->fail("contact_sweeps above 1024");
+  if (s->feat.sweeps != (int)sweeps) {
+    if (!set_device(s)) return 1;
+    s->feat.sweeps = (int)sweeps;
+    s->invalidate();
+  }
+  return 0;
+}
+int phz_contact_sweeps(const phz_sim* s) { return s ? s->feat.sweeps : 0; }
+
+int phz_readback_contact_state(phz_sim* s, double* cs, double* ext) {
+  if (!s) return 1;
+  if (!s->feat.contact) return s->fail("ground contact not enabled — call enable_ground_contact first");
+  if (!cs) return s->fail("null output");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  const int nb = s->model.nb;
+  const size_t W = (size_t)s->nworld;
+  std::vector<double> rows(W * nb * 8), imp;
+  if (!s->download_rows(s->rows, rows.data(), nb * 8, "readback contact rows")) return 1;
+  if (s->imp_buf) {
+    imp.resize(W * nb * 48);
+    if (!s->download_rows(s->imp_buf, imp.data(), nb * 48, "readback impulses")) return 1;
+  }
+  for (size_t w = 0; w < W; w++)
+    for (int i = 0; i < nb; i++) {
+      double* o = cs + (w * nb + i) * 56;
+      std::memcpy(o, &rows[(w * nb + i) * 8], 8 * sizeof(double));
+      for (int k = 0; k < 48; k++) o[8 + k] = imp.empty() ? 0.0 : imp[(w * nb + i) * 48 + k];
+    }
+  if (ext) {
+    if (s->ext_buf) return s->download_rows(s->ext_buf, ext, nb * 6, "readback contact forces") ? 0 : 1;
+    std::memset(ext, 0, W * nb * 6 * sizeof(double));
+  }
+  return 0;
+}
+
+int phz_load_contact_state(phz_sim* s, const double* cs, const double* ext) {
+  if (!s) return 1;
+  if (!s->feat.contact || s->feat.cmode != 1)
+    return s->fail("impulse contact not enabled — call enable_contact_impulse first");
+  if (!cs) return s->fail("null contact state");
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  const int nb = s->model.nb;
+  const size_t W = (size_t)s->nworld;
+  std::vector<double> rows(W * nb * 8), imp(W * nb * 48);
+  for (size_t w = 0; w < W; w++)
+    for (int i = 0; i < nb; i++) {
+      const double* c = cs + (w * nb + i) * 56;
+      std::memcpy(&rows[(w * nb + i) * 8], c, 8 * sizeof(double));
+      std::memcpy(&imp[(w * nb + i) * 48], c + 8, 48 * sizeof(double));
+    }
+  if (!s->upload_rows(rows.data(), s->rows, nb * 8, "load contact rows") ||
+      !s->upload_rows(imp.data(), s->imp_buf, nb * 48, "load impulses"))
+    return 1;
+  if (ext && !s->upload_rows(ext, s->ext_buf, nb * 6, "load contact forces")) return 1;
+  if (!ext && !s->hip_ok(phz_io_zero(s->ext_buf, (size_t)nb * 6 * s->stride * s->esize(), s->stream), "zero forces"))
+    return 1;
+  return s->hip_ok(hipStreamSynchronize(s->stream), "load_contact_state") ? 0 : 1;
 }
 
 int phz_enable_pd_control(phz_sim* s, const double* dofs, uint32_t n) {

@@ -292,3 +292,37 @@ def pack_pd_dofs(dofs: Sequence[PdDof]) -> np.ndarray:
     for i, d in enumerate(dofs):
         t[i, :5] = [d.q_index, d.v_index, d.kp, d.kd, d.max_force]
     return t
+
+
+@dataclasses.dataclass
+class BodyPlane:
+    """A contact plane welded to a body: its local +Z face at `offset`, finite
+    over +-half_x, +-half_y, reaching `max_depth` into the body; `exclude` lists
+    bodies that never touch it (BodyPlane, crates/phyz-gpu/src/contact_pipeline.rs:300-353)."""
+    body: int
+    offset: float
+    max_depth: float
+    half_x: float
+    half_y: float
+    exclude: Sequence[int] = ()
+
+    def row(self) -> np.ndarray:
+        return np.array([self.body, self.offset, self.max_depth, self.half_x, self.half_y], dtype=np.float64)
+
+
+@dataclasses.dataclass
+class Heightfield:
+    """Terrain nodes heights[iy][ix] at origin + (ix, iy) * cell, origin.z added
+    to every height (phyz_model::Heightfield, crates/phyz-model/src/heightfield.rs)."""
+    origin: Sequence[float]
+    cell: float
+    nx: int
+    ny: int
+    heights: np.ndarray
+
+    def header(self) -> np.ndarray:
+        return np.array([self.nx, self.ny, *self.origin, self.cell], dtype=np.float64)
+
+    def nodes(self) -> np.ndarray:
+        # Heights are f32 in the reference's type; carry exactly those values.
+        return np.ascontiguousarray(np.asarray(self.heights, dtype=np.float32).astype(np.float64).ravel())

@@ -101,6 +101,67 @@ class BatchSim:
                                                                _dp(geom), C.byref(n)))
         return int(n.value)
 
+    def _contact_args(self, gains, plane, heightfield, geometry):
+        if len(gains) != self.nb:
+            raise PhzError(f"body_gains has {len(gains)} entries but the model has {self.nb} bodies")
+        geom = pack_geometries(self.model)[0] if geometry is None else geometry
+        geom = np.ascontiguousarray(geom, dtype=np.float64)
+        kd = np.ascontiguousarray(np.asarray(gains, dtype=np.float64).reshape(self.nb, 2))
+        pl = None if plane is None else np.ascontiguousarray(plane.row())
+        ex = (C.c_uint32 * max(len(plane.exclude) if plane else 0, 1))(*(plane.exclude if plane else ()))
+        nex = len(plane.exclude) if plane else 0
+        hdr = None if heightfield is None else np.ascontiguousarray(heightfield.header())
+        nodes = None if heightfield is None else heightfield.nodes()
+        self._keep = (geom, kd, pl, ex, hdr, nodes)
+        return geom, kd, pl, ex, nex, hdr, nodes
+
+    def enable_ground_contact_with_plane(self, ground_height: float, friction: float, gains: Sequence,
+                                         plane=None, geometry: Optional[np.ndarray] = None) -> int:
+        return self.enable_contact_terrain(ground_height, friction, gains, plane, None, geometry)
+
+    def enable_contact_terrain(self, ground_height: float, friction: float, gains: Sequence, plane=None,
+                               heightfield=None, geometry: Optional[np.ndarray] = None) -> int:
+        geom, kd, pl, ex, nex, hdr, nodes = self._contact_args(gains, plane, heightfield, geometry)
+        n = C.c_uint32(0)
+        self._check(self._L.phz_enable_contact_terrain(self._h, float(ground_height), float(friction), _dp(kd), _dp(geom),
+                                                       _dp(pl), ex, nex, _dp(hdr), _dp(nodes), C.byref(n)))
+        return int(n.value)
+
+    def enable_contact_impulse(self, ground_height: float, friction: float, gains: Sequence, plane=None,
+                               heightfield=None, solver: Optional[Sequence[float]] = None,
+                               geometry: Optional[np.ndarray] = None) -> int:
+        geom, kd, pl, ex, nex, hdr, nodes = self._contact_args(gains, plane, heightfield, geometry)
+        sp = None if solver is None else np.ascontiguousarray(np.asarray(solver, dtype=np.float64))
+        n = C.c_uint32(0)
+        self._check(self._L.phz_enable_contact_impulse(self._h, float(ground_height), float(friction), _dp(kd), _dp(geom),
+                                                       _dp(pl), ex, nex, _dp(hdr), _dp(nodes), _dp(sp), C.byref(n)))
+        return int(n.value)
+
+    def set_heightfield(self, heightfield):
+        hdr = np.ascontiguousarray(heightfield.header())
+        nodes = heightfield.nodes()
+        self._check(self._L.phz_set_heightfield(self._h, _dp(hdr), _dp(nodes)))
+
+    @property
+    def contact_sweeps(self) -> int:
+        return int(self._L.phz_contact_sweeps(self._h))
+
+    @contact_sweeps.setter
+    def contact_sweeps(self, n: int):
+        self._check(self._L.phz_set_contact_sweeps(self._h, int(n)))
+
+    def readback_contact_state(self):
+        """(cs [nworld][nb][56], ext [nworld][nb][6]): readback rows, warm-start impulses, carried forces."""
+        cs = np.zeros((self.nworld, self.nb, 56))
+        ext = np.zeros((self.nworld, self.nb, 6))
+        self._check(self._L.phz_readback_contact_state(self._h, _dp(cs), _dp(ext)))
+        return cs, ext
+
+    def load_contact_state(self, cs, ext=None):
+        c = np.ascontiguousarray(np.asarray(cs, dtype=np.float64).reshape(self.nworld, self.nb, 56))
+        e = None if ext is None else np.ascontiguousarray(np.asarray(ext, dtype=np.float64).reshape(self.nworld, self.nb, 6))
+        self._check(self._L.phz_load_contact_state(self._h, _dp(c), _dp(e)))
+
     def enable_pd_control(self, dofs: Sequence[PdDof]):
         t = np.ascontiguousarray(pack_pd_dofs(dofs)) if len(dofs) else np.zeros((0, 8))
         self._check(self._L.phz_enable_pd_control(self._h, _dp(t) if len(dofs) else None, len(dofs)))
