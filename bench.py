@@ -19,6 +19,11 @@ committed rocprofv3 --pmc summary when one matches the workload.
 cpu_baseline: the f64 CPU oracle (a port of the reference's CPU step), threaded
 over worlds on the host cores, timed on a bounded sample of the same workload;
 it also checks one device step of the sampled worlds against the oracle.
+
+terrain_impulse (unless --no-impulse): the same measurement of workload 6, the
+ant on a rolling heightfield with impulse-mode contact (16 sweeps per step),
+131072 worlds x 1000 steps, f32, with its own roofline, CPU baseline and parity.
+control_loop (unless --no-control): the ant driven by the on-device policy.
 """
 from __future__ import annotations
 
@@ -108,39 +113,75 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
     }
 
 
-def cpu_baseline(w, sim, prec, budget_s=20.0):
-    """Oracle (f64 port of the reference CPU step) on the host cores, on a bounded
-    sample of the workload; plus a one-step parity check of the sampled worlds."""
+def device_step_parity(w, sim, prec):
+    """One more device step from the benchmark's late states against the oracle,
+    on 64 sampled worlds: the device's own noisy torques (read back after the
+    step) drive an oracle without the noise stream; impulse mode also starts
+    from the device's carried contact forces and warm-start impulses."""
+    import dataclasses
     from tests.helpers import as_precision, oracle_for, rel_err_rows
-    threads = max(1, min(16, os.cpu_count() or 1))
-    orc = oracle_for(w)
-    # Parity: one more device step from the benchmark's late states, sampled worlds.
+    idx = np.linspace(0, w.nworld - 1, 64).astype(int)
+    imp = w.impulse_sweeps > 0
     qg, vg = sim.readback_states()
+    if imp:
+        cs0, ext0 = sim.readback_contact_state()
+        cs0, ext0 = np.ascontiguousarray(cs0[idx]), np.ascontiguousarray(ext0[idx])
     sim.step()
     ctrl = as_precision(sim.readback_controls(), prec)
     qdd = sim.readback_qdd()
-    idx = np.linspace(0, w.nworld - 1, 64).astype(int)
-    ext = [orc.contact(qg[k], vg[k])[0] if w.contact is not None else None for k in idx]
-    want = np.stack([orc.aba(qg[k], vg[k], ctrl[k], ext[i]) for i, k in enumerate(idx)])
-    err = float(rel_err_rows(qdd[idx], want).max())
+    if not imp and w.heightfield is None:
+        orc = oracle_for(w)
+        ext = [orc.contact(qg[k], vg[k])[0] if w.contact is not None else None for k in idx]
+        want = np.stack([orc.aba(qg[k], vg[k], ctrl[k], ext[i]) for i, k in enumerate(idx)])
+        return {"worlds_checked": len(idx), "qdd_rel_err_max": float(rel_err_rows(qdd[idx], want).max())}
+    orc = oracle_for(dataclasses.replace(w, noise=None))
+    q, v, c = (np.ascontiguousarray(a[idx]) for a in (qg, vg, ctrl))
+    want, _ = orc.step_batch(q, v, c, 1, threads=8, ext_state=ext0 if imp else None, cs_state=cs0 if imp else None)
+    out = {"worlds_checked": len(idx), "qdd_rel_err_max": float(rel_err_rows(qdd[idx], want).max())}
+    if imp:
+        cs1, ext1 = sim.readback_contact_state()
+        es = max(float(np.abs(ext0).max()), 1.0)
+        out["contact_force_rel_err_max"] = float(np.abs(ext1[idx] - ext0).max() / es)
+        isc = max(float(np.abs(cs0[:, :, 8:]).max()), 1e-6)
+        out["impulse_rel_err_max"] = float(np.abs(cs1[idx, :, 8:] - cs0[:, :, 8:]).max() / isc)
+    return out
+
+
+def cpu_baseline(w, sim, prec, budget_s=20.0):
+    """Oracle (f64 port of the reference CPU step) on the host cores, on a bounded
+    sample of the workload; plus a one-step parity check of the sampled worlds."""
+    from tests.helpers import oracle_for
+    threads = max(1, min(16, os.cpu_count() or 1))
+    parity = device_step_parity(w, sim, prec)
+    orc = oracle_for(w)
+    imp = w.impulse_sweeps > 0
+    nb = w.model.nbodies
+
+    def carried(n):
+        return (np.zeros((n, nb, 6)), np.zeros((n, nb, 56))) if imp else (None, None)
+
     # Timing: the same workload's initial states, n worlds x s steps within the budget.
     n = min(w.nworld, 4096)
     q, v, c, tg = w.initial_state(n)
     rng = orc.rng_states(n)
+    e, cs = carried(n)
     t0 = time.perf_counter()
-    orc.step_batch(q, v, c, 2, targets=tg, rng=rng, threads=threads)
+    orc.step_batch(q, v, c, 2, targets=tg, rng=rng, threads=threads, ext_state=e, cs_state=cs)
     probe = time.perf_counter() - t0
     rate = 2 * n / max(probe, 1e-6)
     s = max(2, int(budget_s * rate / n))
     q, v, c, tg = w.initial_state(n)
     rng = orc.rng_states(n)
+    e, cs = carried(n)
     t0 = time.perf_counter()
-    orc.step_batch(q, v, c, s, targets=tg, rng=rng, threads=threads)
+    orc.step_batch(q, v, c, s, targets=tg, rng=rng, threads=threads, ext_state=e, cs_state=cs)
     dt = time.perf_counter() - t0
     n1 = min(n, 256)
     q1, v1, c1, tg1 = w.initial_state(n1)
+    e, cs = carried(n1)
     t1 = time.perf_counter()
-    orc.step_batch(q1, v1, c1, max(2, s // 16), targets=tg1, rng=orc.rng_states(n1), threads=1)
+    orc.step_batch(q1, v1, c1, max(2, s // 16), targets=tg1, rng=orc.rng_states(n1), threads=1, ext_state=e,
+                   cs_state=cs)
     dt1 = time.perf_counter() - t1
     cpu_model = ""
     try:
@@ -158,7 +199,7 @@ def cpu_baseline(w, sim, prec, budget_s=20.0):
         "sample": f"{w.name}: first {n} worlds x {s} steps, f64 oracle, {threads} threads ({dt:.1f} s)",
         "single_thread_value": round(n1 * max(2, s // 16) / dt1, 1),
         "cpu": cpu_model,
-    }, {"worlds_checked": len(idx), "qdd_rel_err_max": err}
+    }, parity
 
 
 def run_control_loop(prec: str, reps: int, with_cpu: bool):
@@ -260,6 +301,58 @@ def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
             "control_steps_per_s": round(nworld * n_control / dt, 1)}
 
 
+def config_of(w, r):
+    c = {"workload": w.name, "config_index": w.index, "nworld": w.nworld, "bodies": w.model.nbodies,
+         "nv": w.model.nv, "dt": w.model.dt, "steps_per_launch": r["roofline"]["steps_per_launch"]}
+    if w.heightfield is not None:
+        h = w.heightfield
+        c["heightfield"] = {"nx": h.nx, "ny": h.ny, "cell": h.cell}
+    if w.impulse_sweeps > 0:
+        c["contact"] = {"mode": "impulse", "sweeps": w.impulse_sweeps}
+    return c
+
+
+def measure(w, precs, steps, warmup, reps, with_cpu):
+    """Event-timed spans of `steps` steps per precision, the roofline of the step
+    kernel, and (with_cpu) the oracle's CPU rate plus a one-step parity check."""
+    flops_tab = json.load(open(FLOPS_JSON))
+    traffic_tab = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else None
+    primary = "f32" if "f32" in precs else precs[0]
+    results = {}
+    sims = {}
+    for prec in precs:
+        log(f"[bench] {w.name} {prec}: {w.nworld} worlds, warmup {warmup}, timed {steps} steps")
+        sim, wall, ev, info, warm_done = run_gpu(w, prec, steps, warmup, reps)
+        sims[prec] = sim
+        ws = w.nworld * steps / wall
+        med = float(np.median(ev))
+        spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
+        results[prec] = {
+            "value": round(ws, 1),
+            "ms_per_step": round(wall * 1e3 / steps, 6),
+            "event_ms_per_span": {"median": round(med, 4), "min": round(float(min(ev)), 4),
+                                  "max": round(float(max(ev)), 4), "reps": len(ev), "noisy": bool(spread > 0.25)},
+            "world_steps_per_s_event_median": round(w.nworld * steps / (med / 1e3), 1),
+            "roofline": roofline(w, prec, steps, ev, info, flops_tab, traffic_tab),
+            "kernel": info,
+            "warmup_steps_run": warm_done,
+        }
+        log(f"[bench] {w.name} {prec}: {ws:.4g} world-steps/s, {results[prec]['roofline']['achieved']:.3f} TFLOP/s "
+            f"({100 * results[prec]['roofline']['frac']:.2f}% of peak)")
+    cpu = None
+    parity = {}
+    if with_cpu:
+        for prec in precs:
+            log(f"[bench] {w.name}: cpu_baseline + parity check ({prec})")
+            c, p = cpu_baseline(w, sims[prec], prec)
+            parity[prec] = p
+            if prec == primary:
+                cpu = c
+    for sim in sims.values():
+        sim.close()
+    return {"primary": primary, "results": results, "cpu": cpu, "parity": parity}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,6 +362,8 @@ def main():
     ap.add_argument("--reps", type=int, default=7)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-control", action="store_true", help="skip the on-device control-loop measurement")
+    ap.add_argument("--no-impulse", action="store_true",
+                    help="skip the terrain + impulse-contact measurement (workload 6)")
     ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
     ap.add_argument("--precision", choices=["f32", "f64"], default=None, help="run one precision only")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -299,68 +394,45 @@ def main():
         args.steps = w.nsteps
     if args.warmup is None:
         args.warmup = args.steps
-    flops_tab = json.load(open(FLOPS_JSON))
-    traffic_tab = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else None
     precs = [args.precision] if args.precision else list(w.precisions)
-    primary = "f32" if "f32" in precs else precs[0]
-    results = {}
-    sims = {}
-    for prec in precs:
-        log(f"[bench] {w.name} {prec}: {w.nworld} worlds, warmup {args.warmup}, timed {args.steps} steps")
-        sim, wall, ev, info, warm_done = run_gpu(w, prec, args.steps, args.warmup, args.reps)
-        sims[prec] = sim
-        ws = w.nworld * args.steps / wall
-        med = float(np.median(ev))
-        spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
-        results[prec] = {
-            "value": round(ws, 1),
-            "ms_per_step": round(wall * 1e3 / args.steps, 6),
-            "event_ms_per_span": {"median": round(med, 4), "min": round(float(min(ev)), 4),
-                                  "max": round(float(max(ev)), 4), "reps": len(ev), "noisy": bool(spread > 0.25)},
-            "world_steps_per_s_event_median": round(w.nworld * args.steps / (med / 1e3), 1),
-            "roofline": roofline(w, prec, args.steps, ev, info, flops_tab, traffic_tab),
-            "kernel": info,
-            "warmup_steps_run": warm_done,
-        }
-        log(f"[bench] {prec}: {ws:.4g} world-steps/s, {results[prec]['roofline']['achieved']:.3f} TFLOP/s "
-            f"({100 * results[prec]['roofline']['frac']:.2f}% of peak)")
-    cpu = None
-    parity = {}
-    if not args.no_cpu:
-        for prec in precs:
-            log(f"[bench] cpu_baseline + parity check ({prec})")
-            c, p = cpu_baseline(w, sims[prec], prec)
-            parity[prec] = p
-            if prec == primary:
-                cpu = c
-    r = results[primary]
+    r = measure(w, precs, args.steps, args.warmup, args.reps, not args.no_cpu)
+    primary = r["primary"]
+    p = r["results"][primary]
     line = {
         "metric": METRIC,
-        "value": r["value"],
+        "value": p["value"],
         "unit": "world-steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": r["ms_per_step"],
+        "ms_per_step": p["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": primary,
         "data": "synthetic",
-        "config": {"workload": w.name, "config_index": w.index, "nworld": w.nworld, "bodies": w.model.nbodies,
-                   "nv": w.model.nv, "dt": w.model.dt, "steps_per_launch": r["roofline"]["steps_per_launch"]},
-        "roofline": r["roofline"],
-        "cpu_baseline": cpu,
-        "event_ms_per_span": r["event_ms_per_span"],
-        "kernel": r["kernel"],
+        "config": config_of(w, p),
+        "roofline": p["roofline"],
+        "cpu_baseline": r["cpu"],
+        "event_ms_per_span": p["event_ms_per_span"],
+        "kernel": p["kernel"],
     }
-    if cpu:
-        line["gpu_over_cpu"] = round(r["value"] / cpu["value"], 1)
+    if r["cpu"]:
+        line["gpu_over_cpu"] = round(p["value"] / r["cpu"]["value"], 1)
     for prec in precs:
         if prec != primary:
-            line[prec] = results[prec]
-    if parity:
-        line["parity"] = parity
+            line[prec] = r["results"][prec]
+    if r["parity"]:
+        line["parity"] = r["parity"]
+    if not args.no_impulse and args.workload != 6:
+        wi = W.config(6)
+        ri = measure(wi, ["f32"], wi.nsteps, wi.nsteps, min(args.reps, 5), not args.no_cpu)
+        pi = ri["results"]["f32"]
+        line["terrain_impulse"] = {"value": pi["value"], "unit": "world-steps/s", "dtype": "f32",
+                                   "ms_per_step": pi["ms_per_step"], "config": config_of(wi, pi),
+                                   "roofline": pi["roofline"], "cpu_baseline": ri["cpu"],
+                                   "event_ms_per_span": pi["event_ms_per_span"], "kernel": pi["kernel"],
+                                   "parity": ri["parity"].get("f32")}
     if not args.no_control:
         line["control_loop"] = run_control_loop("f32", min(args.reps, 5), not args.no_cpu)
     print(json.dumps(line), flush=True)

@@ -59,7 +59,7 @@ def lib():
         L.orc_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, dp, dp, dp, u64p, dp, dp, C.c_int, C.c_int, dp, dp]
         L.orc_set_contact_cfg.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, C.c_int, dp, C.c_int, C.c_int, dp, dp]
         L.orc_contact_pass.argtypes = [C.c_void_p, dp, dp, dp, dp, dp]
-        L.orc_count_ops.argtypes = [C.c_void_p, dp, dp, dp, dp, C.c_uint64, C.c_int, u64p]
+        L.orc_count_ops.argtypes = [C.c_void_p, dp, dp, dp, dp, C.c_uint64, C.c_int, u64p, dp, dp]
         _lib = L
     return _lib
 
@@ -229,13 +229,16 @@ class Oracle:
                              _d(rows), int(threads), 1 if dense else 0, _d(ext_state), _d(cs_state))
         return qdd, rows
 
-    def count_ops(self, q, v, ctrl, targets=None, rng_state=1, dense=False):
-        """Per-phase operation counts of one world-step: {phase: {counter: n}}."""
+    def count_ops(self, q, v, ctrl, targets=None, rng_state=1, dense=False, ext_state=None, cs_state=None):
+        """Per-phase operation counts of one world-step: {phase: {counter: n}}.
+        ext_state [nb][6] / cs_state [nb][56]: impulse-mode carried state (default zero)."""
         c = np.zeros(len(PHASES) * len(COUNTERS), dtype=np.uint64)
         tg = np.ascontiguousarray(targets if targets is not None else np.zeros(max(self.n_pd, 1)), dtype=np.float64)
+        e = None if ext_state is None else np.ascontiguousarray(np.asarray(ext_state, dtype=np.float64).reshape(self.nb, 6))
+        s = None if cs_state is None else np.ascontiguousarray(np.asarray(cs_state, dtype=np.float64).reshape(self.nb, 56))
         lib().orc_count_ops(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)),
                             _d(np.ascontiguousarray(ctrl, dtype=np.float64)), _d(tg), int(rng_state), 1 if dense else 0,
-                            c.ctypes.data_as(u64p))
+                            c.ctypes.data_as(u64p), _d(e), _d(s))
         c = c.reshape(len(PHASES), len(COUNTERS))
         return {p: {k: int(c[i, j]) for j, k in enumerate(COUNTERS)} for i, p in enumerate(PHASES)}
 

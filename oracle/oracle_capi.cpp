@@ -237,8 +237,10 @@ int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, d
 // Count operations of one world-step at the given state (struct formulation
 // when mode 0, dense when mode 1). counts: 5 phases x 6 counters
 // (add, mul, div, sqrt, trans, other), phases: noise, pd, contact, aba, integrate.
+// ext0 [nb][6] / cs0 [nb][56]: impulse-mode carried state (nullable: zero);
+// its values count as state.
 int orc_count_ops(orc_model* o, const double* q0, const double* v0, const double* ctrl0, const double* targets0,
-                  uint64_t rng_state, int mode, uint64_t* counts) {
+                  uint64_t rng_state, int mode, uint64_t* counts, const double* ext0, const double* cs0) {
   const Model& m = o->m;
   std::vector<OpScalar> q(m.nq), v(m.nv), ctrl(m.nv), tg(m.pd.size());
   for (int j = 0; j < m.nq; j++) q[j] = OpScalar::state(q0[j]);
@@ -255,7 +257,9 @@ int orc_count_ops(orc_model* o, const double* q0, const double* v0, const double
     last = c;
   };
   WorldScratch<OpScalar> ws;
-  std::vector<OpScalar> rows(m.nb * CONTACT_ROW);
+  ws.reset(m);
+  if (ext0) for (int i = 0; i < m.nb; i++) for (int k = 0; k < 6; k++) ws.ext[i].set(k, OpScalar::state(ext0[i * 6 + k]));
+  if (cs0) for (size_t k = 0; k < ws.cs.size(); k++) ws.cs[k] = OpScalar::state(cs0[k]);
   uint64_t r = rng_state;
   step_world<OpScalar>(m, q.data(), v.data(), ctrl.data(), tg.data(), m.noise ? &r : nullptr, ws, nullptr, mode == 1,
                        hook);

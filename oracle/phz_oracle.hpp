@@ -814,17 +814,37 @@ template <class S> SymI<S> sym_add(const SymI<S>& x, const SymI<S>& y) {
   return r;
 }
 
-template <class S> void aba_struct(const Model& m, const S* q, const S* v, const S* ctrl, const SV<S>* ext, S* qdd) {
-  const int nb = m.nb;
-  std::vector<S> qfrc(m.nv);
-  generalized_forces(m, q, v, ctrl, qfrc.data());
-  std::vector<Xf<S>> xt(nb);
-  std::vector<SV<S>> vel(nb), cb(nb), pa(nb), acc(nb);
-  std::vector<SymI<S>> ia(nb);
-  std::vector<int> has_child(nb, 0);
-  for (int i = 0; i < nb; i++) if (m.bodies[i].parent >= 0) has_child[m.bodies[i].parent] = 1;
+// What a second solve with other external forces can reuse (q, v, ctrl fixed):
+// transforms, velocities, bias forces, the joint factorizations and I_a c.
+template <class S> struct AbaCache {
+  std::vector<S> qfrc;
+  std::vector<Xf<S>> xt;
+  std::vector<SV<S>> vel, cb, bias, iac;
   struct JointSolve { S U[36]; S L[36]; S Dd[6]; S u[6]; bool ok; };  // Dd holds 1/d_j
-  std::vector<JointSolve> js(nb);
+  std::vector<JointSolve> js;
+};
+
+// The structure-exploiting ABA (same equations as aba.rs:117-368): symmetric
+// articulated inertias, X^T I X as rotate-then-translate, LDL^T joint solves.
+// Fills `c` for aba_resolve.
+template <class S>
+void aba_factor(const Model& m, const S* q, const S* v, const S* ctrl, const SV<S>* ext, S* qdd, AbaCache<S>& c) {
+  const int nb = m.nb;
+  c.qfrc.assign(m.nv, S(0.0));
+  std::vector<S>& qfrc = c.qfrc;
+  generalized_forces(m, q, v, ctrl, qfrc.data());
+  c.xt.assign(nb, Xf<S>());
+  c.vel.assign(nb, SV<S>());
+  c.cb.assign(nb, SV<S>());
+  c.bias.assign(nb, SV<S>());
+  c.iac.assign(nb, SV<S>());
+  c.js.assign(nb, typename AbaCache<S>::JointSolve());
+  std::vector<Xf<S>>& xt = c.xt;
+  std::vector<SV<S>>& vel = c.vel;
+  std::vector<SV<S>>& cb = c.cb;
+  std::vector<SV<S>> pa(nb), acc(nb);
+  std::vector<SymI<S>> ia(nb);
+  auto& js = c.js;
   SV<S> a0;
   a0.lin = V3<S>{S(-m.gravity[0]), S(-m.gravity[1]), S(-m.gravity[2])};
   for (int j = 0; j < m.nv; j++) qdd[j] = S(0.0);
@@ -837,13 +857,14 @@ template <class S> void aba_struct(const Model& m, const S* q, const S* v, const
     else { vel[i] = apply_motion(xt[i], vel[b.parent]) + vj; cb[i] = cross_motion(vel[i], vj); }
     SM<S> I = rigid_inertia<S>(b);
     pa[i] = cross_force(vel[i], mul(I, vel[i]));
+    c.bias[i] = pa[i];
     if (ext) pa[i] = pa[i] - ext[i];
     ia[i] = sym_from(I);
   }
   for (int i = nb - 1; i >= 0; i--) {
     const Body& b = m.bodies[i];
     int nd = joint_ndof(b.jtype);
-    JointSolve& J = js[i];
+    auto& J = js[i];
     J.ok = true;
     SymI<S> Ia = ia[i];
     SV<S> pA = pa[i];
@@ -909,7 +930,8 @@ template <class S> void aba_struct(const Model& m, const S* q, const S* v, const
       // pa = p_A + Ia c + W u
       SV<S> wu;
       for (int r = 0; r < 6; r++) { S s0 = S(0.0); for (int k = 0; k < nd; k++) s0 = s0 + W[k * 6 + r] * J.u[k]; wu.set(r, s0); }
-      pA = pA + sym_mul(Ia, cb[i]) + wu;
+      c.iac[i] = sym_mul(Ia, cb[i]);
+      pA = pA + c.iac[i] + wu;
     } else if (b.parent < 0) {
       continue;
     }
@@ -920,7 +942,62 @@ template <class S> void aba_struct(const Model& m, const S* q, const S* v, const
     const Body& b = m.bodies[i];
     int nd = joint_ndof(b.jtype);
     SV<S> ap = apply_motion(xt[i], b.parent < 0 ? a0 : acc[b.parent]) + cb[i];
-    const JointSolve& J = js[i];
+    const auto& J = js[i];
+    if (nd == 0 || !J.ok) { acc[i] = ap; continue; }
+    S y[6];
+    for (int k = 0; k < nd; k++) {
+      S uta = S(0.0);
+      for (int t = 0; t < 6; t++) uta = uta + J.U[k * 6 + t] * ap.get(t);
+      y[k] = J.u[k] - uta;
+      for (int t = 0; t < k; t++) y[k] = y[k] - J.L[k * nd + t] * y[t];
+    }
+    for (int k = 0; k < nd; k++) y[k] = y[k] * J.Dd[k];
+    for (int k = nd - 1; k >= 0; k--) for (int t = k + 1; t < nd; t++) y[k] = y[k] - J.L[t * nd + k] * y[t];
+    for (int k = 0; k < nd; k++) { qdd[b.voff + k] = y[k]; ap = ap + subspace_col<S>(b, k) * y[k]; }
+    acc[i] = ap;
+  }
+}
+
+template <class S> void aba_struct(const Model& m, const S* q, const S* v, const S* ctrl, const SV<S>* ext, S* qdd) {
+  AbaCache<S> c;
+  aba_factor(m, q, v, ctrl, ext, qdd, c);
+}
+
+// The force-dependent half of aba_factor for new external forces: with q, v,
+// ctrl unchanged the articulated inertias, U, D and I_a c are the same, so only
+// u = tau - S^T p_A, p_a = p_A + I_a c + U D^-1 u and pass 3 are redone. Used by
+// the impulse sweeps; algebraically identical to a full solve.
+template <class S> void aba_resolve(const Model& m, AbaCache<S>& c, const SV<S>* ext, S* qdd) {
+  const int nb = m.nb;
+  std::vector<SV<S>> pa(nb), acc(nb);
+  SV<S> a0;
+  a0.lin = V3<S>{S(-m.gravity[0]), S(-m.gravity[1]), S(-m.gravity[2])};
+  for (int i = 0; i < nb; i++) pa[i] = ext ? c.bias[i] - ext[i] : c.bias[i];
+  for (int i = nb - 1; i >= 0; i--) {
+    const Body& b = m.bodies[i];
+    const int nd = joint_ndof(b.jtype);
+    auto& J = c.js[i];
+    SV<S> pA = pa[i];
+    if (nd > 0) {
+      for (int k = 0; k < nd; k++) J.u[k] = c.qfrc[b.voff + k] - dot(subspace_col<S>(b, k), pa[i]);
+      if (!J.ok || b.parent < 0) continue;
+      S y[6];
+      for (int k = 0; k < nd; k++) { y[k] = J.u[k]; for (int t = 0; t < k; t++) y[k] = y[k] - J.L[k * nd + t] * y[t]; }
+      for (int k = 0; k < nd; k++) y[k] = y[k] * J.Dd[k];
+      for (int k = nd - 1; k >= 0; k--) for (int t = k + 1; t < nd; t++) y[k] = y[k] - J.L[t * nd + k] * y[t];
+      SV<S> wu;
+      for (int r = 0; r < 6; r++) { S s0 = S(0.0); for (int k = 0; k < nd; k++) s0 = s0 + J.U[k * 6 + r] * y[k]; wu.set(r, s0); }
+      pA = pA + c.iac[i] + wu;
+    } else if (b.parent < 0) {
+      continue;
+    }
+    pa[b.parent] = pa[b.parent] + inv_apply_force(c.xt[i], pA);
+  }
+  for (int i = 0; i < nb; i++) {
+    const Body& b = m.bodies[i];
+    const int nd = joint_ndof(b.jtype);
+    SV<S> ap = apply_motion(c.xt[i], b.parent < 0 ? a0 : acc[b.parent]) + c.cb[i];
+    const auto& J = c.js[i];
     if (nd == 0 || !J.ok) { acc[i] = ap; continue; }
     S y[6];
     for (int k = 0; k < nd; k++) {
@@ -1029,6 +1106,15 @@ template <class S> void forward_kinematics(const Model& m, const S* q, const S* 
       out[i].w_pos = p.w_pos + p.w_rot * x.pos;
       out[i].vel = apply_motion(x, p.vel) + vj;
     }
+  }
+}
+// Body velocities for other joint velocities at the same q: the tree
+// transforms (and out[].w_rot / w_pos) are reused.
+template <class S> void fk_velocity(const Model& m, const std::vector<Xf<S>>& xt, const S* v, FK<S>* out) {
+  for (int i = 0; i < m.nb; i++) {
+    const Body& b = m.bodies[i];
+    SV<S> vj = joint_velocity<S>(b, v);
+    out[i].vel = b.parent < 0 ? vj : apply_motion(xt[i], out[b.parent].vel) + vj;
   }
 }
 inline double fsign(double x) { return x > 0.0 ? 1.0 : (x < 0.0 ? -1.0 : 0.0); }
@@ -1459,6 +1545,7 @@ template <class S> struct WorldScratch {
   std::vector<S> qdd;
   std::vector<S> cs;       // impulse mode: nb x 56 contact state with warm-start impulses, persistent
   std::vector<S> vfree;
+  AbaCache<S> cache;       // impulse mode: the step's ABA factorization, reused by the sweeps
   void reset(const Model& m) {
     fk.assign(m.nb, FK<S>());
     ext.assign(m.nb, SV<S>());
@@ -1491,15 +1578,33 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
     // Impulse mode (mod.rs:899-928): a leading ABA with the previous step's
     // contact forces, then `sweeps` x [contact at the free velocity
     // v + dt qdd, ABA]; each contact pass warm-starts from the last.
-    aba(ws.ext.data());
-    hook(PH_ABA);
-    for (int sw = 0; sw < m.cc.sweeps; sw++) {
-      for (int k = 0; k < m.nv; k++) ws.vfree[k] = v[k] + S(m.dt) * ws.qdd[k];
-      forward_kinematics(m, q, ws.vfree.data(), ws.fk.data());
-      contact_pass(m, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
-      hook(PH_CONTACT);
+    // dense: every sweep is a full solve (the reference's sequencing);
+    // otherwise the kernels' split form: transforms, bias forces and joint
+    // factorizations once, then per sweep only the velocities at v + dt qdd
+    // and the force-dependent half of the ABA (aba_resolve).
+    if (dense) {
       aba(ws.ext.data());
       hook(PH_ABA);
+      for (int sw = 0; sw < m.cc.sweeps; sw++) {
+        for (int k = 0; k < m.nv; k++) ws.vfree[k] = v[k] + S(m.dt) * ws.qdd[k];
+        forward_kinematics(m, q, ws.vfree.data(), ws.fk.data());
+        contact_pass(m, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
+        hook(PH_CONTACT);
+        aba(ws.ext.data());
+        hook(PH_ABA);
+      }
+    } else {
+      aba_factor(m, q, v, ctrl, ws.ext.data(), ws.qdd.data(), ws.cache);
+      forward_kinematics(m, q, v, ws.fk.data());
+      hook(PH_ABA);
+      for (int sw = 0; sw < m.cc.sweeps; sw++) {
+        for (int k = 0; k < m.nv; k++) ws.vfree[k] = v[k] + S(m.dt) * ws.qdd[k];
+        fk_velocity(m, ws.cache.xt, ws.vfree.data(), ws.fk.data());
+        contact_pass(m, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
+        hook(PH_CONTACT);
+        aba_resolve(m, ws.cache, ws.ext.data(), ws.qdd.data());
+        hook(PH_ABA);
+      }
     }
   } else {
     const SV<S>* ext = nullptr;

@@ -360,7 +360,12 @@ def from_workload(w, precision: str, nworld: Optional[int] = None, device: int =
     """A BatchSim configured for a phyz_amd.workloads.Workload (contact, PD, control noise)."""
     n = w.nworld if nworld is None else nworld
     sim = BatchSim(w.model, n, precision, device)
-    if w.contact is not None:
+    if w.contact is not None and w.impulse_sweeps > 0:
+        sim.enable_contact_impulse(w.contact.ground_height, w.contact.friction, w.contact_gains(), None, w.heightfield)
+        sim.contact_sweeps = w.impulse_sweeps
+    elif w.contact is not None and w.heightfield is not None:
+        sim.enable_contact_terrain(w.contact.ground_height, w.contact.friction, w.contact_gains(), None, w.heightfield)
+    elif w.contact is not None:
         sim.enable_ground_contact(w.contact.ground_height, w.contact.stiffness, w.contact.damping, w.contact.friction)
     if w.pd is not None:
         sim.enable_pd_control(w.pd)

@@ -23,6 +23,10 @@ crates/phyz-gpu/src/policy_pipeline.rs:417-456), which the oracle replays.
   5 hand             fixed palm + 24 revolute DOF in 5 fingers (5,5,5,5,4);
                      m 0.01-0.05 kg, L 0.02-0.05 m; PD servos on every DOF with
                      per-world targets; dt 5e-4. 16384 worlds x 2000 steps, f64.
+  6 ant_terrain_impulse  workload 3 on a 41 x 41 node rolling heightfield (8 m
+                     square, +-0.06 m) with impulse-mode contact: a leading ABA,
+                     then 16 sweeps of [contact at the free velocity, ABA re-solve]
+                     per step (mod.rs:899-928). 131072 worlds x 1000 steps, f32.
 """
 from __future__ import annotations
 
@@ -32,8 +36,8 @@ from typing import List, Optional, Tuple
 
 import numpy as np
 
-from .model import (BALL, FIXED, FREE, PRISMATIC, REVOLUTE, Geometry, Joint, Model, ModelBuilder, PdDof,
-                    SpatialInertia, SpatialTransform, pack_geometries, pack_pd_dofs, rotation_axis_angle)
+from .model import (BALL, FIXED, FREE, PRISMATIC, REVOLUTE, Geometry, Heightfield, Joint, Model, ModelBuilder,
+                    PdDof, SpatialInertia, SpatialTransform, pack_geometries, pack_pd_dofs, rotation_axis_angle)
 
 NOISE_NORMAL = 0
 NOISE_UNIFORM = 1
@@ -69,6 +73,8 @@ class Workload:
     noise: Optional[Noise] = None
     init_seed: int = 0
     _init: Optional[object] = None
+    heightfield: Optional[Heightfield] = None  # terrain in place of the flat ground
+    impulse_sweeps: int = 0                    # > 0: impulse-mode contact with this many sweeps
 
     def initial_state(self, nworld: Optional[int] = None):
         """World-major f64 (q, v, ctrl, targets|None) for the first `nworld` worlds."""
@@ -80,6 +86,15 @@ class Workload:
         if self.contact is None:
             return None, 0
         return pack_geometries(self.model, self.contact.stiffness, self.contact.damping)
+
+    def contact_gains(self):
+        """Per-body (stiffness, damping): the workload's ground gains on every body."""
+        return [(self.contact.stiffness, self.contact.damping)] * self.model.nbodies
+
+    def impulse_erp(self) -> float:
+        """Baumgarte factor of impulse mode: dt / (2 * 0.02 * 1 + dt), time constant
+        0.02 s, damping ratio 1 (the impulse-mode default of mod.rs:680-701)."""
+        return self.model.dt / (0.04 + self.model.dt)
 
     def pd_table(self):
         return None if self.pd is None else pack_pd_dofs(self.pd)
@@ -298,10 +313,35 @@ def config(index: int) -> Workload:
         m, kp, kd = hand_model()
         pd = [PdDof(j, j, kp, kd, kp * math.pi) for j in range(m.nv)]
         return Workload(5, "hand", m, 16384, 2000, ("f64",), pd=pd, init_seed=105, _init=_init_hand)
+    if index == 6:
+        w = config(3)
+        return dataclasses.replace(w, index=6, name="ant_terrain_impulse", heightfield=rolling_terrain(),
+                                   impulse_sweeps=16)
     raise ValueError(f"no workload {index}")
 
 
+# The reference's five benchmark configurations; EXTRA are contact-mode
+# workloads beyond them (heightfield terrain, impulse solve).
 ALL = (1, 2, 3, 4, 5)
+EXTRA = (6,)
+
+
+# ── 6: ant on rolling terrain, impulse-mode contact ─────────────────────────
+def rolling_terrain(n: int = 41, cell: float = 0.2, amp: float = 0.06, seed: int = 6) -> Heightfield:
+    """An n x n node heightfield, 8 m square centred on the origin: a seeded sum
+    of six plane waves of 1.5-4 m wavelength, peak-to-peak about 2 amp."""
+    rng = np.random.default_rng(seed)
+    xs = (np.arange(n) - (n - 1) / 2) * cell
+    X, Y = np.meshgrid(xs, xs)  # [iy][ix]
+    h = np.zeros((n, n))
+    for _ in range(6):
+        lam = rng.uniform(1.5, 4.0)
+        th = rng.uniform(0.0, 2 * math.pi)
+        ph = rng.uniform(0.0, 2 * math.pi)
+        k = 2 * math.pi / lam
+        h += np.sin(k * (math.cos(th) * X + math.sin(th) * Y) + ph)
+    h *= amp / np.abs(h).max()
+    return Heightfield(origin=(float(xs[0]), float(xs[0]), 0.0), cell=cell, nx=n, ny=n, heights=h)
 
 
 # ── control loop: the ant driven by an on-device policy ─────────────────────

@@ -11,7 +11,12 @@ away. FLOPs = add + mul + div + sqrt (an FMA counts 2); transcendentals
 (the reference's literal 6x6 formulation) is recorded beside it.
 
 Contact workloads are counted at a state where the contact bodies are touching
-(after a seeded oracle rollout), so the contact law is included.
+(after a seeded oracle rollout), so the contact law is included. Impulse-mode
+workloads are counted in the split form the kernels run (one factorization,
+then per sweep the free-velocity body velocities, the contact pass and the
+force-only ABA re-solve) with the carried forces and warm-start impulses of
+that rollout; their bytes add the round trip of that carried state for the
+bodies with a shape.
 
 Bytes per world-step are the state round trip of a one-step-per-launch design:
 read q, v (and ctrl or targets when the step reads them), write q, v, in the
@@ -39,20 +44,26 @@ OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flops_per_world_
 def count(w, warm):
     orc = oracle_for(w)
     q, v, c, tg = w.initial_state(64)
+    nb = w.model.nbodies
+    ext, cs = np.zeros((64, nb, 6)), np.zeros((64, nb, 56))
+    imp = w.impulse_sweeps > 0
     if warm:
-        orc.step_batch(q, v, c, warm, targets=tg, rng=orc.rng_states(64), threads=8)
+        orc.step_batch(q, v, c, warm, targets=tg, rng=orc.rng_states(64), threads=8,
+                       ext_state=ext if imp else None, cs_state=cs if imp else None)
     k = 0
     if w.contact is not None:
-        _, rows = orc.contact(q[0], v[0])
-        for k in range(64):
-            _, rows = orc.contact(q[k], v[k])
-            if rows[:, 0].sum() >= 2:
-                break
+        # The first world with at least two bodies in contact (carried state
+        # included in impulse mode, where a probe step decides it).
+        probe = [q.copy(), v.copy(), c.copy(), ext.copy(), cs.copy()]
+        _, rows = orc.step_batch(*probe[:3], 1, targets=tg, rng=orc.rng_states(64), threads=8, want_contacts=True,
+                                 ext_state=probe[3] if imp else None, cs_state=probe[4] if imp else None)
+        k = int(np.argmax((rows[:, :, 0] > 0).sum(axis=1) >= 2))
     tgk = None if tg is None else tg[k]
     rng = orc.rng_states(1)[0] if w.noise is not None else 1
     res = {}
     for mode in ("struct", "dense"):
-        ops = orc.count_ops(q[k], v[k], c[k], targets=tgk, rng_state=int(rng), dense=(mode == "dense"))
+        ops = orc.count_ops(q[k], v[k], c[k], targets=tgk, rng_state=int(rng), dense=(mode == "dense"),
+                            ext_state=ext[k] if imp else None, cs_state=cs[k] if imp else None)
         flops = {ph: d["add"] + d["mul"] + d["div"] + d["sqrt"] for ph, d in ops.items()}
         res[mode] = {"flops": int(sum(flops.values())), "flops_by_phase": flops,
                      "transcendental": int(sum(d["trans"] for d in ops.values())),
@@ -62,12 +73,16 @@ def count(w, warm):
 
 def main():
     out = {}
-    for idx in W.ALL:
+    for idx in W.ALL + W.EXTRA:
         w = W.config(idx)
         r = count(w, warm=300 if w.contact is not None else 0)
         nq, nv = w.model.nq, w.model.nv
         reads_ctrl = w.noise is None and w.pd is None
         per_elem = 2 * nq + 2 * nv + (nv if reads_ctrl else 0) + (len(w.pd) if w.pd else 0)
+        if w.impulse_sweeps > 0:
+            # Carried forces (6) and ground warm-start impulses (24) of each body with a shape.
+            ncb = sum(1 for b in w.model.bodies if b.geometry is not None)
+            per_elem += 2 * (6 + 24) * ncb
         out[w.name] = {
             "config": idx,
             "bodies": w.model.nbodies,

@@ -3,7 +3,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.oracle import Oracle
+from oracle.oracle import ContactCfg, Oracle
 from phyz_amd.model import pack_geometries
 
 
@@ -16,7 +16,20 @@ def oracle_for(workload, f32_uniform: bool = False) -> Oracle:
     noise = None
     if w.noise is not None:
         noise = (w.noise.seed, w.noise.dist, w.noise.a, w.noise.b, w.noise.dofs)
-    return Oracle(w.model, contact=contact, pd=w.pd_table(), noise=noise)
+    return Oracle(w.model, contact=contact, pd=w.pd_table(), noise=noise, contact_cfg=contact_cfg_for(w))
+
+
+def contact_cfg_for(w):
+    """The oracle's ContactCfg for a workload's terrain / impulse settings (None: flat penalty)."""
+    if w.contact is None or (w.heightfield is None and w.impulse_sweeps == 0):
+        return None
+    hf = None
+    if w.heightfield is not None:
+        h = w.heightfield
+        hf = (h.nx, h.ny, *h.origin, h.cell, h.nodes())
+    if w.impulse_sweeps > 0:
+        return ContactCfg(solve_mode=1, sweeps=w.impulse_sweeps, erp=w.impulse_erp(), heightfield=hf)
+    return ContactCfg(solve_mode=0, heightfield=hf)
 
 
 def as_precision(a: np.ndarray, precision: str) -> np.ndarray:

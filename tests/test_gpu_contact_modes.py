@@ -8,6 +8,8 @@ off): the state and the contact state. f64 kernels are held to 1e-10 (one
 step) and 1e-8 (rollouts); f32 kernels to the f32 floor the oracle itself shows
 against the reference (2e-4 relative).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -244,3 +246,48 @@ def test_impulse_sweep_counts(kind, prec):
         ierr = np.abs(dcs[:, :, 8:] - s1[:, :, 8:]).max() / max(np.abs(s1[:, :, 8:]).max(), 1e-6)
         print(f"{kind} {prec} sweeps {sweeps}: qdd {err:.2e} impulses {ierr:.2e}", flush=True)
         assert err <= (1e-10 if prec == "f64" else 2e-4) and ierr <= (1e-9 if prec == "f64" else 2e-4)
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+def test_terrain_impulse_workload(prec):
+    """The benchmark's terrain + impulse workload (ant, rolling heightfield, 16
+    sweeps, control noise) configured through from_workload, at 256 worlds:
+    250 device steps (noise stream replayed exactly by the oracle; the ants
+    drop from 0.5-1 m and land) from the seeded initial states, then one more step against the oracle from the
+    device's own state, carried contact forces and warm-start impulses."""
+    from phyz_amd.sim import from_workload
+    from tests.helpers import oracle_for
+    w = W.config(6)
+    n = 256
+    orc = oracle_for(w)
+    q, v, c, _ = w.initial_state(n)
+    q, v = as_precision(q, prec), as_precision(v, prec)
+    sim = from_workload(w, prec, nworld=n)
+    assert sim.contact_sweeps == 16
+    sim.load_states(q, v, c)
+    sim.step_many(250)
+    qd, vd = sim.readback_states()
+    dcs, dext = sim.readback_contact_state()
+    ext, cs = np.zeros((n, 9, 6)), np.zeros((n, 9, 56))
+    rng = orc.rng_states(n)
+    orc.step_batch(q, v, c, 250, rng=rng, threads=8, ext_state=ext, cs_state=cs)
+    touching = (dcs[:, :, 0] > 0).sum()
+    dq = np.abs(qd - q).max()
+    print(f"{prec}: 250 steps, {touching} feet touching, state q {dq:.2e}", flush=True)
+    assert touching > n  # most worlds have feet on the terrain
+    if prec == "f64":
+        assert dq <= 1e-8 and np.abs(vd - v).max() <= 1e-7 * max(1.0, np.abs(v).max())
+    # One step from the device's state with the device's noisy torques.
+    orc0 = oracle_for(dataclasses.replace(w, noise=None))
+    sim.step()
+    ctrl = as_precision(sim.readback_controls(), prec)
+    qdd = sim.readback_qdd()
+    cs1, ext1 = sim.readback_contact_state()
+    e0, s0 = np.ascontiguousarray(dext), np.ascontiguousarray(dcs)
+    want, _ = orc0.step_batch(qd.copy(), vd.copy(), ctrl, 1, threads=8, ext_state=e0, cs_state=s0)
+    err = rel_err_rows(qdd, want).max()
+    ierr = np.abs(cs1[:, :, 8:] - s0[:, :, 8:]).max() / max(np.abs(s0[:, :, 8:]).max(), 1e-6)
+    eerr = np.abs(ext1 - e0).max() / max(np.abs(e0).max(), 1.0)
+    print(f"   one step: qdd {err:.2e} impulses {ierr:.2e} forces {eerr:.2e}", flush=True)
+    assert err <= (1e-10 if prec == "f64" else 2e-4)
+    assert ierr <= (1e-9 if prec == "f64" else 2e-4) and eerr <= (1e-9 if prec == "f64" else 2e-4)

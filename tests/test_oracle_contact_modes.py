@@ -193,3 +193,48 @@ def test_impulse_sliding_box_decelerates_at_mu_g():
     orc.step_batch(q, v, c, 100, ext_state=ext, cs_state=cs)
     decel = (v0 - v[0, 3]) / (100 * m.dt)
     assert decel == pytest.approx(mu * 9.81, rel=0.02)
+
+
+@pytest.mark.parametrize("case", ["box_hf", "trunk_plane"])
+def test_split_impulse_step_equals_full_solves(case):
+    """The kernels' impulse step (one factorization, per sweep only the
+    velocities at v + dt qdd and the force-dependent half of the ABA) against
+    full solves every sweep by CRBA + Cholesky: the ABA is linear in the
+    external forces, so the two agree to f64 rounding over many steps."""
+    if case == "box_hf":
+        m = TM.shapes()["box"]
+        cfg = ContactCfg(solve_mode=1, sweeps=6, erp=m.dt / (0.04 + m.dt), heightfield=TM.bumpy_heightfield())
+        geom, _ = pack_geometries(m, gains=uniform_frequency_gains(m, 50.0, 1.0))
+        hz = geom[0, 3]
+        q0 = np.zeros((3, m.nq))
+        q0[:, 0:3] = [[0.0, 0.0, 0.0], [0.1, -0.2, 0.3], [0.4, 0.1, -0.1]]
+        q0[:, 3:5] = [[0.0, 0.0], [0.3, -0.2], [-0.4, 0.35]]
+        q0[:, 5] = hz + 0.02
+    else:
+        m = TM.deck_and_feet()
+        cfg = ContactCfg(solve_mode=1, sweeps=4, erp=m.dt / (0.04 + m.dt), plane=TM.DECK_PLANE)
+        geom, _ = pack_geometries(m, gains=uniform_frequency_gains(m, 50.0, 1.0))
+        geom[TM.DECK_PLANE[0], 7] = 1.0
+        q0 = np.zeros((2, m.nq))
+        q0[:, 5] = 0.05
+        q0[:, 6:12] = [0.1, 0.2, 0.0, 0.1, 0.0, 0.07 + 0.05 - 0.004]
+        q0[:, 12:18] = [0.0, 0.0, 0.3, -0.15, 0.02, 0.07 + 0.02 - 0.004]
+        q0[1, 3] = 0.01
+    orc = Oracle(m, contact=(geom, 0.0, 0.8), contact_cfg=cfg)
+    rng = np.random.default_rng(4)
+    n = q0.shape[0]
+    v0 = rng.normal(size=(n, m.nv)) * 0.2
+    c0 = rng.normal(size=(n, m.nv)) * 0.5
+    out = []
+    for dense in (False, True):
+        q, v, c = q0.copy(), v0.copy(), c0.copy()
+        ext, cs = np.zeros((n, m.nbodies, 6)), np.zeros((n, m.nbodies, 56))
+        qdd, _ = orc.step_batch(q, v, c, 60, dense=dense, ext_state=ext, cs_state=cs)
+        out.append((q, v, qdd, ext, cs))
+    (qa, va, da, ea, ca), (qb, vb, db, eb, cb) = out
+    assert np.abs(ea).max() > 1.0, "the bodies must be in contact"
+    assert np.abs(qa - qb).max() <= 1e-10
+    assert np.abs(va - vb).max() <= 1e-8 * max(1.0, np.abs(vb).max())
+    assert rel_err_rows(db, da).max() <= 1e-8
+    assert np.abs(ea - eb).max() <= 1e-8 * np.abs(eb).max()
+    assert np.abs(ca - cb).max() <= 1e-8 * max(1.0, np.abs(cb).max())
