@@ -1247,6 +1247,8 @@ template <class S> void contact_tangents(const V3<S>& n, V3<S>& u, V3<S>& w) {
   w = cross(n, u);
 }
 
+template <class S> void plane_pass(const Model& m, const FK<S>* fk, SV<S>* ext, S* cs);
+
 // One contact pass over a world (phyz_kernels.cu:804-1132): ground or terrain
 // contacts per body, then the body-attached plane. Penalty mode applies the
 // bounded Kelvin-Voigt law; impulse mode makes one warm-started Coulomb update
@@ -1357,8 +1359,16 @@ template <class S> void contact_pass(const Model& m, const FK<S>* fk, SV<S>* ext
     }
   }
 
-  // Body-attached plane: the plane body's local +Z face at plane_offset,
-  // acting on every other collidable body not excluded, forces on both.
+  plane_pass(m, fk, ext, cs);
+}
+
+// Body-attached plane: the plane body's local +Z face at plane_offset,
+// acting on every other collidable body not excluded, forces on both
+// (phyz_kernels.cu:982-1132). Adds to ext; cs as in contact_pass.
+template <class S> void plane_pass(const Model& m, const FK<S>* fk, SV<S>* ext, S* cs) {
+  const ContactCfg& c = m.cc;
+  const bool imp = c.solve_mode == 1;
+  const double dt = m.dt, dtc = std::max(dt, 1e-9);
   if (c.plane_body < 0) return;
   const int pb = c.plane_body;
   const M3<S>& Rp = fk[pb].w_rot;
@@ -1466,6 +1476,126 @@ template <class S> void ground_contact(const Model& m, const FK<S>* fk, SV<S>* e
   contact_pass<S>(m, fk, ext, nullptr, rows);
 }
 
+// Impulse-mode ground/terrain contact split the way the kernels run it. Within
+// one step q is fixed, so everything about a contact point except its velocity
+// is the same in every sweep: support point, terrain height and normal,
+// penetration, tangent frame, the three effective masses and the SolImp bias.
+// ground_prepare computes those once per step; ground_sweep makes the
+// velocity-dependent update per sweep. With m' = max(m_n / n_active, 1e-9),
+// c_t = max(m_t, 1e-9) / n_active, the update of contact_pass reads
+//   f_n = max((bias - v_n (1 + e)) m' + s_n, 0),  f_t = s_t - b_t c_t,
+// the same quantity as (bias - r_n) / a_nn and -(b_t - a_tt s_t) / a_tt.
+template <class S> struct GroundPoint {
+  V3<S> sup, nb, tu, tw;  // body-frame point, normal, tangents
+  S mn, cu, cw, bias;
+  bool in;
+};
+template <class S> struct GroundPrep {
+  std::vector<GroundPoint<S>> pts;
+  std::vector<int> off, np;
+  std::vector<char> any;
+  std::vector<S> row5;  // nb x 5: touching, deepest, deepest point (x, y, z)
+};
+template <class S> void ground_prepare(const Model& m, const FK<S>* fk, GroundPrep<S>& gp) {
+  const ContactCfg& c = m.cc;
+  const double dtc = std::max(m.dt, 1e-9);
+  gp.pts.clear();
+  gp.off.assign(m.nb, 0);
+  gp.np.assign(m.nb, 0);
+  gp.any.assign(m.nb, 0);
+  gp.row5.assign((size_t)m.nb * 5, S(0.0));
+  for (int i = 0; i < m.nb; i++) {
+    const Geom& g = m.geoms[i];
+    gp.off[i] = (int)gp.pts.size();
+    if (g.type == G_NONE) continue;
+    const Body& b = m.bodies[i];
+    const M3<S>& R = fk[i].w_rot;
+    V3<S> z_body{R.m[2][0], R.m[2][1], R.m[2][2]};
+    const int npts = g.type == G_BOX ? 8 : 1;
+    gp.np[i] = npts;
+    GroundPoint<S> pt[8];
+    S pen[8];
+    V3<S> supw[8];
+    int n_active = 0;
+    for (int cp = 0; cp < npts; cp++) {
+      pt[cp].sup = g.type == G_BOX ? box_corner<S>(g, cp) : support_point<S>(g, z_body);
+      supw[cp] = fk[i].w_pos + R * pt[cp].sup;
+      V3<S> n_w;
+      S th = terrain(m, supw[cp].x, supw[cp].y, n_w);
+      pen[cp] = n_w.z * (th - supw[cp].z);
+      pt[cp].in = pen[cp] > S(-c.margin);
+      pt[cp].nb = tmul(R, n_w);
+      if (pt[cp].in) n_active++;
+    }
+    const S na(double(n_active < 1 ? 1 : n_active));
+    S deepest(0.0);
+    V3<S> dw;
+    for (int cp = 0; cp < npts; cp++) {
+      GroundPoint<S>& p = pt[cp];
+      if (p.in) {
+        contact_tangents(p.nb, p.tu, p.tw);
+        p.mn = s_max(contact_eff_mass<S>(b, p.sup, p.nb) / na, S(1e-9));
+        p.cu = s_max(contact_eff_mass<S>(b, p.sup, p.tu), S(1e-9)) / na;
+        p.cw = s_max(contact_eff_mass<S>(b, p.sup, p.tw), S(1e-9)) / na;
+        p.bias = impedance_at(c, pen[cp]) * S(c.erp) * s_max(pen[cp], S(0.0)) / S(dtc);
+        gp.any[i] = 1;
+        if (pen[cp] > deepest) { deepest = pen[cp]; dw = supw[cp]; }
+      }
+      gp.pts.push_back(p);
+    }
+    if (gp.any[i]) {
+      S* r = &gp.row5[(size_t)i * 5];
+      r[0] = S(1.0); r[1] = deepest; r[2] = dw.x; r[3] = dw.y; r[4] = dw.z;
+    }
+  }
+}
+// One sweep of the prepared ground contacts at the body velocities in fk,
+// then the plane (contact_pass's order). ext is overwritten; cs and rows as in
+// contact_pass; the row's force is R times the body's summed ground force.
+template <class S> void ground_sweep(const Model& m, const GroundPrep<S>& gp, const FK<S>* fk, SV<S>* ext, S* cs,
+                                     S* rows) {
+  const ContactCfg& c = m.cc;
+  const double dtc = std::max(m.dt, 1e-9);
+  for (int i = 0; i < m.nb; i++) {
+    ext[i] = SV<S>();
+    if (!gp.any[i]) {
+      if (cs) for (int k = 0; k < CS_STRIDE; k++) cs[i * CS_STRIDE + k] = S(0.0);
+      if (rows) for (int k = 0; k < CONTACT_ROW; k++) rows[i * CONTACT_ROW + k] = S(0.0);
+      continue;
+    }
+    for (int cp = 0; cp < gp.np[i]; cp++) {
+      const GroundPoint<S>& p = gp.pts[gp.off[i] + cp];
+      S* slot = cs + i * CS_STRIDE + CS_IMPULSE_OFF + cp * 3;
+      if (!p.in) { for (int k = 0; k < 3; k++) slot[k] = S(0.0); continue; }
+      V3<S> v_pt = fk[i].vel.lin + cross(fk[i].vel.ang, p.sup);
+      S v_n = dot(v_pt, p.nb);
+      S e = effective_restitution(c, c.restitution, s_min(v_n, S(0.0)));
+      S fn = s_max((p.bias - v_n * (S(1.0) + e)) * p.mn + slot[0], S(0.0));
+      S ftu = slot[1] - dot(v_pt, p.tu) * p.cu;
+      S ftw = slot[2] - dot(v_pt, p.tw) * p.cw;
+      S limit = S(m.mu) * fn;
+      S tn = s_sqrt(ftu * ftu + ftw * ftw);
+      if (tn > limit) {
+        S scl = tn > S(0.0) ? limit / tn : S(0.0);
+        ftu = ftu * scl;
+        ftw = ftw * scl;
+      }
+      slot[0] = fn; slot[1] = ftu; slot[2] = ftw;
+      V3<S> fb = (p.nb * fn + p.tu * ftu + p.tw * ftw) * (S(1.0) / S(dtc));
+      ext[i].ang = ext[i].ang + cross(p.sup, fb);
+      ext[i].lin = ext[i].lin + fb;
+    }
+    V3<S> f_total = fk[i].w_rot * ext[i].lin;
+    const S* r5 = &gp.row5[(size_t)i * 5];
+    S row[CONTACT_ROW] = {r5[0], r5[1], r5[2], r5[3], r5[4], f_total.x, f_total.y, f_total.z};
+    for (int k = 0; k < CONTACT_ROW; k++) {
+      if (cs) cs[i * CS_STRIDE + k] = row[k];
+      if (rows) rows[i * CONTACT_ROW + k] = row[k];
+    }
+  }
+  plane_pass(m, fk, ext, cs);
+}
+
 // ─────────────────────────────────────────────────────────────────────────────
 // Semi-implicit Euler (integrate.rs:41-92): v += dt qdd, then q from the new v.
 // ─────────────────────────────────────────────────────────────────────────────
@@ -1546,6 +1676,7 @@ template <class S> struct WorldScratch {
   std::vector<S> cs;       // impulse mode: nb x 56 contact state with warm-start impulses, persistent
   std::vector<S> vfree;
   AbaCache<S> cache;       // impulse mode: the step's ABA factorization, reused by the sweeps
+  GroundPrep<S> gprep;     // impulse mode: the step's contact geometry, reused by the sweeps
   void reset(const Model& m) {
     fk.assign(m.nb, FK<S>());
     ext.assign(m.nb, SV<S>());
@@ -1578,10 +1709,11 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
     // Impulse mode (mod.rs:899-928): a leading ABA with the previous step's
     // contact forces, then `sweeps` x [contact at the free velocity
     // v + dt qdd, ABA]; each contact pass warm-starts from the last.
-    // dense: every sweep is a full solve (the reference's sequencing);
-    // otherwise the kernels' split form: transforms, bias forces and joint
-    // factorizations once, then per sweep only the velocities at v + dt qdd
-    // and the force-dependent half of the ABA (aba_resolve).
+    // dense: every sweep is a full contact pass and a full solve (the
+    // reference's sequencing); otherwise the kernels' split form: transforms,
+    // bias forces, joint factorizations and contact geometry once, then per
+    // sweep only the velocities at v + dt qdd, the velocity-dependent contact
+    // update (ground_sweep) and the force-dependent half of the ABA (aba_resolve).
     if (dense) {
       aba(ws.ext.data());
       hook(PH_ABA);
@@ -1597,10 +1729,12 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
       aba_factor(m, q, v, ctrl, ws.ext.data(), ws.qdd.data(), ws.cache);
       forward_kinematics(m, q, v, ws.fk.data());
       hook(PH_ABA);
+      ground_prepare(m, ws.fk.data(), ws.gprep);
+      hook(PH_CONTACT);
       for (int sw = 0; sw < m.cc.sweeps; sw++) {
         for (int k = 0; k < m.nv; k++) ws.vfree[k] = v[k] + S(m.dt) * ws.qdd[k];
         fk_velocity(m, ws.cache.xt, ws.vfree.data(), ws.fk.data());
-        contact_pass(m, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
+        ground_sweep(m, ws.gprep, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
         hook(PH_CONTACT);
         aba_resolve(m, ws.cache, ws.ext.data(), ws.qdd.data());
         hook(PH_ABA);

@@ -444,7 +444,9 @@ template <class M, class T> __device__ __forceinline__ T impedance_at(T depth) {
   }
 }
 template <class M, class T> __device__ __forceinline__ T restitution_at(T approach) {
-  if constexpr (M::c_rest_v <= 0.0) {
+  if constexpr (M::c_rest == 0.0) {
+    return T(0);  // every branch below is c_rest times a finite factor
+  } else if constexpr (M::c_rest_v <= 0.0) {
     return T(M::c_rest);
   } else {
     const T sp = dabs(approach);
@@ -553,73 +555,107 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
   return ext;
 }
 
-// Impulse-mode ground/terrain contact of body i (phyz_kernels.cu:845-937): one
-// warm-started update per contact point from the free velocity `vel`. slot
-// holds this body's ground impulses (3 per point); pslot its plane impulses,
-// cleared with the rest of the contact state when the body is off the ground.
-// Returns the body-frame spatial force; writes the readback row when `write`.
+// Impulse-mode ground/terrain contact (phyz_kernels.cu:845-937), split in two.
+// Within a step q is fixed, so a contact point's support point, terrain height
+// and normal, penetration, tangent frame, effective masses and SolImp bias are
+// the same in every sweep: ground_prepare computes them once per step and
+// ground_sweep makes the velocity-dependent warm-started update per sweep.
+// With m' = max(m_n / n_active, 1e-9) and c_t = max(m_t, 1e-9) / n_active the
+// reference's update (bias - r_n) / a_nn and -(b_t - a_tt s_t) / a_tt reads
+//   f_n = max((bias - v_n (1 + e)) m' + s_n, 0),  f_t = s_t - b_t c_t.
+template <class M> constexpr int ground_pts(int i) {
+  return M::gtype[i] == G_NONE ? 0 : (M::gtype[i] == G_BOX ? 8 : 1);
+}
+template <class M> constexpr int ground_off(int i) {
+  int s = 0;
+  for (int k = 0; k < i; k++) s += ground_pts<M>(k);
+  return s;
+}
+template <class M, class T> struct GroundPrep {
+  static constexpr int N = ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1;
+  V3<T> sup[N], nb[N], tu[N], tw[N];  // body frame
+  T mn[N], cu[N], cw[N], bias[N];
+  bool in[N];
+  bool any[M::NB];
+};
+
+// Body i's contact geometry; writes the position part of its readback row
+// (touching, deepest penetration, deepest point) when `write`.
 template <class M, class T, int i>
-__device__ __forceinline__ SV<T> contact_body_imp(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const Terrain<T>& tr,
-                                                  T* slot, T* pslot, T* out, int S, bool write) {
-  constexpr int gt = M::gtype[i];
-  constexpr int npts = gt == G_BOX ? 8 : 1;
+__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const Terrain<T>& tr, GroundPrep<M, T>& gp,
+                                               T* out, int S, bool write) {
+  constexpr int n = ground_pts<M>(i), o = ground_off<M>(i);
   const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
-  const V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);
-  V3<T> sup[npts], supw[npts], nw[npts];
-  T pen[npts];
+  const V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);  // world +Z in the body frame
+  V3<T> supw[n];
+  T pen[n];
   int nact = 0;
 #pragma unroll
-  for (int cp = 0; cp < npts; cp++) {
-    sup[cp] = contact_point<M, T, i>(cp, zb);
-    supw[cp] = pw + mul(Rw, sup[cp]);
-    const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw[cp]);
-    pen[cp] = nw[cp].z * (th - supw[cp].z);
-    nact += pen[cp] > T(-M::c_margin) ? 1 : 0;
+  for (int cp = 0; cp < n; cp++) {
+    gp.sup[o + cp] = contact_point<M, T, i>(cp, zb);
+    supw[cp] = pw + mul(Rw, gp.sup[o + cp]);
+    V3<T> nw;
+    const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw);
+    pen[cp] = nw.z * (th - supw[cp].z);
+    gp.in[o + cp] = pen[cp] > T(-M::c_margin);
+    gp.nb[o + cp] = M::HAS_HF ? tmul(Rw, nw) : zb;
+    nact += gp.in[o + cp] ? 1 : 0;
   }
-  const T na = T(nact < 1 ? 1 : nact);
-  SV<T> ext = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
-  V3<T> ftot = v3(T(0), T(0), T(0));
+  const T na = n == 1 ? T(1) : T(nact < 1 ? 1 : nact);
   T deepest = T(0);
   V3<T> dw = v3(T(0), T(0), T(0));
   bool any = false;
 #pragma unroll
-  for (int cp = 0; cp < npts; cp++) {
-    const bool in = pen[cp] > T(-M::c_margin);
-    const V3<T> nb = tmul(Rw, nw[cp]);
-    const V3<T> vpt = vel.l + cross(vel.a, sup[cp]);
-    V3<T> tu, tw;
-    tangent_frame(nb, tu, tw);
-    T* sl = slot + 3 * cp;
-    const T a_nn = T(1) / dmax(eff_mass<M, T, i>(sup[cp], nb) / na, T(1e-9));
-    const T a_uu = na / dmax(eff_mass<M, T, i>(sup[cp], tu), T(1e-9));
-    const T a_ww = na / dmax(eff_mass<M, T, i>(sup[cp], tw), T(1e-9));
-    T upd[3] = {sl[0], sl[1], sl[2]};
-    impulse_update<M, T>(pen[cp], dot(vpt, nb), dot(vpt, tu), dot(vpt, tw), a_nn, a_uu, a_ww, upd);
-#pragma unroll
-    for (int k = 0; k < 3; k++) sl[k] = in ? upd[k] : T(0);
-    const V3<T> fb = (nb * sl[0] + tu * sl[1] + tw * sl[2]) * T(1.0 / dtc);
-    ext.a = ext.a + cross(sup[cp], fb);
-    ext.l = ext.l + fb;
-    ftot = ftot + mul(Rw, fb);
+  for (int cp = 0; cp < n; cp++) {
+    const int k = o + cp;
+    tangent_frame(gp.nb[k], gp.tu[k], gp.tw[k]);
+    gp.mn[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.nb[k]) / na, T(1e-9));
+    gp.cu[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.tu[k]), T(1e-9)) / na;
+    gp.cw[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.tw[k]), T(1e-9)) / na;
+    gp.bias[k] = impedance_at<M, T>(pen[cp]) * T(M::c_erp) * dmax(pen[cp], T(0)) / T(dtc);
+    const bool in = gp.in[k];
     any = any || in;
     const bool deeper = in && pen[cp] > deepest;
     deepest = deeper ? pen[cp] : deepest;
     dw = sel(deeper, supw[cp], dw);
   }
-  if (!any) {
-#pragma unroll
-    for (int k = 0; k < 3 * npts; k++) pslot[k] = T(0);
-  }
+  gp.any[i] = any;
   if (write) {
-    T* o = out + 8 * i * S;
-    o[0] = any ? T(1) : T(0);
-    o[S] = any ? deepest : T(0);
-    o[2 * S] = any ? dw.x : T(0);
-    o[3 * S] = any ? dw.y : T(0);
-    o[4 * S] = any ? dw.z : T(0);
-    o[5 * S] = any ? ftot.x : T(0);
-    o[6 * S] = any ? ftot.y : T(0);
-    o[7 * S] = any ? ftot.z : T(0);
+    T* r = out + 8 * i * S;
+    r[0] = any ? T(1) : T(0);
+    r[S] = any ? deepest : T(0);
+    r[2 * S] = any ? dw.x : T(0);
+    r[3 * S] = any ? dw.y : T(0);
+    r[4 * S] = any ? dw.z : T(0);
+  }
+}
+
+// One sweep of body i's prepared ground contacts at body-frame velocity vel;
+// slot holds its ground impulses (3 per point). Returns the body-frame force.
+template <class M, class T, int i>
+__device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const SV<T>& vel, T* slot) {
+  constexpr int n = ground_pts<M>(i), o = ground_off<M>(i);
+  const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
+  SV<T> ext = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+#pragma unroll
+  for (int cp = 0; cp < n; cp++) {
+    const int k = o + cp;
+    const V3<T> vpt = vel.l + cross(vel.a, gp.sup[k]);
+    const T b_n = dot(vpt, gp.nb[k]);
+    const T e = restitution_at<M, T>(dmin(b_n, T(0)));
+    const T fn = dmax((gp.bias[k] - b_n * (T(1) + e)) * gp.mn[k] + slot[3 * cp], T(0));
+    const T tu = slot[3 * cp + 1] - dot(vpt, gp.tu[k]) * gp.cu[k];
+    const T tw = slot[3 * cp + 2] - dot(vpt, gp.tw[k]) * gp.cw[k];
+    const T limit = T(M::mu) * fn;
+    const T tn = dsqrt(tu * tu + tw * tw);
+    const T sc = tn > limit ? (tn > T(0) ? limit / tn : T(0)) : T(1);
+    const bool in = gp.in[k];
+    slot[3 * cp] = in ? fn : T(0);
+    slot[3 * cp + 1] = in ? tu * sc : T(0);
+    slot[3 * cp + 2] = in ? tw * sc : T(0);
+    const V3<T> fb = (gp.nb[k] * slot[3 * cp] + gp.tu[k] * slot[3 * cp + 1] + gp.tw[k] * slot[3 * cp + 2]) * T(1.0 / dtc);
+    ext.a = ext.a + cross(gp.sup[k], fb);
+    ext.l = ext.l + fb;
   }
   return ext;
 }
@@ -1270,6 +1306,11 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     }
   });
   sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
+  GroundPrep<M, T> gp;
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    if constexpr (M::gtype[i] != G_NONE) ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], tr, gp, rows, S, write_rows);
+  });
   // A plain loop: compact, spill-free, and exact at every sweep count. Left to
   // the compiler's own unrolling choice, the f64 kernel of an 8-corner box gave
   // wrong impulses from the fourth sweep on (checked across sweep counts in
@@ -1294,7 +1335,23 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if constexpr (M::gtype[i] != G_NONE) {
-        ext[i] = contact_body_imp<M, T, i>(ws.Rw[i], ws.Pw[i], vf[i], tr, impg[i], impp[i], rows, S, wr);
+        ext[i] = ground_sweep<M, T, i>(gp, vf[i], impg[i]);
+        if constexpr (M::PLANE >= 0) {
+          // The reference clears a body's whole contact state, plane impulses
+          // included, when it is off the ground; the plane pass then starts
+          // those from zero in every sweep.
+          if (!gp.any[i]) {
+#pragma unroll
+            for (int k = 0; k < 3 * ground_pts<M>(i); k++) impp[i][k] = T(0);
+          }
+        }
+        if (wr) {
+          const V3<T> ft = mul(ws.Rw[i], ext[i].l);  // summed ground force, world frame
+          T* r = rows + 8 * i * S;
+          r[5 * S] = gp.any[i] ? ft.x : T(0);
+          r[6 * S] = gp.any[i] ? ft.y : T(0);
+          r[7 * S] = gp.any[i] ? ft.z : T(0);
+        }
       } else if constexpr (i == M::PLANE) {
         ext[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
       }
