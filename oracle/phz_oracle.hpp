@@ -826,7 +826,7 @@ template <class S> struct AbaCache {
 
 // The structure-exploiting ABA (same equations as aba.rs:117-368): symmetric
 // articulated inertias, X^T I X as rotate-then-translate, LDL^T joint solves.
-// Fills `c` for aba_resolve.
+// Fills `c` for aba_delta.
 template <class S>
 void aba_factor(const Model& m, const S* q, const S* v, const S* ctrl, const SV<S>* ext, S* qdd, AbaCache<S>& c) {
   const int nb = m.nb;
@@ -963,23 +963,22 @@ template <class S> void aba_struct(const Model& m, const S* q, const S* v, const
   aba_factor(m, q, v, ctrl, ext, qdd, c);
 }
 
-// The force-dependent half of aba_factor for new external forces: with q, v,
-// ctrl unchanged the articulated inertias, U, D and I_a c are the same, so only
-// u = tau - S^T p_A, p_a = p_A + I_a c + U D^-1 u and pass 3 are redone. Used by
-// the impulse sweeps; algebraically identical to a full solve.
-template <class S> void aba_resolve(const Model& m, AbaCache<S>& c, const SV<S>* ext, S* qdd) {
+// The ABA's response dqdd to a change dext of the external forces with q, v,
+// ctrl fixed: the solve is affine in the forces, so qdd(ext0 + dext) =
+// qdd(ext0) + dqdd. Passes 2 and 3 run on the force change alone with the
+// cached factorization: dp_A = -dext, du = -S^T dp_A, dp_a = dp_A + U D^-1 du;
+// da = X da_parent (zero at the root), dqdd = D^-1 (du - U^T da), da += S dqdd.
+template <class S> void aba_delta(const Model& m, AbaCache<S>& c, const SV<S>* dext, S* dqdd) {
   const int nb = m.nb;
   std::vector<SV<S>> pa(nb), acc(nb);
-  SV<S> a0;
-  a0.lin = V3<S>{S(-m.gravity[0]), S(-m.gravity[1]), S(-m.gravity[2])};
-  for (int i = 0; i < nb; i++) pa[i] = ext ? c.bias[i] - ext[i] : c.bias[i];
+  for (int i = 0; i < nb; i++) pa[i] = SV<S>() - dext[i];
   for (int i = nb - 1; i >= 0; i--) {
     const Body& b = m.bodies[i];
     const int nd = joint_ndof(b.jtype);
     auto& J = c.js[i];
     SV<S> pA = pa[i];
     if (nd > 0) {
-      for (int k = 0; k < nd; k++) J.u[k] = c.qfrc[b.voff + k] - dot(subspace_col<S>(b, k), pa[i]);
+      for (int k = 0; k < nd; k++) J.u[k] = S(0.0) - dot(subspace_col<S>(b, k), pa[i]);
       if (!J.ok || b.parent < 0) continue;
       S y[6];
       for (int k = 0; k < nd; k++) { y[k] = J.u[k]; for (int t = 0; t < k; t++) y[k] = y[k] - J.L[k * nd + t] * y[t]; }
@@ -987,7 +986,7 @@ template <class S> void aba_resolve(const Model& m, AbaCache<S>& c, const SV<S>*
       for (int k = nd - 1; k >= 0; k--) for (int t = k + 1; t < nd; t++) y[k] = y[k] - J.L[t * nd + k] * y[t];
       SV<S> wu;
       for (int r = 0; r < 6; r++) { S s0 = S(0.0); for (int k = 0; k < nd; k++) s0 = s0 + J.U[k * 6 + r] * y[k]; wu.set(r, s0); }
-      pA = pA + c.iac[i] + wu;
+      pA = pA + wu;
     } else if (b.parent < 0) {
       continue;
     }
@@ -996,9 +995,10 @@ template <class S> void aba_resolve(const Model& m, AbaCache<S>& c, const SV<S>*
   for (int i = 0; i < nb; i++) {
     const Body& b = m.bodies[i];
     const int nd = joint_ndof(b.jtype);
-    SV<S> ap = apply_motion(c.xt[i], b.parent < 0 ? a0 : acc[b.parent]) + c.cb[i];
+    SV<S> ap = b.parent < 0 ? SV<S>() : apply_motion(c.xt[i], acc[b.parent]);
     const auto& J = c.js[i];
-    if (nd == 0 || !J.ok) { acc[i] = ap; continue; }
+    if (nd == 0) { acc[i] = ap; continue; }
+    if (!J.ok) { for (int k = 0; k < nd; k++) dqdd[b.voff + k] = S(0.0); acc[i] = ap; continue; }
     S y[6];
     for (int k = 0; k < nd; k++) {
       S uta = S(0.0);
@@ -1008,7 +1008,7 @@ template <class S> void aba_resolve(const Model& m, AbaCache<S>& c, const SV<S>*
     }
     for (int k = 0; k < nd; k++) y[k] = y[k] * J.Dd[k];
     for (int k = nd - 1; k >= 0; k--) for (int t = k + 1; t < nd; t++) y[k] = y[k] - J.L[t * nd + k] * y[t];
-    for (int k = 0; k < nd; k++) { qdd[b.voff + k] = y[k]; ap = ap + subspace_col<S>(b, k) * y[k]; }
+    for (int k = 0; k < nd; k++) { dqdd[b.voff + k] = y[k]; ap = ap + subspace_col<S>(b, k) * y[k]; }
     acc[i] = ap;
   }
 }
@@ -1713,7 +1713,7 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
     // reference's sequencing); otherwise the kernels' split form: transforms,
     // bias forces, joint factorizations and contact geometry once, then per
     // sweep only the velocities at v + dt qdd, the velocity-dependent contact
-    // update (ground_sweep) and the force-dependent half of the ABA (aba_resolve).
+    // update (ground_sweep) and the ABA's response to the force change (aba_delta).
     if (dense) {
       aba(ws.ext.data());
       hook(PH_ABA);
@@ -1728,6 +1728,8 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
     } else {
       aba_factor(m, q, v, ctrl, ws.ext.data(), ws.qdd.data(), ws.cache);
       forward_kinematics(m, q, v, ws.fk.data());
+      std::vector<S> qdd0(ws.qdd), dqdd(m.nv);
+      std::vector<SV<S>> ext0(ws.ext), dext(m.nb);
       hook(PH_ABA);
       ground_prepare(m, ws.fk.data(), ws.gprep);
       hook(PH_CONTACT);
@@ -1736,7 +1738,9 @@ void step_world(const Model& m, S* q, S* v, S* ctrl, const S* targets, uint64_t*
         fk_velocity(m, ws.cache.xt, ws.vfree.data(), ws.fk.data());
         ground_sweep(m, ws.gprep, ws.fk.data(), ws.ext.data(), ws.cs.data(), contact_rows);
         hook(PH_CONTACT);
-        aba_resolve(m, ws.cache, ws.ext.data(), ws.qdd.data());
+        for (int i = 0; i < m.nb; i++) dext[i] = ws.ext[i] - ext0[i];
+        aba_delta(m, ws.cache, dext.data(), dqdd.data());
+        for (int k = 0; k < m.nv; k++) ws.qdd[k] = qdd0[k] + dqdd[k];
         hook(PH_ABA);
       }
     }

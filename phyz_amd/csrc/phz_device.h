@@ -1216,26 +1216,23 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
   });
 }
 
-// Force-dependent half of body i's pass 2 after the contact forces change
-// (impulse sweeps): u = tau - S^T p_A and p_a = p_A + I_a c + U D^-1 u, with
-// U, D^-1 and I_a c kept from the step's full pass 2 (q and v do not change
-// between sweeps, so neither do the articulated inertias).
-template <class M, class T, int i>
-__device__ __forceinline__ void body_bias(WS<M, T>& ws, const T* q, const T* v, const T* ctrl, const SV<T>& iac, SV<T>& pa) {
+// The ABA's response to a change of the external forces with q, v and ctrl
+// fixed (the impulse sweeps). The articulated-body solve is affine in the
+// external forces, so with the step's factorization (X, U, L, D^-1, ok) kept,
+// qdd(ext) = qdd(ext0) + dqdd(ext - ext0), where dqdd runs passes 2 and 3 on
+// the force change alone: dp_A = -(ext - ext0), du = -S^T dp_A,
+// dp_a = dp_A + U D^-1 du up the tree; da = X da_parent (zero at the root:
+// gravity and the velocity-product terms are in qdd(ext0)),
+// dqdd = D^-1 (du - U^T da), da += S dqdd down the tree.
+template <class M, class T, int i> __device__ __forceinline__ void body_delta_up(WS<M, T>& ws, SV<T> (&dp)[M::NB]) {
   constexpr int nd = ndof_of(M::jtype[i]);
   constexpr int p = M::parent[i];
-  constexpr int vo = M::voff[i], qo = M::qoff[i];
   constexpr int MAXD = M::MAXD;
-  pa = ws.pA[i];
+  SV<T> pa = dp[i];
   if constexpr (nd > 0) {
 #pragma unroll
-    for (int k = 0; k < nd; k++) {
-      T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
-      if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
-      ws.uu[i][k] = tau - dot(subspace<M, T, i>(k), ws.pA[i]);
-    }
+    for (int k = 0; k < nd; k++) ws.uu[i][k] = -dot(subspace<M, T, i>(k), dp[i]);
     if constexpr (p >= 0) {
-      // U D^-1 u: solve L D L^T y = u, then U y.
       T y[MAXD];
 #pragma unroll
       for (int k = 0; k < nd; k++) {
@@ -1249,15 +1246,49 @@ __device__ __forceinline__ void body_bias(WS<M, T>& ws, const T* q, const T* v, 
       for (int k = nd - 1; k >= 0; k--)
 #pragma unroll
         for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
-      SV<T> wu = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
 #pragma unroll
       for (int k = 0; k < nd; k++) {
         const SV<T> uk = {v3(ws.U[i][k][0], ws.U[i][k][1], ws.U[i][k][2]), v3(ws.U[i][k][3], ws.U[i][k][4], ws.U[i][k][5])};
-        wu = wu + uk * y[k];
+        pa = pa + uk * y[k];
       }
-      pa = pa + iac + wu;
     }
   }
+  if constexpr (p >= 0) {
+    if (ws.ok[i]) dp[p] = dp[p] + inv_apply_force(ws.X[i], pa);
+  }
+}
+template <class M, class T, int i> __device__ __forceinline__ void body_delta_down(WS<M, T>& ws, T* dqdd) {
+  constexpr int nd = ndof_of(M::jtype[i]);
+  constexpr int p = M::parent[i];
+  constexpr int vo = M::voff[i];
+  constexpr int MAXD = M::MAXD;
+  SV<T> ap;
+  if constexpr (p < 0) ap = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  else ap = apply_motion(ws.X[i], ws.acc[p]);
+  if constexpr (nd > 0) {
+    T y[MAXD];
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      T uta = ws.U[i][k][0] * ap.a.x + ws.U[i][k][1] * ap.a.y + ws.U[i][k][2] * ap.a.z + ws.U[i][k][3] * ap.l.x +
+              ws.U[i][k][4] * ap.l.y + ws.U[i][k][5] * ap.l.z;
+      y[k] = ws.uu[i][k] - uta;
+#pragma unroll
+      for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
+    }
+#pragma unroll
+    for (int k = 0; k < nd; k++) y[k] = y[k] * ws.Dinv[i][k];
+#pragma unroll
+    for (int k = nd - 1; k >= 0; k--)
+#pragma unroll
+      for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
+#pragma unroll
+    for (int k = 0; k < nd; k++) {
+      y[k] = ws.ok[i] ? y[k] : T(0);
+      dqdd[vo + k] = y[k];
+      ap = ap + subspace<M, T, i>(k) * y[k];
+    }
+  }
+  ws.acc[i] = ap;
 }
 
 template <class M> struct HasExt {
@@ -1266,8 +1297,9 @@ template <class M> struct HasExt {
 
 // One impulse-mode step of one world (crates/phyz-gpu/src/cuda/mod.rs:899-928):
 // controls; FK, velocities and bias forces once; a full ABA against the
-// contact forces carried from the previous step; then SWEEPS x [contact at the
-// free velocity v + dt qdd (warm-started), force-only ABA re-solve]; integrate.
+// contact forces carried from the previous step; the contact geometry; then
+// SWEEPS x [contact at the free velocity v + dt qdd (warm-started), the ABA's
+// response to the change of the contact forces]; integrate.
 // ext, impg (ground) and impp (plane) persist between steps.
 template <class M, class T>
 __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
@@ -1281,10 +1313,8 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     constexpr int i = decltype(I)::value;
     body_pass1<M, T, i>(ws, q, v, rows, S, false, false, tr);
   });
-  SV<T> pA0[NB], iac[NB];
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
-    pA0[i] = ws.pA[i];
     if constexpr (HasExt<M>::template at<i>()) ws.pA[i] = ws.pA[i] - ext[i];
     ws.IA[i] = rigid_inertia<M, T, i>();
   });
@@ -1294,7 +1324,6 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     Sym<T> Ia;
     SV<T> pa;
     body_solve<M, T, i>(ws, q, v, ctrl, Ia, pa);
-    iac[i] = (ndof_of(M::jtype[i]) > 0 && p >= 0) ? sym_mul(Ia, ws.cb[i]) : SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
     if constexpr (p >= 0) {
       if (ws.ok[i]) {
         Sym<T> dI;
@@ -1306,6 +1335,15 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     }
   });
   sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
+  // qdd at the carried forces ext0; the sweeps add the response to ext - ext0.
+  T qdd0[M::NV];
+  SV<T> ext0[NB];
+#pragma unroll
+  for (int j = 0; j < M::NV; j++) qdd0[j] = qdd[j];
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    if constexpr (HasExt<M>::template at<i>()) ext0[i] = ext[i];
+  });
   GroundPrep<M, T> gp;
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
@@ -1357,21 +1395,17 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
       }
     });
     if constexpr (M::PLANE >= 0) plane_contacts<M, T, true>(ws.Rw, ws.Pw, vf, impp, ext);
+    SV<T> dp[NB];
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      ws.pA[i] = pA0[i];
-      if constexpr (HasExt<M>::template at<i>()) ws.pA[i] = ws.pA[i] - ext[i];
+      if constexpr (HasExt<M>::template at<i>()) dp[i] = ext0[i] - ext[i];
+      else dp[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
     });
-    rfor<NB>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      constexpr int p = M::parent[i];
-      SV<T> pa;
-      body_bias<M, T, i>(ws, q, v, ctrl, iac[i], pa);
-      if constexpr (p >= 0) {
-        if (ws.ok[i]) ws.pA[p] = ws.pA[p] + inv_apply_force(ws.X[i], pa);
-      }
-    });
-    sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
+    rfor<NB>([&](auto I) { body_delta_up<M, T, decltype(I)::value>(ws, dp); });
+    T dqdd[M::NV];
+    sfor<0, NB>([&](auto I) { body_delta_down<M, T, decltype(I)::value>(ws, dqdd); });
+#pragma unroll
+    for (int j = 0; j < M::NV; j++) qdd[j] = qdd0[j] + dqdd[j];
   }
   sfor<0, NB>([&](auto I) { body_integrate<M, T, decltype(I)::value>(q, v, qdd); });
 }
