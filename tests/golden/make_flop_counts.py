@@ -36,6 +36,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 sys.path.insert(0, ROOT)
 
 from phyz_amd import workloads as W  # noqa: E402
+from phyz_amd.model import G_BOX  # noqa: E402
 from tests.helpers import oracle_for  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flops_per_world_step.json")
@@ -80,9 +81,11 @@ def main():
         reads_ctrl = w.noise is None and w.pd is None
         per_elem = 2 * nq + 2 * nv + (nv if reads_ctrl else 0) + (len(w.pd) if w.pd else 0)
         if w.impulse_sweeps > 0:
-            # Carried forces (6) and ground warm-start impulses (24) of each body with a shape.
-            ncb = sum(1 for b in w.model.bodies if b.geometry is not None)
-            per_elem += 2 * (6 + 24) * ncb
+            # Carried forces (6) and ground warm-start impulses (3 per contact
+            # point: 8 for a box, 1 otherwise) of each body with a shape.
+            for b in w.model.bodies:
+                if b.geometry is not None:
+                    per_elem += 2 * (6 + 3 * (8 if b.geometry.kind == G_BOX else 1))
         out[w.name] = {
             "config": idx,
             "bodies": w.model.nbodies,
