@@ -111,6 +111,28 @@ int phz_set_position_targets(phz_sim* sim, const double* rows);
 int phz_enable_control_noise(phz_sim* sim, uint64_t seed, int dist, double a, double b,
                              const uint32_t* v_indices, uint32_t n);
 
+/* Terms of the reference's CPU model (phyz_model::Model) that its device body
+ * table has no slots for, applied as the CPU dynamics apply them
+ * (crates/phyz-rigid/src/actuation.rs:18-39, crates/phyz-model/src/joint.rs:196-247):
+ *   joint terms  nb x 8: [limited, lo, hi, limit_stiffness, limit_damping,
+ *                friction_loss, 0, 0] per body (Joint::limits, limit_stiffness,
+ *                limit_damping, friction_loss); one-DOF joints only. NULL clears.
+ * A batched simulator built from a Model with limits or friction loss calls
+ * this once after create. */
+int phz_set_joint_terms(phz_sim* sim, const double* table);
+/* Model::actuators (crates/phyz-model/src/model.rs:18-82, actuator_forces_at
+ * 203-231): n x 16 [joint (body index), gear, gain, bias_q, bias_v,
+ * has_ctrl_range, ctrl_lo, ctrl_hi, has_force_range, force_lo, force_hi, 0...];
+ * each drives the first DOF of its joint with gear (gain clamp(ctrl) +
+ * bias_q q + bias_v v), then the force range. With n > 0 the controls of
+ * load_states / set_controls / readback_controls and the control-noise indices
+ * are one per actuator (Model::nu) instead of one per DOF, and are zeroed
+ * here. PD servos write per-DOF controls, so they and actuators exclude each
+ * other. n = 0 clears. */
+int phz_set_actuators(phz_sim* sim, const double* table, uint32_t n);
+/* Controls per world: the actuator count, or nv without actuators. */
+int phz_nctrl(const phz_sim* sim);
+
 /* BatchSim::load_states (mod.rs:799-807) and set_controls (mod.rs:810-815).
  * ctrl may be NULL (zeros). Loading states also reseeds the control stream. */
 int phz_load_states(phz_sim* sim, const double* q, const double* v, const double* ctrl);

@@ -59,6 +59,8 @@ def lib():
         L.orc_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, dp, dp, dp, u64p, dp, dp, C.c_int, C.c_int, dp, dp]
         L.orc_set_contact_cfg.argtypes = [C.c_void_p, C.c_int, C.c_int, dp, C.c_int, dp, C.c_int, C.c_int, dp, dp]
         L.orc_contact_pass.argtypes = [C.c_void_p, dp, dp, dp, dp, dp]
+        L.orc_set_joint_terms.argtypes = [C.c_void_p, dp]
+        L.orc_set_actuators.argtypes = [C.c_void_p, dp, C.c_int]
         L.orc_count_ops.argtypes = [C.c_void_p, dp, dp, dp, dp, C.c_uint64, C.c_int, u64p, dp, dp]
         _lib = L
     return _lib
@@ -118,6 +120,25 @@ class Oracle:
         self.cfg = contact_cfg
         if contact_cfg is not None:
             contact_cfg.apply(L, self._h)
+        self.nctrl = self.nv
+        if model is not None:
+            from phyz_amd.model import pack_actuators, pack_joint_terms
+            if model.has_joint_terms():
+                self.set_joint_terms(pack_joint_terms(model))
+            if model.actuators:
+                self.set_actuators(pack_actuators(model))
+
+    def set_joint_terms(self, table):
+        """Limits and friction loss, nb x 8 (phyz_amd.model.pack_joint_terms)."""
+        t = np.ascontiguousarray(table, dtype=np.float64).reshape(self.nb, 8)
+        lib().orc_set_joint_terms(self._h, _d(t))
+
+    def set_actuators(self, table):
+        """Actuators, nu x 16 (phyz_amd.model.pack_actuators); ctrl becomes nu wide."""
+        t = np.ascontiguousarray(table, dtype=np.float64).reshape(-1, 16)
+        if lib().orc_set_actuators(self._h, _d(t), t.shape[0]):
+            raise ValueError("actuator on a body without a moving joint")
+        self.nctrl = t.shape[0] if t.shape[0] else self.nv
 
     def __del__(self):
         if getattr(self, "_h", None) is not None and _lib is not None:

@@ -68,6 +68,39 @@ int orc_set_contact_cfg(orc_model* o, int solve_mode, int sweeps, const double* 
   }
   return 0;
 }
+// Joint terms, nb x 8: [limited, lo, hi, limit_k, limit_d, friction_loss, 0, 0].
+int orc_set_joint_terms(orc_model* o, const double* t) {
+  Model& m = o->m;
+  m.jterms.assign(m.nb, JointTerms());
+  for (int i = 0; i < m.nb; i++) {
+    const double* r = t + i * 8;
+    JointTerms& j = m.jterms[i];
+    j.limited = r[0] != 0.0;
+    j.lo = r[1]; j.hi = r[2]; j.limit_k = r[3]; j.limit_d = r[4]; j.friction_loss = r[5];
+  }
+  return 0;
+}
+// Actuators, n x 16: [body, gear, gain, bias_q, bias_v, has_ctrl_range, ctrl_lo,
+// ctrl_hi, has_force_range, force_lo, force_hi, 0...]; each drives the first
+// DOF of its body's joint. n = 0 removes them.
+int orc_set_actuators(orc_model* o, const double* t, int n) {
+  Model& m = o->m;
+  m.acts.clear();
+  for (int a = 0; a < n; a++) {
+    const double* r = t + a * 16;
+    Actuator A;
+    A.body = (int)r[0];
+    if (A.body < 0 || A.body >= m.nb || joint_ndof(m.bodies[A.body].jtype) == 0) return 1;
+    A.qidx = m.bodies[A.body].qoff;
+    A.vidx = m.bodies[A.body].voff;
+    A.gear = r[1]; A.gain = r[2]; A.bias_q = r[3]; A.bias_v = r[4];
+    A.has_ctrl_range = r[5] != 0.0; A.ctrl_lo = r[6]; A.ctrl_hi = r[7];
+    A.has_force_range = r[8] != 0.0; A.force_lo = r[9]; A.force_hi = r[10];
+    m.acts.push_back(A);
+  }
+  return 0;
+}
+
 int orc_set_pd(orc_model* o, const double* dofs, int n) {
   o->m.pd.clear();
   for (int i = 0; i < n; i++) {
@@ -205,7 +238,7 @@ int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, d
     for (int w = w0; w < w1; w++) {
       double* qw = q + (size_t)w * m.nq;
       double* vw = v + (size_t)w * m.nv;
-      double* cw = ctrl + (size_t)w * m.nv;
+      double* cw = ctrl + (size_t)w * m.nctrl();
       const double* tw = npd ? targets + (size_t)w * npd : nullptr;
       uint64_t* rw = rng ? rng + w : nullptr;
       ws.reset(m);
@@ -242,9 +275,10 @@ int orc_step_batch(orc_model* o, int nworld, int nsteps, double* q, double* v, d
 int orc_count_ops(orc_model* o, const double* q0, const double* v0, const double* ctrl0, const double* targets0,
                   uint64_t rng_state, int mode, uint64_t* counts, const double* ext0, const double* cs0) {
   const Model& m = o->m;
-  std::vector<OpScalar> q(m.nq), v(m.nv), ctrl(m.nv), tg(m.pd.size());
+  std::vector<OpScalar> q(m.nq), v(m.nv), ctrl(m.nctrl()), tg(m.pd.size());
   for (int j = 0; j < m.nq; j++) q[j] = OpScalar::state(q0[j]);
-  for (int j = 0; j < m.nv; j++) { v[j] = OpScalar::state(v0[j]); ctrl[j] = OpScalar::state(ctrl0[j]); }
+  for (int j = 0; j < m.nv; j++) v[j] = OpScalar::state(v0[j]);
+  for (int j = 0; j < m.nctrl(); j++) ctrl[j] = OpScalar::state(ctrl0[j]);
   for (size_t d = 0; d < m.pd.size(); d++) tg[d] = OpScalar::state(targets0[d]);
   OpCount c;
   OpCount* prev = op_counter();

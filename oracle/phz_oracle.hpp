@@ -167,6 +167,13 @@ inline OpScalar s_log(const OpScalar& x) {
   count_trans();
   return OpScalar::state(std::log(x.v));
 }
+inline double s_tanh(double x) { return std::tanh(x); }
+inline float s_tanh(float x) { return std::tanh(x); }
+inline OpScalar s_tanh(const OpScalar& x) {
+  if (x.k) return OpScalar(std::tanh(x.v));
+  count_trans();
+  return OpScalar::state(std::tanh(x.v));
+}
 template <class S> inline S s_abs(const S& x) {
   if constexpr (std::is_same<S, OpScalar>::value) { if (!x.k) count_other(); OpScalar r = x; r.v = std::fabs(x.v); return r; }
   else return std::fabs(x);
@@ -389,6 +396,22 @@ struct Body {
   double ptj_rot[9], ptj_pos[3], axis[3];
   double damping, stiffness, spring_ref, armature;
 };
+// Joint terms of the reference's CPU model that its device body table does not
+// carry (crates/phyz-model/src/joint.rs:27-72): the soft position limit and dry
+// friction of a one-DOF joint.
+struct JointTerms {
+  bool limited = false;
+  double lo = 0.0, hi = 0.0;
+  double limit_k = 1000.0, limit_d = 60.0;  // DEFAULT_LIMIT_STIFFNESS / _DAMPING (joint.rs:96-104)
+  double friction_loss = 0.0;
+};
+// An actuator driving the first DOF of one joint (crates/phyz-model/src/model.rs:18-82).
+struct Actuator {
+  int body = 0, qidx = 0, vidx = 0;
+  double gear = 1.0, gain = 1.0, bias_q = 0.0, bias_v = 0.0;
+  bool has_ctrl_range = false, has_force_range = false;
+  double ctrl_lo = 0.0, ctrl_hi = 0.0, force_lo = 0.0, force_hi = 0.0;
+};
 struct Geom {
   int type;
   double p[6];            // [1..7): shape parameters / mesh AABB
@@ -435,6 +458,11 @@ struct Model {
   int noise_dist = NOISE_NORMAL;
   double noise_a = 0.0, noise_b = 1.0;
   std::vector<int> noise_dofs;
+  // limits, friction loss (per body; empty: none) and actuators (empty: ctrl is
+  // a per-DOF generalized force, otherwise one control per actuator)
+  std::vector<JointTerms> jterms;
+  std::vector<Actuator> acts;
+  int nctrl() const { return acts.empty() ? nv : (int)acts.size(); }
 };
 
 // Unpack a body table; returns an error string or "" on success.
@@ -550,13 +578,54 @@ template <class S> SV<S> joint_velocity(const Body& b, const S* v) {
 // through per DOF, plus passive -damping*qd on every DOF and the spring
 // -k(q - q_ref) on single-DOF joints (joint.rs:232-247). Limits and
 // friction_loss are not representable in the body table, so they are zero.
+// Soft joint-limit force of a one-DOF joint (joint.rs:196-226): a one-sided
+// spring-damper on the violation depth whose damping only resists motion
+// deeper into the limit.
+template <class S> S limit_force(const JointTerms& t, const S& q, const S& qd) {
+  if (!t.limited) return S(0.0);
+  S depth, sign;
+  if (q < S(t.lo)) { depth = S(t.lo) - q; sign = S(1.0); }
+  else if (q > S(t.hi)) { depth = q - S(t.hi); sign = S(-1.0); }
+  else return S(0.0);
+  S inward = s_max(S(0.0) - sign * qd, S(0.0));
+  return sign * (S(t.limit_k) * depth + S(t.limit_d) * inward);
+}
+// Actuator law f = gear (gain clamp(ctrl) + bias_q q + bias_v v), then the
+// force range (model.rs:57-82).
+template <class S> S actuator_force(const Actuator& a, const S& ctrl, const S& q, const S& v) {
+  S c = ctrl;
+  if (a.has_ctrl_range) c = s_clamp(c, S(std::min(a.ctrl_lo, a.ctrl_hi)), S(std::max(a.ctrl_lo, a.ctrl_hi)));
+  S f = S(a.gear) * (S(a.gain) * c + S(a.bias_q) * q + S(a.bias_v) * v);
+  if (a.has_force_range) f = s_clamp(f, S(std::min(a.force_lo, a.force_hi)), S(std::max(a.force_lo, a.force_hi)));
+  return f;
+}
+// qfrc = actuator forces (or ctrl per DOF without actuators, model.rs:175-231)
+// + the passive terms of each DOF (actuation.rs:18-39, joint.rs:232-247):
+// damping, and on one-DOF joints the spring, the soft limit and the dry
+// friction -f_loss tanh(qd / 1e-3).
 template <class S> void generalized_forces(const Model& m, const S* q, const S* v, const S* ctrl, S* qfrc) {
-  for (int j = 0; j < m.nv; j++) qfrc[j] = ctrl[j];
-  for (const Body& b : m.bodies) {
+  if (m.acts.empty()) {
+    for (int j = 0; j < m.nv; j++) qfrc[j] = ctrl[j];
+  } else {
+    for (int j = 0; j < m.nv; j++) qfrc[j] = S(0.0);
+    for (size_t a = 0; a < m.acts.size(); a++) {
+      const Actuator& A = m.acts[a];
+      qfrc[A.vidx] = qfrc[A.vidx] + actuator_force(A, ctrl[a], q[A.qidx], v[A.vidx]);
+    }
+  }
+  for (int i = 0; i < m.nb; i++) {
+    const Body& b = m.bodies[i];
     int nd = joint_ndof(b.jtype);
     for (int k = 0; k < nd; k++) {
       S f = -(S(b.damping) * v[b.voff + k]);
-      if (nd == 1) f = f - S(b.stiffness) * (q[b.qoff] - S(b.spring_ref));
+      if (nd == 1) {
+        f = f - S(b.stiffness) * (q[b.qoff] - S(b.spring_ref));
+        if (!m.jterms.empty()) {
+          const JointTerms& t = m.jterms[i];
+          f = f + limit_force(t, q[b.qoff], v[b.voff]);
+          if (t.friction_loss > 0.0) f = f - S(t.friction_loss) * s_tanh(v[b.voff] / S(1e-3));
+        }
+      }
       qfrc[b.voff + k] = qfrc[b.voff + k] + f;
     }
   }

@@ -31,6 +31,9 @@ SIGNATURES = {
     "phz_enable_pd_control": (C.c_int, [SIM, dp, C.c_uint32]),
     "phz_set_position_targets": (C.c_int, [SIM, dp]),
     "phz_enable_control_noise": (C.c_int, [SIM, C.c_uint64, C.c_int, C.c_double, C.c_double, u32p, C.c_uint32]),
+    "phz_set_joint_terms": (C.c_int, [SIM, dp]),
+    "phz_set_actuators": (C.c_int, [SIM, dp, C.c_uint32]),
+    "phz_nctrl": (C.c_int, [SIM]),
     "phz_load_states": (C.c_int, [SIM, dp, dp, dp]),
     "phz_set_controls": (C.c_int, [SIM, dp]),
     "phz_step": (C.c_int, [SIM]),

@@ -49,6 +49,9 @@ enum { G_NONE = 0, G_SPHERE = 1, G_BOX = 2, G_CAPSULE = 3, G_CYLINDER = 4, G_MES
 constexpr int ndof_of(int jt) { return jt == J_FIXED ? 0 : (jt == J_BALL ? 3 : (jt == J_FREE ? 6 : 1)); }
 
 // ── math ─────────────────────────────────────────────────────────────────────
+// Kernels are compiled with -ffinite-math-only: no expression may produce an
+// inf or NaN even on a path a select later discards, so every division whose
+// denominator can vanish divides by a guarded value (`x / (ok ? d : 1)`).
 __device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
 __device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
@@ -58,6 +61,8 @@ __device__ __forceinline__ float dlog(float x) { return logf(x); }
 __device__ __forceinline__ double datan2(double y, double x) { return atan2(y, x); }
 __device__ __forceinline__ double dpow(double x, double y) { return pow(x, y); }
 __device__ __forceinline__ float dpow(float x, float y) { return powf(x, y); }
+__device__ __forceinline__ double dtanh(double x) { return tanh(x); }
+__device__ __forceinline__ float dtanh(float x) { return tanhf(x); }
 __device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x); }
 template <class T> __device__ __forceinline__ T dmax(T a, T b) { return a > b ? a : b; }
 template <class T> __device__ __forceinline__ T dmin(T a, T b) { return a < b ? a : b; }
@@ -235,14 +240,14 @@ template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
   T s, c;
   dsincos(ang * T(0.5), &s, &c);
   const bool small = ang < T(Eps<T>::v);
-  T f = small ? T(0.5) : s / ang;
+  T f = small ? T(0.5) : s / (small ? T(1) : ang);
   return {small ? T(1) : c, w.x * f, w.y * f, w.z * f};
 }
 template <class T> __device__ __forceinline__ V3<T> quat_log(const Q<T>& q) {
   V3<T> v = v3(q.x, q.y, q.z);
   T n = dsqrt(dot(v, v));
   const bool small = n < T(Eps<T>::v);
-  T f = small ? T(2) : T(2) * datan2(n, q.w) / n;
+  T f = small ? T(2) : T(2) * datan2(n, q.w) / (small ? T(1) : n);
   return v * f;
 }
 // Rotation matrix of unit q (active), row-major.
@@ -277,7 +282,7 @@ __device__ __forceinline__ float uniform01(u64& s, float) { return (float)(unsig
 struct StepArgs {
   void* q;             // [nq][stride]
   void* v;             // [nv][stride]
-  void* ctrl;          // [nv][stride]
+  void* ctrl;          // [nctrl][stride]: one row per actuator, or per DOF without actuators
   void* qdd;           // [nv][stride], last step's accelerations
   const void* targets; // [npd][stride]
   u64* rng;            // [stride]
@@ -399,7 +404,7 @@ template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_poin
       sp = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
     } else if constexpr (gt == G_CYLINDER) {
       T rl = dsqrt(n.x * n.x + n.y * n.y);
-      T f = rl > T(1e-6) ? T(M::gp[i][0]) / rl : T(0);
+      T f = rl > T(1e-6) ? T(M::gp[i][0]) / (rl > T(1e-6) ? rl : T(1)) : T(0);
       sp = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
     } else {  // mesh AABB
       sp = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
@@ -460,7 +465,7 @@ template <class T> __device__ __forceinline__ void tangent_frame(V3<T> n, V3<T>&
   const V3<T> a = v3(ax ? T(0) : T(1), ax ? T(1) : T(0), T(0));
   const V3<T> c = cross(n, a);
   const T l = dsqrt(dot(c, c));
-  u = sel(l > T(0), c * (T(1) / l), c);
+  u = sel(l > T(0), c * (T(1) / (l > T(0) ? l : T(1))), c);
   w = cross(n, u);
 }
 
@@ -480,7 +485,7 @@ __device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_n
   T tw = -(b_w - a_ww * slot[2]) / a_ww;
   const T limit = T(M::mu) * fn;
   const T tn = dsqrt(tu * tu + tw * tw);
-  const T sc = tn > limit ? (tn > T(0) ? limit / tn : T(0)) : T(1);
+  const T sc = tn > limit ? (tn > T(0) ? limit / (tn > T(0) ? tn : T(1)) : T(0)) : T(1);
   slot[0] = fn;
   slot[1] = tu * sc;
   slot[2] = tw * sc;
@@ -522,7 +527,7 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     V3<T> vt3 = vpt - nb * vn;
     T vt = dsqrt(dot(vt3, vt3));
     const bool slip = vt > T(1e-6);
-    T ivt = slip ? T(1) / vt : T(0);
+    T ivt = slip ? T(1) / (slip ? vt : T(1)) : T(0);
     V3<T> td = vt3 * ivt;
     T coul = T(M::mu) * fn * dmin(T(1), vt * T(1e3));
     T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i>(sup, td) * vt);
@@ -648,7 +653,7 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
     const T tw = slot[3 * cp + 2] - dot(vpt, gp.tw[k]) * gp.cw[k];
     const T limit = T(M::mu) * fn;
     const T tn = dsqrt(tu * tu + tw * tw);
-    const T sc = tn > limit ? (tn > T(0) ? limit / tn : T(0)) : T(1);
+    const T sc = tn > limit ? (tn > T(0) ? limit / (tn > T(0) ? tn : T(1)) : T(0)) : T(1);
     const bool in = gp.in[k];
     slot[3 * cp] = in ? fn : T(0);
     slot[3 * cp + 1] = in ? tu * sc : T(0);
@@ -727,7 +732,7 @@ __device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw,
             const V3<T> vt3 = vrel - nw * vn;
             const T vt = dsqrt(dot(vt3, vt3));
             const bool slip = vt > T(1e-6);
-            const V3<T> td = vt3 * (slip ? T(1) / vt : T(0));
+            const V3<T> td = vt3 * (slip ? T(1) / (slip ? vt : T(1)) : T(0));
             T ft = dmin(T(M::mu) * fn * dmin(T(1), vt * T(1e3)), T(1.0 / dtc) * series(td) * vt);
             ft = slip ? ft : T(0);
             fw = nw * fn - td * ft;
@@ -845,6 +850,46 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
   }
 }
 
+// Generalized force on DOF k of body i's joint: the actuators driving it (or
+// the DOF's own ctrl entry when the model has none, model.rs:175-231), then the
+// passive terms (actuation.rs:18-39, joint.rs:196-247): damping, and on a
+// one-DOF joint the spring, the soft position limit and dry friction.
+template <class M, class T, int a> __device__ __forceinline__ T actuator_force(T c, T qj, T vj) {
+  if constexpr (M::act_cr[a]) c = dmin(dmax(c, T(M::act_clo[a])), T(M::act_chi[a]));
+  T f = T(M::act_gear[a]) * (T(M::act_gain[a]) * c + T(M::act_bq[a]) * qj + T(M::act_bv[a]) * vj);
+  if constexpr (M::act_fr[a]) f = dmin(dmax(f, T(M::act_flo[a])), T(M::act_fhi[a]));
+  return f;
+}
+template <class M, class T, int i, int k>
+__device__ __forceinline__ T dof_force(const T* q, const T* v, const T* ctrl) {
+  constexpr int nd = ndof_of(M::jtype[i]);
+  constexpr int vo = M::voff[i], qo = M::qoff[i];
+  T tau;
+  if constexpr (M::NU == 0) {
+    tau = ctrl[vo + k];
+  } else {
+    tau = T(0);
+    sfor<0, M::NU>([&](auto A) {
+      constexpr int a = decltype(A)::value;
+      if constexpr (M::act_v[a] == vo + k) tau = tau + actuator_force<M, T, a>(ctrl[a], q[M::act_q[a]], v[vo + k]);
+    });
+  }
+  T f = -(T(M::damping[i]) * v[vo + k]);
+  if constexpr (nd == 1) {
+    f = f - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
+    if constexpr (M::lim_on[i]) {
+      const T x = q[qo], xd = v[vo];
+      const bool below = x < T(M::lim_lo[i]), above = x > T(M::lim_hi[i]);
+      const T depth = below ? T(M::lim_lo[i]) - x : x - T(M::lim_hi[i]);
+      const T sign = below ? T(1) : T(-1);
+      const T lf = sign * (T(M::lim_k[i]) * depth + T(M::lim_d[i]) * dmax(-(sign * xd), T(0)));
+      f = f + ((below || above) ? lf : T(0));
+    }
+    if constexpr (M::floss[i] > 0.0) f = f - T(M::floss[i]) * dtanh(v[vo] / T(1e-3));
+  }
+  return tau + f;
+}
+
 // Joint solve of body i (U, D = LDL^T, u) and its articulated inertia / bias
 // force as seen by the parent (I_a, p_a), from I_A and p_A. Returns false for
 // a body without DOFs (then Ia, pa are I_A, p_A unchanged).
@@ -859,15 +904,13 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
   Ia = ws.IA[i];
   pa = ws.pA[i];
   if constexpr (nd > 0) {
-#pragma unroll
-    for (int k = 0; k < nd; k++) {
+    sfor<0, nd>([&](auto K) {
+      constexpr int k = decltype(K)::value;
       SV<T> uk = sym_mul(ws.IA[i], subspace<M, T, i>(k));
       ws.U[i][k][0] = uk.a.x; ws.U[i][k][1] = uk.a.y; ws.U[i][k][2] = uk.a.z;
       ws.U[i][k][3] = uk.l.x; ws.U[i][k][4] = uk.l.y; ws.U[i][k][5] = uk.l.z;
-      T tau = ctrl[vo + k] - T(M::damping[i]) * v[vo + k];
-      if constexpr (nd == 1) tau = tau - T(M::stiffness[i]) * (q[qo] - T(M::spring_ref[i]));
-      ws.uu[i][k] = tau - dot(subspace<M, T, i>(k), ws.pA[i]);
-    }
+      ws.uu[i][k] = dof_force<M, T, i, k>(q, v, ctrl) - dot(subspace<M, T, i>(k), ws.pA[i]);
+    });
     T D[MAXD][MAXD];
 #pragma unroll
     for (int r = 0; r < nd; r++)
@@ -885,7 +928,7 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
 #pragma unroll
       for (int k = 0; k < j; k++) dj = dj - ws.Lm[i][j][k] * E[j][k];
       ws.ok[i] = ws.ok[i] && !(dabs(dj) < T(1e-20));
-      ws.Dinv[i][j] = T(1) / dj;
+      ws.Dinv[i][j] = T(1) / (dabs(dj) < T(1e-20) ? T(1) : dj);
 #pragma unroll
       for (int r = j + 1; r < nd; r++) {
         T e = D[r][j];
@@ -1044,7 +1087,7 @@ template <class T> __device__ __forceinline__ void add_sym(const T* lds, int s, 
 
 // Control noise and PD servos of group G's DOFs, before the dynamics.
 template <class M, class T, int G>
-__device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)[M::NV], T (&ctrl)[M::NV], const T* tgt,
+__device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)[M::NV], T (&ctrl)[M::NCTRL], const T* tgt,
                                                u64& rng) {
   // ── control noise: every group advances the whole stream; values only for its DOFs ──
   if constexpr (M::NNOISE > 0) {
@@ -1052,14 +1095,14 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
       sfor<0, M::NNOISE>([&](auto K) {
         constexpr int k = decltype(K)::value;
         T u = uniform01(rng, T(0));
-        if constexpr (M::dof_owner[M::noise_dof[k]] == G)
+        if constexpr (M::ctrl_owner[M::noise_dof[k]] == G)
           ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b - M::noise_a) * u;
       });
     } else {
       sfor<0, (M::NNOISE + 1) / 2>([&](auto K) {
         constexpr int k = 2 * decltype(K)::value;
-        constexpr bool mine0 = M::dof_owner[M::noise_dof[k]] == G;
-        constexpr bool mine1 = k + 1 < M::NNOISE && M::dof_owner[M::noise_dof[k + 1 < M::NNOISE ? k + 1 : k]] == G;
+        constexpr bool mine0 = M::ctrl_owner[M::noise_dof[k]] == G;
+        constexpr bool mine1 = k + 1 < M::NNOISE && M::ctrl_owner[M::noise_dof[k + 1 < M::NNOISE ? k + 1 : k]] == G;
         T u1 = uniform01(rng, T(0));
         T u2 = uniform01(rng, T(0));
         if constexpr (mine0 || mine1) {
@@ -1086,7 +1129,7 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
 // One step of group G for one world (lane). State arrays are in registers; a
 // group reads and writes only the DOFs of its own bodies (plus the trunk's).
 template <class M, class T, int G>
-__device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+__device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NCTRL], T (&qdd)[M::NV],
                                            const T* tgt, u64& rng, T* rows, int S, bool write_rows, T* lds, int lane,
                                            const Terrain<T>& tr) {
   constexpr int NB = M::NB;
@@ -1302,7 +1345,7 @@ template <class M> struct HasExt {
 // response to the change of the contact forces]; integrate.
 // ext, impg (ground) and impp (plane) persist between steps.
 template <class M, class T>
-__device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NV], T (&qdd)[M::NV],
+__device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NCTRL], T (&qdd)[M::NV],
                                              const T* tgt, u64& rng, SV<T> (&ext)[M::NB], T (&impg)[M::NB][24],
                                              T (&impp)[M::NB][24], const Terrain<T>& tr, T* rows, int S,
                                              bool write_rows) {
@@ -1424,17 +1467,21 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
   T* gq = (T*)a.q;
   T* gv = (T*)a.v;
   T* gc = (T*)a.ctrl;
-  T q[M::NQ], v[M::NV], ctrl[M::NV], qdd[M::NV];
+  T q[M::NQ], v[M::NV], ctrl[M::NCTRL], qdd[M::NV];
   sfor<0, M::NQ>([&](auto J) {
     constexpr int j = decltype(J)::value;
     if constexpr (M::dof_group[j] == G || M::dof_group[j] == -1) {
       q[j] = gq[j * S + wl];
       v[j] = gv[j * S + wl];
-      ctrl[j] = gc[j * S + wl];
     } else {
-      q[j] = T(0); v[j] = T(0); ctrl[j] = T(0);
+      q[j] = T(0); v[j] = T(0);
     }
     qdd[j] = T(0);
+  });
+  sfor<0, M::NCTRL>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    if constexpr (M::ctrl_group[j] == G || M::ctrl_group[j] == -1) ctrl[j] = gc[j * S + wl];
+    else ctrl[j] = T(0);
   });
   T tgt[M::NPD > 0 ? M::NPD : 1];
   sfor<0, M::NPD>([&](auto K) {
@@ -1503,9 +1550,12 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
     if constexpr (M::dof_group[j] == G || (G == 0 && M::dof_group[j] == -1)) {
       gq[j * S + w] = q[j];
       gv[j * S + w] = v[j];
-      gc[j * S + w] = ctrl[j];
       ((T*)a.qdd)[j * S + w] = qdd[j];
     }
+  });
+  sfor<0, M::NCTRL>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    if constexpr (M::ctrl_group[j] == G || (G == 0 && M::ctrl_group[j] == -1)) gc[j * S + w] = ctrl[j];
   });
   if constexpr (M::NNOISE > 0 && G == 0) a.rng[w] = rng;
 }

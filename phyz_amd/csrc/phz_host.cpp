@@ -160,6 +160,19 @@ struct Features {
   int dist = 0;
   double a = 0, b = 1;
   std::vector<int> noise_dofs;
+  // Terms of the CPU model that the device body table has no slots for
+  // (joint.rs:27-104, model.rs:18-82): the soft position limit and dry friction
+  // of one-DOF joints (one entry per body; empty: none), and actuators (empty:
+  // ctrl is a per-DOF generalized force; otherwise one control per actuator).
+  struct JointTerm { bool limited = false; double lo = 0, hi = 0, k = 1000, d = 60, floss = 0; };
+  std::vector<JointTerm> jterms;
+  struct Act {
+    int body = 0, q = 0, v = 0;
+    double gear = 1, gain = 1, bq = 0, bv = 0;
+    bool cr = false, fr = false;
+    double clo = 0, chi = 0, flo = 0, fhi = 0;  // sorted bounds
+  };
+  std::vector<Act> acts;
 };
 
 // ── code generation ──────────────────────────────────────────────────────────
@@ -219,38 +232,50 @@ Plan plan_partition(const ModelD& m, const Features& f) {
     any_fixed = any_fixed || trunk[i];
   }
   int mode = 1;
-  if (!any_fixed) {
-    // Floating trunk: every body on a path from a root to a branch point
-    // (a body with two or more children whose subtrees hold two or more bodies).
+  // Floating trunk: every body on a path from a root to a branch point (a body
+  // with two or more children whose subtrees hold two or more bodies). Also
+  // used when the welded bodies have a single articulated subtree (a fixed
+  // forearm under a wrist and a palm): the trunk then runs through the wrist.
+  auto floating = [&]() {
     mode = 2;
+    trunk.assign(nb, 0);
     for (int i = 0; i < nb; i++) {
       int heavy = 0;
       for (int c : kids[i]) heavy += size[c] >= 2;
       if (heavy >= 2)
         for (int j = i; j >= 0; j = m.b[j].parent) trunk[j] = 1;
     }
-  }
-  std::vector<std::vector<int>> parts;
-  for (int i = 0; i < nb; i++) {
-    if (trunk[i] || m.b[i].parent < 0 || !trunk[m.b[i].parent]) continue;
-    std::vector<int> part;
-    for (int j = i; j < nb; j++) {
-      int a = j;
-      while (a >= 0 && a != i && !trunk[a]) a = m.b[a].parent;
-      if (a == i) part.push_back(j);
-    }
-    parts.push_back(part);
-  }
-  for (int i = 0; i < nb; i++)  // floating roots outside any trunk (several independent trees)
-    if (!trunk[i] && m.b[i].parent < 0) {
+  };
+  auto collect = [&]() {
+    std::vector<std::vector<int>> parts;
+    for (int i = 0; i < nb; i++) {
+      if (trunk[i] || m.b[i].parent < 0 || !trunk[m.b[i].parent]) continue;
       std::vector<int> part;
       for (int j = i; j < nb; j++) {
         int a = j;
-        while (a >= 0 && a != i) a = m.b[a].parent;
+        while (a >= 0 && a != i && !trunk[a]) a = m.b[a].parent;
         if (a == i) part.push_back(j);
       }
       parts.push_back(part);
     }
+    for (int i = 0; i < nb; i++)  // floating roots outside any trunk (several independent trees)
+      if (!trunk[i] && m.b[i].parent < 0) {
+        std::vector<int> part;
+        for (int j = i; j < nb; j++) {
+          int a = j;
+          while (a >= 0 && a != i) a = m.b[a].parent;
+          if (a == i) part.push_back(j);
+        }
+        parts.push_back(part);
+      }
+    return parts;
+  };
+  if (!any_fixed) floating();
+  std::vector<std::vector<int>> parts = collect();
+  if (mode == 1 && parts.size() < 2 && want != "1") {
+    floating();
+    parts = collect();
+  }
   const bool forced = want == "1" || want == "2";
   if (parts.size() < 2) return lane_per_world();
   if (mode == 2 && !forced && nb < 14) return lane_per_world();
@@ -455,6 +480,44 @@ std::string gen_model(const ModelD& m, const Features& f) {
   o << "  static constexpr double pd_max[" << npa << "] = " << arr1(npa, [&](int d) { return num(pdv(d, 4)); }) << ";\n";
   o << "  static constexpr int noise_dof[" << nna << "] = "
     << arr1(nna, [&](int k) { return std::to_string(nn ? f.noise_dofs[k] : 0); }) << ";\n";
+  // Actuators and joint limits / dry friction.
+  const int nu = (int)f.acts.size(), nctrl = nu ? nu : m.nv, nua = std::max(nu, 1);
+  const Features::Act act0;
+  auto act = [&](int a) -> const Features::Act& { return nu ? f.acts[a] : act0; };
+  o << "  static constexpr int NU = " << nu << ", NCTRL = " << nctrl << ";\n";
+  auto ia = [&](const char* name, auto get) {
+    o << "  static constexpr int " << name << "[" << nua << "] = " << arr1(nua, [&](int a) { return std::to_string(get(act(a))); }) << ";\n";
+  };
+  auto ba = [&](const char* name, auto get) {
+    o << "  static constexpr bool " << name << "[" << nua << "] = "
+      << arr1(nua, [&](int a) { return std::string(get(act(a)) ? "true" : "false"); }) << ";\n";
+  };
+  auto da = [&](const char* name, auto get) {
+    o << "  static constexpr double " << name << "[" << nua << "] = " << arr1(nua, [&](int a) { return num(get(act(a))); }) << ";\n";
+  };
+  ia("act_v", [](const Features::Act& x) { return x.v; });
+  ia("act_q", [](const Features::Act& x) { return x.q; });
+  da("act_gear", [](const Features::Act& x) { return x.gear; });
+  da("act_gain", [](const Features::Act& x) { return x.gain; });
+  da("act_bq", [](const Features::Act& x) { return x.bq; });
+  da("act_bv", [](const Features::Act& x) { return x.bv; });
+  ba("act_cr", [](const Features::Act& x) { return x.cr; });
+  da("act_clo", [](const Features::Act& x) { return x.clo; });
+  da("act_chi", [](const Features::Act& x) { return x.chi; });
+  ba("act_fr", [](const Features::Act& x) { return x.fr; });
+  da("act_flo", [](const Features::Act& x) { return x.flo; });
+  da("act_fhi", [](const Features::Act& x) { return x.fhi; });
+  o << "  static constexpr int ctrl_group[" << nctrl << "] = "
+    << arr1(nctrl, [&](int c) { return std::to_string(dof_group[nu ? f.acts[c].v : c]); }) << ";\n";
+  o << "  static constexpr int ctrl_owner[" << nctrl << "] = "
+    << arr1(nctrl, [&](int c) { return std::to_string(dof_owner[nu ? f.acts[c].v : c]); }) << ";\n";
+  const bool jt = !f.jterms.empty();
+  bb("lim_on", [&](int i) { return jt && f.jterms[i].limited && ndof_of(m.b[i].jtype) == 1; });
+  db("lim_lo", [&](int i) { return jt ? f.jterms[i].lo : 0.0; });
+  db("lim_hi", [&](int i) { return jt ? f.jterms[i].hi : 0.0; });
+  db("lim_k", [&](int i) { return jt ? f.jterms[i].k : 0.0; });
+  db("lim_d", [&](int i) { return jt ? f.jterms[i].d : 0.0; });
+  db("floss", [&](int i) { return jt && ndof_of(m.b[i].jtype) == 1 ? f.jterms[i].floss : 0.0; });
   o << "};\n";
   return o.str();
 }
@@ -845,6 +908,8 @@ struct Kern {
 struct phz_sim {
   ModelD model;
   Features feat;
+  int ctrl_rows = 0;  // rows the ctrl buffer holds (nv at create; grows for actuators)
+  int nctrl() const { return feat.acts.empty() ? model.nv : (int)feat.acts.size(); }
   int nworld = 0, stride = 0;
   bool f64 = false;
   int device = -1;
@@ -1313,12 +1378,13 @@ int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t 
     }
     const size_t E = s->esize(), S = (size_t)s->stride;
     if (!s->alloc(&s->q, (size_t)nq * S * E, "alloc q") || !s->alloc(&s->v, (size_t)nv * S * E, "alloc v") ||
-        !s->alloc(&s->ctrl, (size_t)nv * S * E, "alloc ctrl") || !s->alloc(&s->qdd, (size_t)nv * S * E, "alloc qdd") ||
+        !s->alloc(&s->ctrl, (size_t)std::max(nv, 1u) * S * E, "alloc ctrl") || !s->alloc(&s->qdd, (size_t)nv * S * E, "alloc qdd") ||
         !s->alloc((void**)&s->rng, S * 8, "alloc rng") ||
         !s->hip_ok(hipStreamSynchronize(s->stream), "create sync")) {
       g_create_error = s->err;
       return 1;
     }
+    s->ctrl_rows = (int)std::max(nv, 1u);
   }
   *out = s.release();
   return 0;
@@ -1497,6 +1563,8 @@ int phz_load_contact_state(phz_sim* s, const double* cs, const double* ext) {
 int phz_enable_pd_control(phz_sim* s, const double* dofs, uint32_t n) {
   if (!s) return 1;
   if (n == 0 || !dofs) return s->fail("PD pipeline needs at least one servoed DOF");
+  if (!s->feat.acts.empty())
+    return s->fail("PD servos write per-DOF controls, but this model's controls drive its actuators");
   for (uint32_t d = 0; d < n; d++) {
     const double* r = dofs + (size_t)d * kPdStride;
     if (!is_int(r[0]) || !is_int(r[1]) || r[0] < 0 || r[1] < 0 || r[0] >= s->model.nq || r[1] >= s->model.nv)
@@ -1533,7 +1601,8 @@ int phz_enable_control_noise(phz_sim* s, uint64_t seed, int dist, double a, doub
   if (n > 0 && !v_indices) return s->fail("null DOF list");
   std::vector<int> dofs;
   for (uint32_t k = 0; k < n; k++) {
-    if (v_indices[k] >= (uint32_t)s->model.nv) return s->fail(fmt("noise DOF %u out of range (nv %d)", v_indices[k], s->model.nv));
+    if (v_indices[k] >= (uint32_t)s->nctrl())
+      return s->fail(fmt("noise control %u out of range (%d controls)", v_indices[k], s->nctrl()));
     dofs.push_back((int)v_indices[k]);
   }
   if (!set_device(s)) return 1;
@@ -1548,6 +1617,72 @@ int phz_enable_control_noise(phz_sim* s, uint64_t seed, int dist, double a, doub
   return 0;
 }
 
+int phz_set_joint_terms(phz_sim* s, const double* table) {
+  if (!s) return 1;
+  const int nb = s->model.nb;
+  std::vector<Features::JointTerm> jt;
+  if (table) {
+    jt.resize(nb);
+    for (int i = 0; i < nb; i++) {
+      const double* r = table + (size_t)i * 8;
+      for (int k = 0; k < 6; k++)
+        if (!std::isfinite(r[k])) return s->fail(fmt("joint terms of body %d: non-finite value in slot %d", i, k));
+      if (r[3] < 0 || r[4] < 0 || r[5] < 0)
+        return s->fail(fmt("joint terms of body %d: limit stiffness, damping and friction loss must be >= 0", i));
+      jt[i] = Features::JointTerm{r[0] != 0.0, r[1], r[2], r[3], r[4], r[5]};
+    }
+  }
+  s->feat.jterms = jt;
+  s->invalidate();
+  return 0;
+}
+
+int phz_set_actuators(phz_sim* s, const double* table, uint32_t n) {
+  if (!s) return 1;
+  if (n > 0 && !table) return s->fail("null actuator table");
+  if (n > 0 && s->feat.npd > 0)
+    return s->fail("PD servos write per-DOF controls; a model with actuators cannot also have PD servos");
+  std::vector<Features::Act> acts(n);
+  for (uint32_t a = 0; a < n; a++) {
+    const double* r = table + (size_t)a * 16;
+    for (int k = 0; k < 11; k++)
+      if (!std::isfinite(r[k])) return s->fail(fmt("actuator %u: non-finite value in slot %d", a, k));
+    if (!is_int(r[0]) || r[0] < 0 || r[0] >= s->model.nb)
+      return s->fail(fmt("actuator %u: joint %g out of range (%d joints)", a, r[0], s->model.nb));
+    const BodyD& b = s->model.b[(int)r[0]];
+    if (ndof_of(b.jtype) == 0) return s->fail(fmt("actuator %u drives joint %d, which has no DOF", a, (int)r[0]));
+    Features::Act& x = acts[a];
+    x.body = (int)r[0]; x.q = b.qoff; x.v = b.voff;
+    x.gear = r[1]; x.gain = r[2]; x.bq = r[3]; x.bv = r[4];
+    x.cr = r[5] != 0.0; x.clo = std::min(r[6], r[7]); x.chi = std::max(r[6], r[7]);
+    x.fr = r[8] != 0.0; x.flo = std::min(r[9], r[10]); x.fhi = std::max(r[9], r[10]);
+  }
+  const int nctrl = n ? (int)n : s->model.nv;
+  if (s->feat.noise)
+    for (int d : s->feat.noise_dofs)
+      if (d >= nctrl) return s->fail(fmt("noise control %d out of range (%d controls)", d, nctrl));
+  if (!set_device(s)) return 1;
+  if (s->has_device()) {
+    const size_t bytes = (size_t)std::max(nctrl, 1) * s->stride * s->esize();
+    if (nctrl > s->ctrl_rows) {
+      s->invalidate();
+      if (!s->hip_ok(hipStreamSynchronize(s->stream), "actuators sync")) return 1;
+      hipFree(s->ctrl);
+      s->ctrl = nullptr;
+      if (!s->alloc(&s->ctrl, bytes, "ctrl alloc")) return 1;
+      s->ctrl_rows = nctrl;
+    }
+    // Controls change meaning (per DOF <-> per actuator): start from zero.
+    if (!s->hip_ok(phz_io_zero(s->ctrl, bytes, s->stream), "zero ctrl") ||
+        !s->hip_ok(hipStreamSynchronize(s->stream), "actuators sync"))
+      return 1;
+  }
+  s->feat.acts = acts;
+  s->invalidate();
+  return 0;
+}
+int phz_nctrl(const phz_sim* s) { return s ? s->nctrl() : 0; }
+
 int phz_load_states(phz_sim* s, const double* q, const double* v, const double* ctrl) {
   if (!s) return 1;
   if (!q || !v) return s->fail("null q or v");
@@ -1555,8 +1690,8 @@ int phz_load_states(phz_sim* s, const double* q, const double* v, const double* 
   if (!set_device(s)) return 1;
   if (!s->upload_rows(q, s->q, s->model.nq, "upload q") || !s->upload_rows(v, s->v, s->model.nv, "upload v")) return 1;
   if (ctrl) {
-    if (!s->upload_rows(ctrl, s->ctrl, s->model.nv, "upload ctrl")) return 1;
-  } else if (!s->hip_ok(phz_io_zero(s->ctrl, (size_t)s->model.nv * s->stride * s->esize(), s->stream), "zero ctrl")) {
+    if (!s->upload_rows(ctrl, s->ctrl, s->nctrl(), "upload ctrl")) return 1;
+  } else if (!s->hip_ok(phz_io_zero(s->ctrl, (size_t)s->nctrl() * s->stride * s->esize(), s->stream), "zero ctrl")) {
     return 1;
   }
   if (s->feat.noise && !s->hip_ok(phz_io_seed(s->rng, s->feat.seed, s->nworld, s->stream), "seed rng")) return 1;
@@ -1568,7 +1703,7 @@ int phz_set_controls(phz_sim* s, const double* ctrl) {
   if (!ctrl) return s->fail("null ctrl");
   if (!s->has_device()) return s->fail("host-only sim has no device buffers");
   if (!set_device(s)) return 1;
-  if (!s->upload_rows(ctrl, s->ctrl, s->model.nv, "upload ctrl")) return 1;
+  if (!s->upload_rows(ctrl, s->ctrl, s->nctrl(), "upload ctrl")) return 1;
   return s->hip_ok(hipStreamSynchronize(s->stream), "set_controls") ? 0 : 1;
 }
 
@@ -1607,7 +1742,7 @@ int phz_readback_controls(phz_sim* s, double* ctrl) {
   if (!s || !ctrl) return 1;
   if (!s->has_device()) return s->fail("host-only sim has no device buffers");
   if (!set_device(s)) return 1;
-  return s->download_rows(s->ctrl, ctrl, s->model.nv, "readback ctrl") ? 0 : 1;
+  return s->download_rows(s->ctrl, ctrl, s->nctrl(), "readback ctrl") ? 0 : 1;
 }
 int phz_readback_qdd(phz_sim* s, double* qdd) {
   if (!s || !qdd) return 1;

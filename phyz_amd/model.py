@@ -28,6 +28,10 @@ G_NONE, G_SPHERE, G_BOX, G_CAPSULE, G_CYLINDER, G_MESH = 0, 1, 2, 3, 4, 5
 
 BODY_STRIDE = 36
 GEOM_STRIDE = 24
+JOINT_TERMS_STRIDE = 8
+ACTUATOR_STRIDE = 16
+DEFAULT_LIMIT_STIFFNESS = 1000.0  # joint.rs:96-104
+DEFAULT_LIMIT_DAMPING = 60.0
 PD_DOF_STRIDE = 8
 CONTACT_ROW = 8
 MAX_BODIES = 32
@@ -142,9 +146,67 @@ class Joint:
     stiffness: float = 0.0
     spring_ref: float = 0.0
     armature: float = 0.0
+    # Terms of the CPU model that the device body table does not carry
+    # (joint.rs:27-104): the soft position limit and dry friction of a one-DOF joint.
+    limits: Optional[Sequence[float]] = None
+    limit_stiffness: float = DEFAULT_LIMIT_STIFFNESS
+    limit_damping: float = DEFAULT_LIMIT_DAMPING
+    friction_loss: float = 0.0
+    name: str = ""
 
     def ndof(self) -> int:
         return joint_ndof(self.jtype)
+
+    def limit_force(self, q: float, qd: float) -> float:
+        """Soft joint-limit force (joint.rs:196-226): zero inside the range or on a
+        multi-DOF joint; past a bound, a spring on the depth plus damping that
+        only resists motion further into the limit."""
+        if self.ndof() != 1 or self.limits is None:
+            return 0.0
+        lo, hi = self.limits
+        if q < lo:
+            depth, sign = lo - q, 1.0
+        elif q > hi:
+            depth, sign = q - hi, -1.0
+        else:
+            return 0.0
+        return sign * (self.limit_stiffness * depth + self.limit_damping * max(-sign * qd, 0.0))
+
+
+@dataclasses.dataclass
+class Actuator:
+    """Drives the first DOF of one joint (phyz_model::Actuator, model.rs:18-82):
+    f = gear (gain clamp(ctrl) + bias_q q + bias_v v), then the force range."""
+    name: str
+    joint_name: str
+    joint_idx: int  # body index: one joint per body
+    gear: float = 1.0
+    ctrl_range: Optional[Sequence[float]] = None
+    gain: float = 1.0
+    bias_q: float = 0.0
+    bias_v: float = 0.0
+    force_range: Optional[Sequence[float]] = None
+
+    def clamp_ctrl(self, ctrl: float) -> float:
+        if self.ctrl_range is None:
+            return ctrl
+        lo, hi = self.ctrl_range
+        return min(max(ctrl, min(lo, hi)), max(lo, hi))
+
+    def force_at(self, ctrl: float, q: float, v: float) -> float:
+        f = self.gear * (self.gain * self.clamp_ctrl(ctrl) + self.bias_q * q + self.bias_v * v)
+        if self.force_range is not None:
+            lo, hi = self.force_range
+            f = min(max(f, min(lo, hi)), max(lo, hi))
+        return f
+
+    @staticmethod
+    def motor(name: str, joint_name: str, joint_idx: int, gear: float) -> "Actuator":
+        return Actuator(name, joint_name, joint_idx, gear)
+
+    @staticmethod
+    def position(name: str, joint_name: str, joint_idx: int, gear: float, kp: float, kv: float) -> "Actuator":
+        return Actuator(name, joint_name, joint_idx, gear, gain=kp, bias_q=-kp, bias_v=-kv)
 
 
 @dataclasses.dataclass
@@ -153,7 +215,8 @@ class Body:
     parent: int
     joint: Joint
     inertia: SpatialInertia
-    geometry: Optional[Geometry] = None
+    geometry: Optional[Geometry] = None  # the contact shape (the first collision geom)
+    collisions: List[Geometry] = dataclasses.field(default_factory=list)  # all collision geoms, in order
 
 
 @dataclasses.dataclass
@@ -165,10 +228,27 @@ class Model:
     nv: int
     q_offsets: List[int]
     v_offsets: List[int]
+    actuators: List[Actuator] = dataclasses.field(default_factory=list)
 
     @property
     def nbodies(self) -> int:
         return len(self.bodies)
+
+    @property
+    def joints(self) -> List[Joint]:
+        return [b.joint for b in self.bodies]
+
+    def nu(self) -> int:
+        """Number of actuators (MuJoCo's nu)."""
+        return len(self.actuators)
+
+    def nctrl(self) -> int:
+        """Controls per world: one per actuator, or one per DOF without actuators."""
+        return self.nu() if self.actuators else self.nv
+
+    def has_joint_terms(self) -> bool:
+        return any(b.joint.ndof() == 1 and (b.joint.limits is not None or b.joint.friction_loss > 0.0)
+                   for b in self.bodies)
 
     def default_state(self):
         return np.zeros(self.nq), np.zeros(self.nv)
@@ -179,6 +259,7 @@ class ModelBuilder:
 
     def __init__(self):
         self._bodies: List[Body] = []
+        self._actuators: List[Actuator] = []
         self._gravity = np.array([0.0, 0.0, -GRAVITY])
         self._dt = 0.001
 
@@ -204,6 +285,10 @@ class ModelBuilder:
     def add_spherical_body(self, name, parent, parent_to_joint, inertia, **kw):
         return self.add_body(name, parent, Joint(BALL, parent_to_joint, np.zeros(3), **kw), inertia)
 
+    def add_actuator(self, actuator: Actuator) -> "ModelBuilder":
+        self._actuators.append(actuator)
+        return self
+
     def add_free_body(self, name, parent, parent_to_joint, inertia, geometry=None):
         return self.add_body(name, parent, Joint(FREE, parent_to_joint, np.zeros(3)), inertia, geometry)
 
@@ -218,7 +303,7 @@ class ModelBuilder:
             vo.append(nv)
             nq += b.joint.ndof()
             nv += b.joint.ndof()
-        return Model(list(self._bodies), self._gravity.copy(), self._dt, nq, nv, qo, vo)
+        return Model(list(self._bodies), self._gravity.copy(), self._dt, nq, nv, qo, vo, list(self._actuators))
 
 
 def pack_bodies(model: Model) -> np.ndarray:
@@ -245,6 +330,34 @@ def pack_bodies(model: Model) -> np.ndarray:
     return t
 
 
+def pack_joint_terms(model: Model) -> np.ndarray:
+    """Joint terms, nb x 8 f64: [limited, lo, hi, limit_k, limit_d, friction_loss, 0, 0]
+    (an extension table: the reference's device body table has no such slots)."""
+    t = np.zeros((model.nbodies, JOINT_TERMS_STRIDE), dtype=np.float64)
+    for i, b in enumerate(model.bodies):
+        j = b.joint
+        lim = j.limits is not None and j.ndof() == 1
+        t[i, 0] = 1.0 if lim else 0.0
+        if lim:
+            t[i, 1], t[i, 2] = j.limits
+        t[i, 3], t[i, 4] = j.limit_stiffness, j.limit_damping
+        t[i, 5] = j.friction_loss if j.ndof() == 1 else 0.0
+    return t
+
+
+def pack_actuators(model: Model) -> np.ndarray:
+    """Actuators, nu x 16 f64: [body, gear, gain, bias_q, bias_v, has_ctrl_range,
+    ctrl_lo, ctrl_hi, has_force_range, force_lo, force_hi, 0 ...]."""
+    t = np.zeros((model.nu(), ACTUATOR_STRIDE), dtype=np.float64)
+    for a, act in enumerate(model.actuators):
+        t[a, 0:5] = [act.joint_idx, act.gear, act.gain, act.bias_q, act.bias_v]
+        if act.ctrl_range is not None:
+            t[a, 5:8] = [1.0, act.ctrl_range[0], act.ctrl_range[1]]
+        if act.force_range is not None:
+            t[a, 8:11] = [1.0, act.force_range[0], act.force_range[1]]
+    return t
+
+
 def pack_geometries(model: Model, stiffness: float = 0.0, damping: float = 0.0,
                     gains: Optional[Sequence] = None):
     """Geometry table, nb x 24 f64 (pack_geometries, layout.rs:182-280).
@@ -258,7 +371,7 @@ def pack_geometries(model: Model, stiffness: float = 0.0, damping: float = 0.0,
     for i, b in enumerate(model.bodies):
         g[i, 13:22] = np.eye(3).reshape(9)
         geo = b.geometry
-        if geo is not None:
+        if geo is not None and geo.kind != G_NONE:
             g[i, 10:13] = geo.origin.pos
             g[i, 13:22] = geo.origin.rot.reshape(9)
             g[i, 0] = geo.kind
@@ -270,6 +383,46 @@ def pack_geometries(model: Model, stiffness: float = 0.0, damping: float = 0.0,
         else:
             g[i, 8], g[i, 9] = stiffness, damping
     return g, collidable
+
+
+def model_from_tables(body: np.ndarray, geom: Optional[np.ndarray], gravity, dt: float, nq: int, nv: int,
+                      joint_terms: Optional[np.ndarray] = None, actuators: Optional[np.ndarray] = None,
+                      body_names: Optional[Sequence[str]] = None, joint_names: Optional[Sequence[str]] = None,
+                      actuator_names: Optional[Sequence[str]] = None) -> Model:
+    """The Model that pack_bodies / pack_geometries / pack_joint_terms /
+    pack_actuators describe (their inverse, names optional)."""
+    body = np.asarray(body, dtype=np.float64).reshape(-1, BODY_STRIDE)
+    nb = body.shape[0]
+    bodies, qo, vo = [], [], []
+    for i in range(nb):
+        r = body[i]
+        I = np.array([[r[8], r[11], r[12]], [r[11], r[9], r[13]], [r[12], r[13], r[10]]])
+        j = Joint(int(r[1]), SpatialTransform.new(r[14:23].reshape(3, 3), r[23:26]), r[26:29].copy(),
+                  damping=float(r[29]), stiffness=float(r[30]), spring_ref=float(r[31]), armature=float(r[32]),
+                  name="" if joint_names is None else str(joint_names[i]))
+        if joint_terms is not None:
+            t = np.asarray(joint_terms, dtype=np.float64).reshape(nb, JOINT_TERMS_STRIDE)[i]
+            j.limits = (float(t[1]), float(t[2])) if t[0] != 0.0 else None
+            j.limit_stiffness, j.limit_damping, j.friction_loss = float(t[3]), float(t[4]), float(t[5])
+        geo = None
+        if geom is not None:
+            g = np.asarray(geom, dtype=np.float64).reshape(nb, GEOM_STRIDE)[i]
+            if int(g[0]) != G_NONE:
+                npar = {G_SPHERE: 1, G_BOX: 3, G_CAPSULE: 2, G_CYLINDER: 2, G_MESH: 6}[int(g[0])]
+                geo = Geometry(int(g[0]), tuple(float(x) for x in g[1:1 + npar]),
+                               SpatialTransform.new(g[13:22].reshape(3, 3), g[10:13]))
+        name = f"body_{i}" if body_names is None else str(body_names[i])
+        bodies.append(Body(name, int(r[0]), j, SpatialInertia.new(r[4], r[5:8], I), geo, [] if geo is None else [geo]))
+        qo.append(int(r[2]))
+        vo.append(int(r[3]))
+    acts = []
+    if actuators is not None:
+        for a, r in enumerate(np.asarray(actuators, dtype=np.float64).reshape(-1, ACTUATOR_STRIDE)):
+            jn = bodies[int(r[0])].joint.name
+            acts.append(Actuator("" if actuator_names is None else str(actuator_names[a]), jn, int(r[0]), float(r[1]),
+                                 (float(r[6]), float(r[7])) if r[5] != 0.0 else None, float(r[2]), float(r[3]),
+                                 float(r[4]), (float(r[9]), float(r[10])) if r[8] != 0.0 else None))
+    return Model(bodies, np.asarray(gravity, dtype=np.float64).copy(), float(dt), int(nq), int(nv), qo, vo, acts)
 
 
 def uniform_frequency_gains(model: Model, omega: float, zeta: float):

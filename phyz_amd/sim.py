@@ -16,7 +16,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _lib
-from .model import Model, PdDof, pack_bodies, pack_geometries, pack_pd_dofs
+from .model import Model, PdDof, pack_actuators, pack_bodies, pack_geometries, pack_joint_terms, pack_pd_dofs
 from .policy import XF_STRIDE, PolicySpec, pack_obs_ops
 
 F32, F64 = 0, 1
@@ -41,7 +41,10 @@ def _rows(a, n, width, name) -> np.ndarray:
 class BatchSim:
     """`nworld` copies of one model stepped in lockstep on one MI355X."""
 
-    def __init__(self, model: Model, nworld: int, precision: str = "f32", device: int = 0):
+    def __init__(self, model: Model, nworld: int, precision: str = "f32", device: int = 0, model_terms: bool = True):
+        """model_terms: apply the model's actuators, joint limits and friction
+        loss (terms of the reference's CPU model that its device pass leaves
+        out); ctrl then holds one control per actuator."""
         self._L = _lib.load()
         self.model = model
         self.nworld = int(nworld)
@@ -56,6 +59,29 @@ class BatchSim:
         if rc != 0:
             raise PhzError(self._L.phz_last_error(None).decode())
         self._h = h
+        if model_terms:
+            if model.has_joint_terms():
+                self.set_joint_terms(pack_joint_terms(model))
+            if model.actuators:
+                self.set_actuators(pack_actuators(model))
+
+    # ── model terms beyond the device body table ──
+    def set_joint_terms(self, table: Optional[np.ndarray]):
+        """Limits and friction loss per body, nb x 8 (phyz_amd.model.pack_joint_terms); None clears."""
+        t = None if table is None else np.ascontiguousarray(np.asarray(table, dtype=np.float64).reshape(self.nb, 8))
+        self._check(self._L.phz_set_joint_terms(self._h, _dp(t)))
+
+    def set_actuators(self, table: Optional[np.ndarray]):
+        """Actuators, nu x 16 (phyz_amd.model.pack_actuators); None or no rows clears.
+        Controls become one per actuator (zeroed)."""
+        t = None if table is None else np.ascontiguousarray(np.asarray(table, dtype=np.float64).reshape(-1, 16))
+        n = 0 if t is None else t.shape[0]
+        self._check(self._L.phz_set_actuators(self._h, _dp(t), n))
+
+    @property
+    def nctrl(self) -> int:
+        """Controls per world: one per actuator, or one per DOF."""
+        return int(self._L.phz_nctrl(self._h))
 
     # ── lifecycle ──
     def close(self):
@@ -180,11 +206,11 @@ class BatchSim:
     def load_states(self, q, v, ctrl=None):
         qq = _rows(q, self.nworld, self.nq, "q")
         vv = _rows(v, self.nworld, self.nv, "v")
-        cc = None if ctrl is None else _rows(ctrl, self.nworld, self.nv, "ctrl")
+        cc = None if ctrl is None else _rows(ctrl, self.nworld, self.nctrl, "ctrl")
         self._check(self._L.phz_load_states(self._h, _dp(qq), _dp(vv), _dp(cc)))
 
     def set_controls(self, ctrl):
-        self._check(self._L.phz_set_controls(self._h, _dp(_rows(ctrl, self.nworld, self.nv, "ctrl"))))
+        self._check(self._L.phz_set_controls(self._h, _dp(_rows(ctrl, self.nworld, self.nctrl, "ctrl"))))
 
     def readback_states(self):
         q = np.zeros((self.nworld, self.nq))
@@ -198,7 +224,7 @@ class BatchSim:
         return rows
 
     def readback_controls(self) -> np.ndarray:
-        c = np.zeros((self.nworld, self.nv))
+        c = np.zeros((self.nworld, self.nctrl))
         self._check(self._L.phz_readback_controls(self._h, _dp(c)))
         return c
 

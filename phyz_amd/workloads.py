@@ -32,12 +32,14 @@ from __future__ import annotations
 
 import dataclasses
 import math
+import os
 from typing import List, Optional, Tuple
 
 import numpy as np
 
 from .model import (BALL, FIXED, FREE, PRISMATIC, REVOLUTE, Geometry, Heightfield, Joint, Model, ModelBuilder,
-                    PdDof, SpatialInertia, SpatialTransform, pack_geometries, pack_pd_dofs, rotation_axis_angle)
+                    PdDof, SpatialInertia, SpatialTransform, model_from_tables, pack_geometries, pack_pd_dofs,
+                    rotation_axis_angle)
 
 NOISE_NORMAL = 0
 NOISE_UNIFORM = 1
@@ -342,6 +344,23 @@ def rolling_terrain(n: int = 41, cell: float = 0.2, amp: float = 0.06, seed: int
         h += np.sin(k * (math.cos(th) * X + math.sin(th) * Y) + ph)
     h *= amp / np.abs(h).max()
     return Heightfield(origin=(float(xs[0]), float(xs[0]), 0.0), cell=cell, nx=n, ny=n, heights=h)
+
+
+# ── the reference's MJCF benchmark models ───────────────────────────────────
+MJCF_TABLES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "golden",
+                           "mjcf_models.npz")
+
+
+def mjcf_model(name: str) -> Model:
+    """One of the reference's benchmark MJCF models (ant, humanoid, shadow_hand,
+    half_cheetah, simple_arm) as phyz_amd.mjcf loads it, from the packed tables
+    tests/golden/make_mjcf_models.py wrote (the model files stay in the reference)."""
+    z = np.load(MJCF_TABLES)
+    g = lambda k: z[f"{name}/{k}"]  # noqa: E731
+    nq, nv, dt = g("dims")
+    acts = g("actuators")
+    return model_from_tables(g("body"), g("geom"), g("gravity"), dt, int(nq), int(nv), g("joint_terms"),
+                             acts if acts.size else None, g("body_names"), g("joint_names"), g("actuator_names"))
 
 
 # ── control loop: the ant driven by an on-device policy ─────────────────────
