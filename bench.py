@@ -23,6 +23,9 @@ it also checks one device step of the sampled worlds against the oracle.
 terrain_impulse (unless --no-impulse): the same measurement of workload 6, the
 ant on a rolling heightfield with impulse-mode contact (16 sweeps per step),
 131072 worlds x 1000 steps, f32, with its own roofline, CPU baseline and parity.
+mjcf (unless --no-mjcf): workloads 7-9, the reference's MJCF ant, humanoid and
+hand driven by their own actuators, f32, with the share of worlds that stay
+finite (the reference's explicit joint-limit law diverges on the lightest links).
 control_loop (unless --no-control): the ant driven by the on-device policy.
 """
 from __future__ import annotations
@@ -120,9 +123,10 @@ def device_step_parity(w, sim, prec):
     from the device's carried contact forces and warm-start impulses."""
     import dataclasses
     from tests.helpers import as_precision, oracle_for, rel_err_rows
-    idx = np.linspace(0, w.nworld - 1, 64).astype(int)
     imp = w.impulse_sweeps > 0
     qg, vg = sim.readback_states()
+    finite = np.flatnonzero(np.isfinite(qg).all(axis=1) & np.isfinite(vg).all(axis=1))
+    idx = finite[np.linspace(0, len(finite) - 1, 64).astype(int)]
     if imp:
         cs0, ext0 = sim.readback_contact_state()
         cs0, ext0 = np.ascontiguousarray(cs0[idx]), np.ascontiguousarray(ext0[idx])
@@ -148,6 +152,7 @@ def device_step_parity(w, sim, prec):
 
 
 def cpu_baseline(w, sim, prec, budget_s=20.0):
+    """budget_s: seconds of multi-threaded oracle time for the timed sample."""
     """Oracle (f64 port of the reference CPU step) on the host cores, on a bounded
     sample of the workload; plus a one-step parity check of the sampled worlds."""
     from tests.helpers import oracle_for
@@ -309,10 +314,12 @@ def config_of(w, r):
         c["heightfield"] = {"nx": h.nx, "ny": h.ny, "cell": h.cell}
     if w.impulse_sweeps > 0:
         c["contact"] = {"mode": "impulse", "sweeps": w.impulse_sweeps}
+    if w.model.actuators:
+        c["actuators"] = w.model.nu()
     return c
 
 
-def measure(w, precs, steps, warmup, reps, with_cpu):
+def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=20.0):
     """Event-timed spans of `steps` steps per precision, the roofline of the step
     kernel, and (with_cpu) the oracle's CPU rate plus a one-step parity check."""
     flops_tab = json.load(open(FLOPS_JSON))
@@ -327,8 +334,11 @@ def measure(w, precs, steps, warmup, reps, with_cpu):
         ws = w.nworld * steps / wall
         med = float(np.median(ev))
         spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
+        qf, vf = sim.readback_states()
+        finite = float(np.mean(np.isfinite(qf).all(axis=1) & np.isfinite(vf).all(axis=1)))
         results[prec] = {
             "value": round(ws, 1),
+            "finite_worlds": round(finite, 4),
             "ms_per_step": round(wall * 1e3 / steps, 6),
             "event_ms_per_span": {"median": round(med, 4), "min": round(float(min(ev)), 4),
                                   "max": round(float(max(ev)), 4), "reps": len(ev), "noisy": bool(spread > 0.25)},
@@ -344,7 +354,7 @@ def measure(w, precs, steps, warmup, reps, with_cpu):
     if with_cpu:
         for prec in precs:
             log(f"[bench] {w.name}: cpu_baseline + parity check ({prec})")
-            c, p = cpu_baseline(w, sims[prec], prec)
+            c, p = cpu_baseline(w, sims[prec], prec, cpu_budget_s)
             parity[prec] = p
             if prec == primary:
                 cpu = c
@@ -364,6 +374,8 @@ def main():
     ap.add_argument("--no-control", action="store_true", help="skip the on-device control-loop measurement")
     ap.add_argument("--no-impulse", action="store_true",
                     help="skip the terrain + impulse-contact measurement (workload 6)")
+    ap.add_argument("--no-mjcf", action="store_true",
+                    help="skip the MJCF-model measurements (workloads 7-9)")
     ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
     ap.add_argument("--precision", choices=["f32", "f64"], default=None, help="run one precision only")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -433,6 +445,17 @@ def main():
                                    "roofline": pi["roofline"], "cpu_baseline": ri["cpu"],
                                    "event_ms_per_span": pi["event_ms_per_span"], "kernel": pi["kernel"],
                                    "parity": ri["parity"].get("f32")}
+    if not args.no_mjcf and args.workload not in W.MJCF_WORKLOADS:
+        line["mjcf"] = {}
+        for idx in sorted(W.MJCF_WORKLOADS):
+            wm = W.config(idx)
+            rm = measure(wm, ["f32"], wm.nsteps, wm.nsteps, 3, not args.no_cpu, cpu_budget_s=8.0)
+            pm = rm["results"]["f32"]
+            line["mjcf"][wm.name] = {"value": pm["value"], "unit": "world-steps/s", "dtype": "f32",
+                                     "finite_worlds": pm["finite_worlds"], "config": config_of(wm, pm),
+                                     "roofline": pm["roofline"], "cpu_baseline": rm["cpu"],
+                                     "event_ms_per_span": pm["event_ms_per_span"], "kernel": pm["kernel"],
+                                     "parity": rm["parity"].get("f32")}
     if not args.no_control:
         line["control_loop"] = run_control_loop("f32", min(args.reps, 5), not args.no_cpu)
     print(json.dumps(line), flush=True)

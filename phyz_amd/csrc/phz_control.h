@@ -126,7 +126,7 @@ __device__ __forceinline__ T obs_feature(const T* q, const T* v, const FKState<M
           mt = mt + T(M::mass[i]);
         }
       });
-      if (mt > T(0)) com = com * (T(1) / mt);
+      if (mt > T(0)) com = com * (T(1) / dmax(mt, T(1e-30)));
       V3<T> tgt = v3(T(0), T(0), T(0));
       sfor<0, b>([&](auto J) {
         constexpr int base = a + 2 + 4 * decltype(J)::value;

@@ -49,12 +49,54 @@ enum { G_NONE = 0, G_SPHERE = 1, G_BOX = 2, G_CAPSULE = 3, G_CYLINDER = 4, G_MES
 constexpr int ndof_of(int jt) { return jt == J_FIXED ? 0 : (jt == J_BALL ? 3 : (jt == J_FREE ? 6 : 1)); }
 
 // ── math ─────────────────────────────────────────────────────────────────────
-// Kernels are compiled with -ffinite-math-only: no expression may produce an
-// inf or NaN even on a path a select later discards, so every division whose
-// denominator can vanish divides by a guarded value (`x / (ok ? d : 1)`).
+// Kernels are compiled with -ffinite-math-only (the f64 impulse-mode step
+// kernel excepted), which lets 0 * x fold away against the model's constant
+// zeros. It also makes a NaN or inf anywhere in a floating-point select
+// poison, the arm not taken included, and the compiler evaluates both arms. So
+// no expression may produce one even on a discarded path: a division whose
+// denominator can vanish divides by dmax(d, floor), with the floor below the
+// select's own threshold so that the bound cannot be folded back into d.
 __device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
 __device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
+// sin and cos of a Box-Muller angle x in [0, 2*pi] (f64). x = k*pi/2 + r with
+// k = rint(2x/pi) in 0..4 and pi/2 split as hi + lo, hi holding 33 significant
+// bits so that k*hi and x - k*hi are exact; |r| <= pi/4 and the split's residual
+// is 3.5e-27. sin r and cos r are their Taylor series through r^17 and r^18,
+// whose truncation stays below 1e-19 on |r| <= pi/4. In an IEEE build of the
+// chain kernel the library sincos gave one of these sines a sign that varied
+// from launch to launch (its optimised IR was correct); this closed form has
+// no such dependence and costs less than the general reduction.
+__device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
+  const double k = rint(x * 0x1.45f306dc9c883p-1);
+  const double r = (x - k * 0x1.921fb54400000p+0) - k * 0x1.0b4611a626331p-34;
+  const double r2 = r * r;
+  double ps = 1.0 / 355687428096000.0;  // 1/17!
+  ps = fma(ps, -r2, 1.0 / 1307674368000.0);
+  ps = fma(ps, -r2, 1.0 / 6227020800.0);
+  ps = fma(ps, -r2, 1.0 / 39916800.0);
+  ps = fma(ps, -r2, 1.0 / 362880.0);
+  ps = fma(ps, -r2, 1.0 / 5040.0);
+  ps = fma(ps, -r2, 1.0 / 120.0);
+  ps = fma(ps, -r2, 1.0 / 6.0);
+  const double sr = fma(-r * r2, ps, r);
+  double pc = 1.0 / 6402373705728000.0;  // 1/18!
+  pc = fma(pc, -r2, 1.0 / 20922789888000.0);
+  pc = fma(pc, -r2, 1.0 / 87178291200.0);
+  pc = fma(pc, -r2, 1.0 / 479001600.0);
+  pc = fma(pc, -r2, 1.0 / 3628800.0);
+  pc = fma(pc, -r2, 1.0 / 40320.0);
+  pc = fma(pc, -r2, 1.0 / 720.0);
+  pc = fma(pc, -r2, 1.0 / 24.0);
+  pc = fma(pc, -r2, 0.5);
+  const double cr = fma(-r2, pc, 1.0);
+  const int q = (int)k & 3;
+  const double a = (q & 1) ? cr : sr;
+  const double b = (q & 1) ? sr : cr;
+  *s = (q & 2) ? -a : a;
+  *c = ((q + 1) & 2) ? -b : b;
+}
+__device__ __forceinline__ void angle_sincos(float x, float* s, float* c) { sincosf(x, s, c); }
 __device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double dlog(double x) { return log(x); }
 __device__ __forceinline__ float dlog(float x) { return logf(x); }
@@ -240,14 +282,14 @@ template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
   T s, c;
   dsincos(ang * T(0.5), &s, &c);
   const bool small = ang < T(Eps<T>::v);
-  T f = small ? T(0.5) : s / (small ? T(1) : ang);
+  T f = small ? T(0.5) : s / dmax(ang, T(0.5) * T(Eps<T>::v));
   return {small ? T(1) : c, w.x * f, w.y * f, w.z * f};
 }
 template <class T> __device__ __forceinline__ V3<T> quat_log(const Q<T>& q) {
   V3<T> v = v3(q.x, q.y, q.z);
   T n = dsqrt(dot(v, v));
   const bool small = n < T(Eps<T>::v);
-  T f = small ? T(2) : T(2) * datan2(n, q.w) / (small ? T(1) : n);
+  T f = small ? T(2) : T(2) * datan2(n, q.w) / dmax(n, T(0.5) * T(Eps<T>::v));
   return v * f;
 }
 // Rotation matrix of unit q (active), row-major.
@@ -404,7 +446,7 @@ template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_poin
       sp = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
     } else if constexpr (gt == G_CYLINDER) {
       T rl = dsqrt(n.x * n.x + n.y * n.y);
-      T f = rl > T(1e-6) ? T(M::gp[i][0]) / (rl > T(1e-6) ? rl : T(1)) : T(0);
+      T f = rl > T(1e-6) ? T(M::gp[i][0]) / dmax(rl, T(5e-7)) : T(0);
       sp = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
     } else {  // mesh AABB
       sp = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
@@ -465,7 +507,7 @@ template <class T> __device__ __forceinline__ void tangent_frame(V3<T> n, V3<T>&
   const V3<T> a = v3(ax ? T(0) : T(1), ax ? T(1) : T(0), T(0));
   const V3<T> c = cross(n, a);
   const T l = dsqrt(dot(c, c));
-  u = sel(l > T(0), c * (T(1) / (l > T(0) ? l : T(1))), c);
+  u = sel(l > T(0), c * (T(1) / dmax(l, T(1e-30))), c);
   w = cross(n, u);
 }
 
@@ -485,7 +527,7 @@ __device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_n
   T tw = -(b_w - a_ww * slot[2]) / a_ww;
   const T limit = T(M::mu) * fn;
   const T tn = dsqrt(tu * tu + tw * tw);
-  const T sc = tn > limit ? (tn > T(0) ? limit / (tn > T(0) ? tn : T(1)) : T(0)) : T(1);
+  const T sc = tn > limit ? (tn > T(0) ? limit / dmax(tn, T(1e-30)) : T(0)) : T(1);
   slot[0] = fn;
   slot[1] = tu * sc;
   slot[2] = tw * sc;
@@ -527,7 +569,7 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     V3<T> vt3 = vpt - nb * vn;
     T vt = dsqrt(dot(vt3, vt3));
     const bool slip = vt > T(1e-6);
-    T ivt = slip ? T(1) / (slip ? vt : T(1)) : T(0);
+    T ivt = slip ? T(1) / dmax(vt, T(5e-7)) : T(0);
     V3<T> td = vt3 * ivt;
     T coul = T(M::mu) * fn * dmin(T(1), vt * T(1e3));
     T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i>(sup, td) * vt);
@@ -653,7 +695,7 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
     const T tw = slot[3 * cp + 2] - dot(vpt, gp.tw[k]) * gp.cw[k];
     const T limit = T(M::mu) * fn;
     const T tn = dsqrt(tu * tu + tw * tw);
-    const T sc = tn > limit ? (tn > T(0) ? limit / (tn > T(0) ? tn : T(1)) : T(0)) : T(1);
+    const T sc = tn > limit ? (tn > T(0) ? limit / dmax(tn, T(1e-30)) : T(0)) : T(1);
     const bool in = gp.in[k];
     slot[3 * cp] = in ? fn : T(0);
     slot[3 * cp + 1] = in ? tu * sc : T(0);
@@ -732,7 +774,7 @@ __device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw,
             const V3<T> vt3 = vrel - nw * vn;
             const T vt = dsqrt(dot(vt3, vt3));
             const bool slip = vt > T(1e-6);
-            const V3<T> td = vt3 * (slip ? T(1) / (slip ? vt : T(1)) : T(0));
+            const V3<T> td = vt3 * (slip ? T(1) / dmax(vt, T(5e-7)) : T(0));
             T ft = dmin(T(M::mu) * fn * dmin(T(1), vt * T(1e3)), T(1.0 / dtc) * series(td) * vt);
             ft = slip ? ft : T(0);
             fw = nw * fn - td * ft;
@@ -1108,7 +1150,7 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
         if constexpr (mine0 || mine1) {
           T r = dsqrt(T(-2) * dlog(T(1) - u1));
           T sn, cs;
-          dsincos(T(6.283185307179586) * u2, &sn, &cs);
+          angle_sincos(T(6.283185307179586) * u2, &sn, &cs);
           if constexpr (mine0) ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
           if constexpr (mine1) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
         }

@@ -546,13 +546,29 @@ uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
   for (unsigned char c : s) { h ^= c; h *= 1099511628211ull; }
   return h;
 }
-const std::vector<std::string>& compile_options() {
-  static const std::vector<std::string> opts = {
+// Step, observation and policy kernels assume finite values
+// (-ffinite-math-only), which lets products with the model's constant zeros
+// fold away: about 45% fewer instructions. The one exception is the f64
+// impulse-mode step kernel, built with IEEE semantics: with the finite-values
+// assumption the f64 terrain + impulse ant computed wrong accelerations
+// (relative error 1e5, the same on every launch) at -O3 on gfx950, while the
+// identical source was right without it, right at -O1, right on the host
+// under the same flags and sanitizer-clean there. IEEE builds are not the
+// default for f64 because several other f64 kernels built that way gave
+// results that changed from launch to launch on identical inputs (finite-math
+// builds of the same sources are bit-reproducible and match the oracle).
+enum class Build { Finite, Ieee };
+const std::vector<std::string>& compile_options(Build b) {
+  static const std::vector<std::string> finite_opts = {
       "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffinite-math-only", "-fno-signed-zeros",
       // Packed FP32 (v_pk_*_f32) stays off in every kernel of this library.
       "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
       "-Rpass-analysis=kernel-resource-usage"};
-  return opts;
+  static const std::vector<std::string> ieee_opts = {
+      "--offload-arch=gfx950", "-O3", "-std=c++17", "-fno-signed-zeros",
+      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+      "-Rpass-analysis=kernel-resource-usage"};
+  return b == Build::Ieee ? ieee_opts : finite_opts;
 }
 std::string cache_dir() {
   if (const char* e = std::getenv("PHZ_KERNEL_CACHE")) return e;
@@ -576,9 +592,9 @@ struct CodeObject {
 std::mutex g_compile_mu;
 std::unordered_map<uint64_t, std::shared_ptr<CodeObject>> g_code_cache;
 
-std::shared_ptr<CodeObject> compile_source(const std::string& src, std::string& err) {
+std::shared_ptr<CodeObject> compile_source(const std::string& src, Build build, std::string& err) {
   std::string key_text = src;
-  for (const auto& o : compile_options()) key_text += "\n" + o;
+  for (const auto& o : compile_options(build)) key_text += "\n" + o;
   const uint64_t key = fnv1a(key_text);
   std::lock_guard<std::mutex> lk(g_compile_mu);
   auto it = g_code_cache.find(key);
@@ -603,7 +619,7 @@ std::shared_ptr<CodeObject> compile_source(const std::string& src, std::string& 
     return nullptr;
   }
   std::vector<const char*> opts;
-  for (const auto& o : compile_options()) opts.push_back(o.c_str());
+  for (const auto& o : compile_options(build)) opts.push_back(o.c_str());
   hiprtcResult rc = hiprtcCompileProgram(prog, (int)opts.size(), opts.data());
   size_t log_size = 0;
   hiprtcGetProgramLogSize(prog, &log_size);
@@ -1018,7 +1034,7 @@ struct phz_sim {
       std::ofstream out(dump);
       out << src;
     }
-    code = compile_source(src, e);
+    code = compile_source(src, f64 && feat.cmode == 1 ? Build::Ieee : Build::Finite, e);
     if (!code) { err = e; return false; }
     return true;
   }
@@ -1091,7 +1107,7 @@ struct phz_sim {
       const std::string src = policy_kernel ? gen_policy_source(pol, feat.npd, f64)
                                             : gen_obs_source(model, policy_on ? &pol : nullptr, f64);
       std::string e;
-      k.code = compile_source(src, e);
+      k.code = compile_source(src, Build::Finite, e);
       if (!k.code) { err = e; return false; }
       k.epoch = ctl_epoch;
     }
@@ -1925,6 +1941,11 @@ int phz_set_policy_std(phz_sim* s, const double* stdv, uint32_t n) {
   if (!s->policy_on) return s->fail("policy pass not enabled — call enable_policy first");
   if ((int)n != s->pol.n_out) return s->fail(fmt("policy has %d actions, got %u stds", s->pol.n_out, n));
   if (!stdv) return s->fail("null std");
+  // The reference uploads any value; a Gaussian needs std > 0, and the kernel's
+  // log-probability (log std, (a - mean) / std) must stay finite.
+  for (uint32_t k = 0; k < n; k++)
+    if (!(std::isfinite(stdv[k]) && (float)stdv[k] > 0.0f))
+      return s->fail(fmt("policy std %u must be finite and positive, got %g", k, stdv[k]));
   if (!s->has_device()) return s->fail("host-only sim has no device buffers");
   if (!set_device(s)) return 1;
   std::vector<float> f(stdv, stdv + n);

@@ -389,7 +389,7 @@ def from_workload(w, precision: str, nworld: Optional[int] = None, device: int =
     if w.contact is not None and w.impulse_sweeps > 0:
         sim.enable_contact_impulse(w.contact.ground_height, w.contact.friction, w.contact_gains(), None, w.heightfield)
         sim.contact_sweeps = w.impulse_sweeps
-    elif w.contact is not None and w.heightfield is not None:
+    elif w.contact is not None and (w.heightfield is not None or w.gains_omega > 0.0):
         sim.enable_contact_terrain(w.contact.ground_height, w.contact.friction, w.contact_gains(), None, w.heightfield)
     elif w.contact is not None:
         sim.enable_ground_contact(w.contact.ground_height, w.contact.stiffness, w.contact.damping, w.contact.friction)

@@ -39,7 +39,7 @@ import numpy as np
 
 from .model import (BALL, FIXED, FREE, PRISMATIC, REVOLUTE, Geometry, Heightfield, Joint, Model, ModelBuilder,
                     PdDof, SpatialInertia, SpatialTransform, model_from_tables, pack_geometries, pack_pd_dofs,
-                    rotation_axis_angle)
+                    rotation_axis_angle, uniform_frequency_gains)
 
 NOISE_NORMAL = 0
 NOISE_UNIFORM = 1
@@ -77,6 +77,7 @@ class Workload:
     _init: Optional[object] = None
     heightfield: Optional[Heightfield] = None  # terrain in place of the flat ground
     impulse_sweeps: int = 0                    # > 0: impulse-mode contact with this many sweeps
+    gains_omega: float = 0.0                   # > 0: per-body contact gains k = m w^2, d = 2 m w
 
     def initial_state(self, nworld: Optional[int] = None):
         """World-major f64 (q, v, ctrl, targets|None) for the first `nworld` worlds."""
@@ -87,10 +88,15 @@ class Workload:
     def geometry_table(self):
         if self.contact is None:
             return None, 0
+        if self.gains_omega > 0.0:
+            return pack_geometries(self.model, gains=self.contact_gains())
         return pack_geometries(self.model, self.contact.stiffness, self.contact.damping)
 
     def contact_gains(self):
-        """Per-body (stiffness, damping): the workload's ground gains on every body."""
+        """Per-body (stiffness, damping): uniform-frequency gains when the workload
+        names a frequency, else the workload's ground gains on every body."""
+        if self.gains_omega > 0.0:
+            return uniform_frequency_gains(self.model, self.gains_omega, 1.0)
         return [(self.contact.stiffness, self.contact.damping)] * self.model.nbodies
 
     def impulse_erp(self) -> float:
@@ -319,13 +325,47 @@ def config(index: int) -> Workload:
         w = config(3)
         return dataclasses.replace(w, index=6, name="ant_terrain_impulse", heightfield=rolling_terrain(),
                                    impulse_sweeps=16)
+    if index in MJCF_WORKLOADS:
+        name, nworld, precisions = MJCF_WORKLOADS[index]
+        m = mjcf_model(name)
+        lo = min(a.ctrl_range[0] for a in m.actuators)
+        hi = max(a.ctrl_range[1] for a in m.actuators)
+        return Workload(index, f"mjcf_{name}", m, nworld, 1000, precisions, contact=Contact(0.0, 0.0, 0.0, 1.0),
+                        noise=Noise(seed=0x3C0 + index, dist=NOISE_UNIFORM, a=lo, b=hi, dofs=list(range(m.nu()))),
+                        init_seed=100 + index, _init=_init_mjcf, gains_omega=50.0)
     raise ValueError(f"no workload {index}")
 
 
-# The reference's five benchmark configurations; EXTRA are contact-mode
-# workloads beyond them (heightfield terrain, impulse solve).
+# The reference's five benchmark configurations; EXTRA are workloads beyond
+# them: contact modes (heightfield terrain, impulse solve) and the reference's
+# own MJCF benchmark models.
 ALL = (1, 2, 3, 4, 5)
-EXTRA = (6,)
+EXTRA = (6, 7, 8, 9)
+
+
+# ── 7-9: the reference's MJCF benchmark models, driven by their actuators ───
+# name, worlds, precisions. Controls: uniform over the actuators' control range
+# every step (the files' ctrlrange, which the loader converts to radians under
+# angle="degree" as the reference does).
+MJCF_WORKLOADS = {7: ("ant", 131072, ("f32",)), 8: ("humanoid", 32768, ("f32", "f64")),
+                  9: ("shadow_hand", 16384, ("f32", "f64"))}
+
+
+def _init_mjcf(w: Workload, n: int):
+    """Hinges uniform over the middle 80% of their range, free roots slightly
+    tilted at their file placement, at rest."""
+    rng = np.random.default_rng(w.init_seed)
+    m = w.model
+    q = np.zeros((n, m.nq))
+    for i, b in enumerate(m.bodies):
+        j, o = b.joint, m.q_offsets[i]
+        if j.ndof() == 1 and j.limits is not None:
+            lo, hi = j.limits
+            r = hi - lo
+            q[:, o] = rng.uniform(lo + 0.1 * r, hi - 0.1 * r, size=n)
+        elif j.ndof() == 6:
+            q[:, o:o + 3] = rng.normal(size=(n, 3)) * 0.05
+    return q, np.zeros((n, m.nv)), np.zeros((n, m.nu())), None
 
 
 # ── 6: ant on rolling terrain, impulse-mode contact ─────────────────────────

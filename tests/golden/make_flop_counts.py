@@ -58,7 +58,8 @@ def count(w, warm):
         probe = [q.copy(), v.copy(), c.copy(), ext.copy(), cs.copy()]
         _, rows = orc.step_batch(*probe[:3], 1, targets=tg, rng=orc.rng_states(64), threads=8, want_contacts=True,
                                  ext_state=probe[3] if imp else None, cs_state=probe[4] if imp else None)
-        k = int(np.argmax((rows[:, :, 0] > 0).sum(axis=1) >= 2))
+        finite = np.isfinite(q).all(axis=1) & np.isfinite(v).all(axis=1)
+        k = int(np.argmax(((rows[:, :, 0] > 0).sum(axis=1) >= 2) & finite))
     tgk = None if tg is None else tg[k]
     rng = orc.rng_states(1)[0] if w.noise is not None else 1
     res = {}
@@ -80,6 +81,8 @@ def main():
         nq, nv = w.model.nq, w.model.nv
         reads_ctrl = w.noise is None and w.pd is None
         per_elem = 2 * nq + 2 * nv + (nv if reads_ctrl else 0) + (len(w.pd) if w.pd else 0)
+        if w.model.actuators and w.noise is not None and len(w.noise.dofs) < w.model.nu():
+            per_elem += w.model.nu()  # controls the stream does not rewrite are read
         if w.impulse_sweeps > 0:
             # Carried forces (6) and ground warm-start impulses (3 per contact
             # point: 8 for a box, 1 otherwise) of each body with a shape.

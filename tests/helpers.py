@@ -11,7 +11,7 @@ def oracle_for(workload, f32_uniform: bool = False) -> Oracle:
     w = workload
     contact = None
     if w.contact is not None:
-        g, _ = pack_geometries(w.model, w.contact.stiffness, w.contact.damping)
+        g, _ = w.geometry_table()
         contact = (g, w.contact.ground_height, w.contact.friction)
     noise = None
     if w.noise is not None:

@@ -126,6 +126,28 @@ def test_graph_replay_bit_identical(prec):
         assert np.array_equal(o[0], outs[0][0]) and np.array_equal(o[1], outs[0][1])
 
 
+@pytest.mark.parametrize("cfg,prec", CASES + [(6, "f32"), (6, "f64")])
+def test_repeat_launch_bit_identical(cfg, prec):
+    """The same inputs stepped again give the same bits, every world: a kernel
+    that picks up values left behind by an earlier launch fails this."""
+    w = W.config(cfg)
+    n = 4096
+    q, v, c, tg = w.initial_state(n)
+    sim = from_workload(w, prec, nworld=n)
+    outs = []
+    for _ in range(8):
+        sim.load_states(q, v, c)
+        if tg is not None:
+            sim.set_position_targets(tg)
+        sim.step()
+        qdd, ctrl = sim.readback_qdd(), sim.readback_controls()
+        bits = np.uint64 if qdd.dtype == np.float64 else np.uint32
+        outs.append((qdd.view(bits), ctrl.view(bits)))
+    for k, (qdd, ctrl) in enumerate(outs[1:], start=1):
+        bad = ~(np.all(qdd == outs[0][0], axis=1) & np.all(ctrl == outs[0][1], axis=1))
+        assert not bad.any(), f"cfg {cfg} {prec}: repeat {k} differs in {bad.sum()} worlds"
+
+
 def test_worlds_independent_and_nan_isolated():
     """A NaN injected into one world stays in that world (no cross-world state)."""
     w = W.config(3)
