@@ -247,6 +247,72 @@ int phz_time_control_kernel(phz_sim* sim, int which, uint32_t step, uint32_t rep
  * phz_kernel_info; [4] is the block size, [5] the worlds per workgroup. */
 int phz_control_kernel_info(phz_sim* sim, int which, int64_t* info);
 
+/* ── PPO update on the device: the reference's TrainPipeline
+ * (crates/phyz-gpu/src/cuda/train.rs:523-805; kernels
+ * crates/phyz-gpu/cuda/phyz_train.cu:95-362). Two three-layer tanh MLPs (an
+ * actor with a global log_std after b3, a critic with one output), flat
+ * parameters in tang's Mlp::to_flat order (W1 [n_h][n_in], b1, W2 [n_h][n_h],
+ * b2, W3 [n_out][n_h], b3), Adam with f64 master weights and moments. ── */
+typedef struct phz_train phz_train;
+
+/* NetDims (train.rs:53-100). */
+typedef struct { uint64_t n_in, n_h, n_out; } phz_net_dims;
+/* AdamCfg (train.rs:102-129); TrainPipeline::new's default is
+ * {3e-4, 0.9, 0.999, 1e-8, 0}. */
+typedef struct { double lr, beta1, beta2, epsilon, weight_decay; } phz_adam_cfg;
+/* KlMode (train.rs:150-156). */
+#define PHZ_KL_CUMULATIVE 0
+#define PHZ_KL_MINIBATCH 1
+/* PpoUpdateCfg (train.rs:131-148). target_kl = +inf never brakes. */
+typedef struct {
+  double clip, entropy_coef, vdelta;
+  uint64_t minibatch, epochs;
+  double target_kl, kl_scale;
+  int32_t kl_mode;
+} phz_ppo_cfg;
+/* UpdateStats (train.rs:158-172). */
+typedef struct {
+  double policy_loss, value_loss, kl;
+  uint64_t grad_steps;
+  int32_t stopped_early;
+} phz_update_stats;
+
+/* TrainPipeline::new (train.rs:570-626): same limits and messages (hidden
+ * width <= 256, output width <= 64, critic output 1). capacity: most samples
+ * per upload; max_b: largest minibatch. */
+int phz_train_create(phz_net_dims actor, phz_net_dims critic, uint64_t capacity, uint64_t max_b, int device_ordinal,
+                     phz_train** out);
+void phz_train_destroy(phz_train* t);
+/* The last error's message; with NULL, the last failed create's. */
+const char* phz_train_last_error(const phz_train* t);
+/* TrainPipeline::device_name (train.rs:628-631). */
+int phz_train_device_name(const phz_train* t, char* buf, uint64_t len);
+/* Parameter count of network 0 (actor, log_std included) or 1 (critic). */
+uint64_t phz_train_param_count(const phz_train* t, int net);
+/* Rows of a minibatch per workgroup tile (chosen at create from LDS size). */
+uint32_t phz_train_rows_per_tile(const phz_train* t);
+/* TrainPipeline::set_adam (train.rs:795-803): moments and step counters persist. */
+int phz_train_set_adam(phz_train* t, const phz_adam_cfg* actor, const phz_adam_cfg* critic);
+/* set_actor_params / set_critic_params (train.rs:633-643): f64 flat arrays;
+ * both the master copy and the f32 mirror are set. */
+int phz_train_set_actor_params(phz_train* t, const double* flat, uint64_t n);
+int phz_train_set_critic_params(phz_train* t, const double* flat, uint64_t n);
+/* actor_params / critic_params (train.rs:645-653): the f64 master weights. */
+int phz_train_actor_params(phz_train* t, double* out, uint64_t n);
+int phz_train_critic_params(phz_train* t, double* out, uint64_t n);
+/* upload_batch (train.rs:655-690) of one SampleBatch (train.rs:509-522), f32
+ * row-major columns with their lengths: obs_a [n][actor n_in], obs_c
+ * [n][critic n_in], act [n][actor n_out], logp_old, adv, ret [n]. */
+int phz_train_upload_batch(phz_train* t, uint64_t n_rows, const float* obs_a, uint64_t obs_a_len, const float* obs_c,
+                           uint64_t obs_c_len, const float* act, uint64_t act_len, const float* logp_old,
+                           uint64_t logp_old_len, const float* adv, uint64_t adv_len, const float* ret, uint64_t ret_len);
+/* update (train.rs:692-791): cfg->epochs passes, epoch e visiting the batch in
+ * order[e] (order_lens[e] entries, a permutation of 0..n_rows) in minibatches
+ * of cfg->minibatch. Stops after the first minibatch whose brake reading
+ * exceeds cfg->target_kl. All shuffles are validated before anything runs. */
+int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
+                     const phz_ppo_cfg* cfg, phz_update_stats* out);
+
 #ifdef __cplusplus
 }
 #endif

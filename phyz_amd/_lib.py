@@ -19,6 +19,30 @@ u64p = C.POINTER(C.c_uint64)
 i64p = C.POINTER(C.c_int64)
 SIM = C.c_void_p
 
+TRAIN = C.c_void_p
+
+
+class NetDims(C.Structure):
+    _fields_ = [("n_in", C.c_uint64), ("n_h", C.c_uint64), ("n_out", C.c_uint64)]
+
+
+class AdamCfg(C.Structure):
+    _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double), ("epsilon", C.c_double),
+                ("weight_decay", C.c_double)]
+
+
+class PpoCfg(C.Structure):
+    _fields_ = [("clip", C.c_double), ("entropy_coef", C.c_double), ("vdelta", C.c_double), ("minibatch", C.c_uint64),
+                ("epochs", C.c_uint64), ("target_kl", C.c_double), ("kl_scale", C.c_double), ("kl_mode", C.c_int32)]
+
+
+class UpdateStats(C.Structure):
+    _fields_ = [("policy_loss", C.c_double), ("value_loss", C.c_double), ("kl", C.c_double),
+                ("grad_steps", C.c_uint64), ("stopped_early", C.c_int32)]
+
+
+fp = C.POINTER(C.c_float)
+
 # name -> (restype, argtypes); every symbol declared in include/phyz_amd.h.
 SIGNATURES = {
     "phz_sim_create": (C.c_int, [dp, C.c_uint32, C.c_uint32, C.c_uint32, dp, C.c_double, C.c_uint32, C.c_int, C.c_int,
@@ -78,6 +102,21 @@ SIGNATURES = {
     "phz_time_rollout": (C.c_int, [SIM, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_uint32, dp]),
     "phz_time_control_kernel": (C.c_int, [SIM, C.c_int, C.c_uint32, C.c_uint32, dp]),
     "phz_control_kernel_info": (C.c_int, [SIM, C.c_int, i64p]),
+    "phz_train_create": (C.c_int, [NetDims, NetDims, C.c_uint64, C.c_uint64, C.c_int, C.POINTER(C.c_void_p)]),
+    "phz_train_destroy": (None, [TRAIN]),
+    "phz_train_last_error": (C.c_char_p, [TRAIN]),
+    "phz_train_device_name": (C.c_int, [TRAIN, C.c_char_p, C.c_uint64]),
+    "phz_train_param_count": (C.c_uint64, [TRAIN, C.c_int]),
+    "phz_train_rows_per_tile": (C.c_uint32, [TRAIN]),
+    "phz_train_set_adam": (C.c_int, [TRAIN, C.POINTER(AdamCfg), C.POINTER(AdamCfg)]),
+    "phz_train_set_actor_params": (C.c_int, [TRAIN, dp, C.c_uint64]),
+    "phz_train_set_critic_params": (C.c_int, [TRAIN, dp, C.c_uint64]),
+    "phz_train_actor_params": (C.c_int, [TRAIN, dp, C.c_uint64]),
+    "phz_train_critic_params": (C.c_int, [TRAIN, dp, C.c_uint64]),
+    "phz_train_upload_batch": (C.c_int, [TRAIN, C.c_uint64, fp, C.c_uint64, fp, C.c_uint64, fp, C.c_uint64, fp,
+                                         C.c_uint64, fp, C.c_uint64, fp, C.c_uint64]),
+    "phz_train_update": (C.c_int, [TRAIN, C.POINTER(u32p), u64p, C.c_uint64, C.POINTER(PpoCfg),
+                                   C.POINTER(UpdateStats)]),
 }
 
 

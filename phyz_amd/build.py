@@ -5,8 +5,9 @@
 1. Embed csrc/phz_device.h and csrc/phz_control.h as raw strings
    (csrc/phz_device_src.inc, csrc/phz_control_src.inc) so the library can hand
    them to hiprtc with each model's constants.
-2. Compile the host library (csrc/phz_host.cpp) and the ahead-of-time layout
-   kernels (csrc/phz_io.hip) for gfx950 and link them with hiprtc.
+2. Compile the host library (csrc/phz_host.cpp), the ahead-of-time layout
+   kernels (csrc/phz_io.hip) and the PPO update pass (csrc/phz_train.hip) for
+   gfx950 and link them with hiprtc.
 
 Packed FP32 instructions are disabled in every device compile.
 """
@@ -63,12 +64,15 @@ def build(verbose: bool = False) -> str:
     os.makedirs(bdir, exist_ok=True)
     io_obj = os.path.join(bdir, "phz_io.o")
     host_obj = os.path.join(bdir, "phz_host.o")
+    train_obj = os.path.join(bdir, "phz_train.o")
     _run([cc, "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", *NO_PACKED_FP32, "-c",
           os.path.join(CSRC, "phz_io.hip"), "-o", io_obj], verbose)
+    _run([cc, "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", *NO_PACKED_FP32, "-c",
+          os.path.join(CSRC, "phz_train.hip"), "-o", train_obj], verbose)
     _run([cc, "-x", "c++", "-O2", "-fPIC", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-c",
           os.path.join(CSRC, "phz_host.cpp"), "-o", host_obj], verbose)
     tmp = LIB + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", io_obj, host_obj, "-o", tmp,
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", io_obj, train_obj, host_obj, "-o", tmp,
           "-L/opt/rocm/lib", "-lhiprtc", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"], verbose)
     os.replace(tmp, LIB)
     return LIB
