@@ -27,6 +27,12 @@ mjcf (unless --no-mjcf): workloads 7-9, the reference's MJCF ant, humanoid and
 hand driven by their own actuators, f32, with the share of worlds that stay
 finite (the reference's explicit joint-limit law diverges on the lightest links).
 control_loop (unless --no-control): the ant driven by the on-device policy.
+ppo_update (unless --no-ppo; --ppo-only runs just this): the PPO update pass at
+the reference's timing shape (a million samples, actor 55-64-64-22, critic
+67-64-64-1, minibatch 4096, one epoch) with the batch resident: samples/s of
+whole updates, the tile kernel's roofline from hipEvents, and, with the CPU
+leg, the f64 CPU update on 128 minibatches plus the device's update of that
+sample against it.
 """
 from __future__ import annotations
 
@@ -253,10 +259,19 @@ def run_control_loop(prec: str, reps: int, with_cpu: bool):
     log(f"[bench] control loop: {out['world_steps_per_s']:.4g} world-steps/s, rollout {t_roll:.3f} ms "
         f"(physics alone {t_phys:.3f} ms), policy {t_pol:.4f} ms = {out['policy_roofline']['achieved']} TFLOP/s, "
         f"obs {t_obs:.4f} ms = {out['obs_roofline']['achieved']} GB/s")
-    # Parity: one control step of sampled worlds against the oracle, exact stream replay.
+    if with_cpu:
+        out["parity"], orc = control_parity(cl, sim, q, v)
+        out["cpu_baseline"] = control_cpu_baseline(cl, orc)
+    return out
+
+
+def control_parity(cl, sim, q, v):
+    """Part of the CPU-baseline leg: one control step of sampled worlds against
+    the oracle, exact stream replay."""
     from oracle import policy_ref as PR
     from oracle.oracle import Oracle
     from phyz_amd.model import pack_geometries, pack_pd_dofs
+    m, n = cl.base.model, cl.nworld
     sim.load_states(q, v)
     sim.seed_policy(cl.seed)
     sim.run_policy(0)
@@ -277,10 +292,7 @@ def run_control_loop(prec: str, reps: int, with_cpu: bool):
         err["act"] = max(err["act"], float(np.abs(out_h[0, k, :-1] - a).max()))
         err["logp"] = max(err["logp"], abs(float(out_h[0, k, -1]) - lp))
         err["targets"] = max(err["targets"], float(np.abs(tgt[k] - t).max()))
-    out["parity"] = {"worlds_checked": len(idx), **{k: float(f"{e:.3g}") for k, e in err.items()}}
-    if with_cpu:
-        out["cpu_baseline"] = control_cpu_baseline(cl, orc)
-    return out
+    return {"worlds_checked": len(idx), **{k: float(f"{e:.3g}") for k, e in err.items()}}, orc
 
 
 def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
@@ -304,6 +316,119 @@ def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
             "kind": "port", "sample": f"{nworld} worlds x {n_control} control steps x {cl.control_every} physics steps, "
                                       f"f64 oracle (Python observation/policy, C++ physics), {dt:.1f} s",
             "control_steps_per_s": round(nworld * n_control / dt, 1)}
+
+
+# The reference's PPO timing shape (crates/phyz-gpu/examples/cuda_train.rs:46-66):
+# a million samples, actor obs 55 -> 64 -> 64 -> 22, critic obs 67 -> 64 -> 64 -> 1,
+# minibatch 4096, one epoch (245 minibatches), no KL brake.
+PPO_SHAPE = {"samples": 1_000_000, "actor_in": 55, "critic_in": 67, "hidden": 64, "act": 22, "minibatch": 4096}
+# Its published times (docs/design/cuda-backend.md:291-299): one update on an
+# RTX PRO 6000 Blackwell, and tang's f64 CPU update.
+PPO_REFERENCE_S = {"device": 3.57, "device_hardware": "RTX PRO 6000 Blackwell", "tang_f64_cpu": 35.26}
+
+
+def ppo_flops(b, nets):
+    """Algorithmic FLOPs of one minibatch of b rows: per network the forward
+    (3 layers), the weight and bias gradients (same size) and the two hidden
+    backprops, 2 FLOPs per multiply-add."""
+    f = 0
+    for n_in, n_h, n_out in nets:
+        layers = n_in * n_h + n_h * n_h + n_h * n_out
+        f += 2 * b * (2 * layers + n_out * n_h + n_h * n_h)
+    return f
+
+
+def run_ppo_update(reps: int, with_cpu: bool):
+    """The PPO update pass (phyz_amd.train) at the reference's timing shape:
+    wall time per update with the batch resident, and the tile kernel's
+    hipEvent time for its roofline."""
+    from phyz_amd.train import AdamCfg, KlMode, NetDims, PpoUpdateCfg, SampleBatch, TrainPipeline
+    P = PPO_SHAPE
+    n, a_in, c_in, h, act, mb = P["samples"], P["actor_in"], P["critic_in"], P["hidden"], P["act"], P["minibatch"]
+    ad, cd = NetDims(a_in, h, act), NetDims(c_in, h, 1)
+    log(f"[bench] ppo update: {n} samples, actor {a_in}-{h}-{h}-{act}, critic {c_in}-{h}-{h}-1, minibatch {mb}")
+    rng = np.random.default_rng(0xC0FFEE)
+    f32 = lambda a: a.astype(np.float32)  # noqa: E731
+    batch = SampleBatch(f32(rng.normal(size=(n, a_in)) * 0.5), f32(rng.normal(size=(n, c_in)) * 0.5),
+                        f32(rng.normal(size=(n, act)) * 0.3), f32(-20.0 + rng.normal(size=n) * 0.4),
+                        f32(rng.normal(size=n)), f32(rng.normal(size=n) * 2.0))
+    a0 = rng.normal(size=ad.param_count() + act) * 0.1
+    c0 = rng.normal(size=cd.param_count()) * 0.1
+    cfg = PpoUpdateCfg(0.2, 0.003, 6.0, mb, 1, float("inf"), float(act), KlMode.MINIBATCH)
+    pipe = TrainPipeline(ad, cd, n, mb)
+    pipe.set_adam(AdamCfg(), AdamCfg())
+    pipe.set_actor_params(a0)
+    pipe.set_critic_params(c0)
+    t0 = time.perf_counter()
+    pipe.upload_batch(n, batch)
+    upload_s = time.perf_counter() - t0
+    orders = [rng.permutation(n).astype(np.uint32) for _ in range(reps + 2)]
+    pipe.update([orders[0]], cfg)  # warmup
+    wall = []
+    for r in range(reps):
+        t0 = time.perf_counter()
+        st = pipe.update([orders[1 + r]], cfg)
+        wall.append(time.perf_counter() - t0)
+    _, ms, nmb = pipe.time_update([orders[-1]], cfg)
+    med = float(np.median(wall))
+    nets = [(a_in, h, act), (c_in, h, 1)]
+    full, last = divmod(n, mb)
+    flops = full * ppo_flops(mb, nets) + (ppo_flops(last, nets) if last else 0)
+    tiles_ms = float(ms[0])
+    out = {
+        "value": round(n / med, 1), "unit": "samples/s", "dtype": "f32 (f64 Adam and gradient sums)",
+        "seconds_per_update": round(med, 6), "ms_per_minibatch": round(med * 1e3 / st.grad_steps, 5),
+        "minibatches": st.grad_steps, "upload_s": round(upload_s, 4),
+        "wall_s": {"median": round(med, 6), "min": round(min(wall), 6), "max": round(max(wall), 6), "reps": reps},
+        "config": {"workload": "ppo_update", **P, "epochs": 1, "tile_rows": pipe.rows_per_tile},
+        "kernel_ms_per_launch": {"ppo_tiles": round(ms[0] / nmb, 5), "ppo_adam": round(ms[1] / nmb, 5)},
+        "roofline": {"bound": "valu", "kernel": "ppo_tiles",
+                     "achieved": round(flops / (tiles_ms / 1e3) / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(flops / (tiles_ms / 1e3) / 1e12 / 157.3, 4), "flops_per_update": flops,
+                     "launch_ms": round(tiles_ms / nmb, 5), "traffic": None},
+        "reference_published": {**PPO_REFERENCE_S, "speedup_vs_published_device": round(PPO_REFERENCE_S["device"] / med, 1)},
+    }
+    log(f"[bench] ppo update: {med * 1e3:.3f} ms per update ({out['ms_per_minibatch'] * 1e3:.1f} us per minibatch), "
+        f"tiles {out['kernel_ms_per_launch']['ppo_tiles'] * 1e3:.1f} us / adam+brake "
+        f"{out['kernel_ms_per_launch']['ppo_adam'] * 1e3:.1f} us per launch; "
+        f"{out['roofline']['achieved']} TFLOP/s in the tile kernel")
+    if with_cpu:
+        out["cpu_baseline"], out["parity"] = ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg)
+    return out
+
+
+def ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg, n_mb: int = 128):
+    """The f64 CPU update (the oracle's restatement of tang's) on the first
+    n_mb minibatches of the same batch, one BLAS thread, as samples/s; and
+    the device's update of that sample against it (per-parameter weight-delta
+    gaps over the largest delta)."""
+    from threadpoolctl import threadpool_limits
+    from oracle.ppo_ref import CpuPpo, Dims
+    from phyz_amd.train import SampleBatch, TrainPipeline
+    rows = n_mb * cfg.minibatch
+    cols = {k: getattr(batch, k)[:rows] for k in ("obs_a", "obs_c", "act", "logp_old", "adv", "ret")}
+    order = [np.random.default_rng(7).permutation(rows).astype(np.uint32)]
+    cpu = CpuPpo(Dims(ad.n_in, ad.n_h, ad.n_out), Dims(cd.n_in, cd.n_h, 1), a0, c0)
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        cpu.update({k: v.astype(np.float64) for k, v in cols.items()}, order, cfg.clip, cfg.entropy_coef, cfg.vdelta,
+                   cfg.minibatch, 1, cfg.target_kl, cfg.kl_scale, int(cfg.kl_mode))
+        dt = time.perf_counter() - t0
+    pipe = TrainPipeline(ad, cd, rows, cfg.minibatch)
+    pipe.set_actor_params(a0)
+    pipe.set_critic_params(c0)
+    pipe.upload_batch(rows, SampleBatch(**cols))
+    pipe.update(order, cfg)
+    gaps = {}
+    for net, x0, xc, xd in (("actor", a0, cpu.actor, pipe.actor_params()), ("critic", c0, cpu.critic, pipe.critic_params())):
+        e = np.abs((xd - x0) - (xc - x0)) / np.abs(xc - x0).max()
+        gaps[net] = {"median": float(f"{np.median(e):.3g}"), "p99": float(f"{np.percentile(e, 99):.3g}"),
+                     "max": float(f"{e.max():.3g}")}
+    base = {"value": round(rows / dt, 1), "unit": "samples/s", "cores": 1, "kind": "port",
+            "sample": f"{n_mb} minibatches x {cfg.minibatch} rows, f64 numpy update (tang's arithmetic), "
+                      f"one BLAS thread ({dt:.2f} s)",
+            "seconds_per_update_extrapolated": round(dt * PPO_SHAPE["samples"] / rows, 2)}
+    return base, {"rows": rows, "weight_delta_gap": gaps}
 
 
 def config_of(w, r):
@@ -377,6 +502,8 @@ def main():
     ap.add_argument("--no-mjcf", action="store_true",
                     help="skip the MJCF-model measurements (workloads 7-9)")
     ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
+    ap.add_argument("--no-ppo", action="store_true", help="skip the PPO update pass measurement")
+    ap.add_argument("--ppo-only", action="store_true", help="measure only the PPO update pass")
     ap.add_argument("--precision", choices=["f32", "f64"], default=None, help="run one precision only")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (HBM counter calibration)")
@@ -398,6 +525,9 @@ def main():
 
     if args.control_only:
         print(json.dumps(run_control_loop("f32", args.reps, not args.no_cpu)), flush=True)
+        return
+    if args.ppo_only:
+        print(json.dumps(run_ppo_update(args.reps, not args.no_cpu)), flush=True)
         return
 
     from phyz_amd import workloads as W
@@ -458,6 +588,8 @@ def main():
                                      "parity": rm["parity"].get("f32")}
     if not args.no_control:
         line["control_loop"] = run_control_loop("f32", min(args.reps, 5), not args.no_cpu)
+    if not args.no_ppo:
+        line["ppo_update"] = run_ppo_update(min(args.reps, 5), not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -312,6 +312,13 @@ int phz_train_upload_batch(phz_train* t, uint64_t n_rows, const float* obs_a, ui
  * exceeds cfg->target_kl. All shuffles are validated before anything runs. */
 int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
                      const phz_ppo_cfg* cfg, phz_update_stats* out);
+/* Measurement: phz_train_update with hipEvents around every launch on the
+ * pipeline's stream; ms_kernels[2] receives the summed times of the tile
+ * kernel and of the Adam kernel (which also applies the KL brake),
+ * *minibatches the minibatches launched. Waits for each minibatch, so its
+ * wall time is not the update's. */
+int phz_train_time_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
+                          const phz_ppo_cfg* cfg, phz_update_stats* out, double* ms_kernels, uint64_t* minibatches);
 
 #ifdef __cplusplus
 }

@@ -117,6 +117,8 @@ SIGNATURES = {
                                          C.c_uint64, fp, C.c_uint64, fp, C.c_uint64]),
     "phz_train_update": (C.c_int, [TRAIN, C.POINTER(u32p), u64p, C.c_uint64, C.POINTER(PpoCfg),
                                    C.POINTER(UpdateStats)]),
+    "phz_train_time_update": (C.c_int, [TRAIN, C.POINTER(u32p), u64p, C.c_uint64, C.POINTER(PpoCfg),
+                                        C.POINTER(UpdateStats), dp, u64p]),
 }
 
 

@@ -16,24 +16,26 @@
 //              run out of LDS. Each workgroup writes its tile's partial weight
 //              and bias gradients in f64 (part[tile][param]) and its partial
 //              statistics (stats_part[tile][4]).
+//              Each layer's weights are staged through LDS when they fit.
 //   ppo_adam   one thread per parameter of both networks: the tile partials
-//              summed in tile order in f64, rounded to f32 (the gradient the
-//              reference hands Adam is f32), then Adam in f64. Writes the f64
-//              master, the row-major f32 mirror (backward) and a transposed
-//              f32 mirror of each weight matrix (forward: lanes over output
-//              neurons read consecutive words).
-//   ppo_brake  one thread: the minibatch's statistics into the update's
-//              running sums, and the KL brake. When it trips, it sets a flag
-//              that every later launch of the update checks first, so the
-//              loop stops after that minibatch exactly as the reference's
-//              host loop does, without the reference's per-minibatch readback.
-// Every sum has a fixed order (rows within a tile, then tiles ascending), so
-// an update is bit-reproducible run to run.
+//              summed in a fixed order in f64, rounded to f32 (the gradient
+//              the reference hands Adam is f32), then Adam in f64. Writes the
+//              f64 master, the row-major f32 mirror (backward) and a
+//              transposed f32 mirror of each weight matrix (forward: lanes
+//              over output neurons read consecutive words). Its first wave
+//              also folds the minibatch's statistics into the update's
+//              running sums and applies the KL brake: when it trips, it sets
+//              the next minibatch's stop flag, which every later launch of the
+//              update checks first. The loop thus stops after that minibatch,
+//              as the reference's host loop does, without the reference's
+//              per-minibatch readback.
+// Every sum has a fixed order, so an update is bit-reproducible run to run.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -44,8 +46,10 @@
 
 namespace {
 
-constexpr int kThreads = 256;   // threads per workgroup of every training launch
-constexpr int kRowBlock = 8;    // rows a thread carries through one dense-layer item
+constexpr int kTileThreads = 512;  // 8 waves per tile workgroup (2 per SIMD)
+constexpr int kAdamThreads = 64;   // one wave per Adam workgroup: spread over every CU
+constexpr int kAdamLanes = 4;      // lanes that share one parameter's sum over the tiles
+constexpr int kRowBlock = 4;       // rows a thread carries through one dense-layer item
 constexpr uint32_t kMaxHidden = 256;  // TRAIN_MAX_H (train.rs:46)
 constexpr uint32_t kMaxOut = 64;      // TRAIN_MAX_OUT (train.rs:50)
 
@@ -63,26 +67,56 @@ struct Dims {
   __host__ __device__ uint32_t tW2() const { return n_h * n_in; }
   __host__ __device__ uint32_t tW3() const { return tW2() + n_h * n_h; }
   __host__ __device__ uint32_t t_size() const { return tW3() + n_h * n_out; }
+  // Largest weight matrix, in floats.
+  __host__ __device__ uint32_t max_matrix() const {
+    const uint32_t a = n_in * n_h, b = n_h * n_h, c = n_h * n_out;
+    return a > b ? (a > c ? a : c) : (b > c ? b : c);
+  }
 };
 
-// LDS of one tile workgroup, in floats: X [R][n_in], H1 [R][n_h], H2 [R][n_h],
-// DA [R][n_h], DB [R][n_h], OUT [R][n_out] (the output, then dL/dout),
-// DLS [R][n_out] (per-row dL/dlog_std), RS [R][4] (per-row statistics),
-// SD [n_out], LSD [n_out].
+__host__ __device__ inline uint32_t pad4(uint32_t x) { return (x + 3u) & ~3u; }
+
+// How a tile workgroup reads the weights: all five matrices staged into LDS
+// at the start (one load phase), one layer at a time through a staging buffer,
+// or straight from the mirrors in HBM (networks too wide for the LDS).
+enum { STAGE_ALL = 0, STAGE_LAYER = 1, STAGE_NONE = 2 };
+
+// LDS of one tile workgroup, in floats; rows padded to whole float4s:
+// X [R][lx], H1, H2, DA, DB [R][lh], OUT [R][lo] (the output, then dL/dout),
+// ACT [R][lo] (the rows' actions), DLS [R][lo] (per-row dL/dlog_std), RV
+// [R][4] (per-row advantage, old log-prob, return), RS [R][4] (per-row
+// statistics), SD and LSD [lo] (std and log std), then the weights:
+// STAGE_ALL  W1t [n_in][n_h], W2t [n_h][n_h], W3t [n_h][n_out], W3 [n_out][n_h],
+//            W2 [n_h][n_h] at WB + w_*;
+// STAGE_LAYER one [K][N] matrix at a time at WB (max_matrix floats).
 struct Lds {
-  uint32_t X, H1, H2, DA, DB, OUT, DLS, RS, SD, LSD, total;
-  __host__ __device__ Lds(const Dims& d, uint32_t R) {
+  uint32_t lx, lh, lo;
+  uint32_t X, H1, H2, DA, DB, OUT, ACT, DLS, RV, RS, SD, LSD, WB, total;
+  uint32_t w_1t, w_2t, w_3t, w_3, w_2;
+  __host__ __device__ Lds(const Dims& d, uint32_t R, int mode) {
+    lx = pad4(d.n_in);
+    lh = pad4(d.n_h);
+    lo = pad4(d.n_out);
     X = 0;
-    H1 = X + R * d.n_in;
-    H2 = H1 + R * d.n_h;
-    DA = H2 + R * d.n_h;
-    DB = DA + R * d.n_h;
-    OUT = DB + R * d.n_h;
-    DLS = OUT + R * d.n_out;
-    RS = DLS + R * d.n_out;
+    H1 = X + R * lx;
+    H2 = H1 + R * lh;
+    DA = H2 + R * lh;
+    DB = DA + R * lh;
+    OUT = DB + R * lh;
+    ACT = OUT + R * lo;
+    DLS = ACT + R * lo;
+    RV = DLS + R * lo;
+    RS = RV + R * 4;
     SD = RS + R * 4;
-    LSD = SD + d.n_out;
-    total = LSD + d.n_out;
+    LSD = SD + lo;
+    WB = LSD + lo;
+    w_1t = 0;
+    w_2t = pad4(w_1t + d.n_in * d.n_h);
+    w_3t = pad4(w_2t + d.n_h * d.n_h);
+    w_3 = pad4(w_3t + d.n_h * d.n_out);
+    w_2 = pad4(w_3 + d.n_out * d.n_h);
+    const uint32_t all = pad4(w_2 + d.n_h * d.n_h);
+    total = WB + (mode == STAGE_ALL ? all : mode == STAGE_LAYER ? pad4(d.max_matrix()) : 0u);
   }
 };
 
@@ -102,215 +136,376 @@ struct TileArgs {
   const float* ret;       // [n_rows]
   float clip, entropy_coef, vdelta;
   double* stats_part;     // [tile][4]
-  const int* stopped;     // the update's KL-brake flag
+  const int* skip;        // nonzero: the KL brake stopped the update before this minibatch
 };
 
-// tanh rounded once to f32 from an f64 evaluation. Near saturation the
-// backward pass uses 1 - h^2, whose relative error is the activation's error
-// over (1 - |h|): a few-ulp f32 tanh there visibly perturbs the gradients of
-// the layer above, which a correctly rounded activation does not.
-__device__ inline float act_tanh(float x) { return (float)tanh((double)x); }
-
-// Y[r][j] = act(b[j] + sum_i Wt[i][j] X[r][i]) for rows r < R, neurons j < N.
-// Lanes run over neurons (coalesced Wt reads, LDS broadcasts of X); each item
-// carries kRowBlock rows. The sum starts from the bias and adds inputs in
-// order, as the reference's per-row loop does (phyz_train.cu:115-132).
-template <bool TANH>
-__device__ void dense_forward(const float* __restrict__ X, uint32_t K, const float* __restrict__ Wt,
-                              const float* __restrict__ bias, uint32_t N, float* __restrict__ Y, uint32_t R) {
-  const uint32_t NP = (N + 63u) & ~63u;
-  const uint32_t items = (R / kRowBlock) * NP;
-  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
-    const uint32_t j = it % NP, r0 = (it / NP) * kRowBlock;
-    if (j >= N) continue;
-    float acc[kRowBlock];
-    const float bj = bias[j];
-#pragma unroll
-    for (int rr = 0; rr < kRowBlock; rr++) acc[rr] = bj;
-    for (uint32_t i = 0; i < K; i++) {
-      const float wij = Wt[i * N + j];
-#pragma unroll
-      for (int rr = 0; rr < kRowBlock; rr++) acc[rr] += wij * X[(r0 + rr) * K + i];
-    }
-#pragma unroll
-    for (int rr = 0; rr < kRowBlock; rr++) Y[(r0 + rr) * N + j] = TANH ? act_tanh(acc[rr]) : acc[rr];
-  }
+// tanh(x) = sign(x) t / (t + 2) with t = expm1(2|x|): within 3 ulp and
+// correctly rounded for 86% of f32 inputs (glibc's tanhf, 65%), and tight
+// near saturation, where the backward pass's 1 - h^2 magnifies an
+// activation's error by 1 / (1 - |h|). Past |x| = 9 tanh rounds to +-1 in f32.
+__device__ inline float act_tanh(float x) {
+  const float ax = fabsf(x);
+  const float t = expm1f(2.0f * (ax < 9.0f ? ax : 9.0f));
+  const float h = ax < 9.0f ? t / (t + 2.0f) : 1.0f;
+  return x != x ? x : copysignf(h, x);
 }
 
-// dH[r][j] = (sum_k D[r][k] W[k][j]) (1 - H[r][j]^2), W row-major [K][N]
-// (phyz_train.cu:212-222).
-__device__ void dense_backward_hidden(const float* __restrict__ D, uint32_t K, const float* __restrict__ W,
-                                      const float* __restrict__ H, uint32_t N, float* __restrict__ DH, uint32_t R) {
+// n / d for n * d < 2^32 by one multiply-high (m = ceil(2^32 / d)).
+struct FastDiv {
+  uint64_t m;
+  uint32_t d;
+  __device__ explicit FastDiv(uint32_t d_) : m(((1ull << 32) + d_ - 1) / d_), d(d_) {}
+  __device__ uint32_t div(uint32_t n) const { return (uint32_t)(((uint64_t)n * m) >> 32); }
+};
+
+enum { EPI_TANH = 0, EPI_LINEAR = 1, EPI_DTANH = 2 };
+
+// Y[r][j] for rows r < R, columns j < N of
+//   EPI_TANH    tanh(b[j] + sum_k X[r][k] Wkn[k][j])
+//   EPI_LINEAR  b[j] + sum_k X[r][k] Wkn[k][j]
+//   EPI_DTANH   (sum_k X[r][k] Wkn[k][j]) (1 - H[r][j]^2)
+// Wkn is [K][N] row-major: the transposed mirror for a forward layer, the
+// row-major weights for a backprop. Lanes run over j (conflict-free Wkn reads,
+// broadcast float4 reads of X); each item carries kRowBlock rows. The sum
+// adds k in order, from the bias in the forward pass, as the reference's
+// per-row loops do (phyz_train.cu:115-132, 212-222).
+template <int EPI>
+__device__ void dense(const float* __restrict__ X, uint32_t ldx, uint32_t K, const float* __restrict__ Wkn,
+                      uint32_t N, const float* __restrict__ bias, const float* __restrict__ H, uint32_t ldh,
+                      float* __restrict__ Y, uint32_t ldy, uint32_t R) {
   const uint32_t NP = (N + 63u) & ~63u;
   const uint32_t items = (R / kRowBlock) * NP;
-  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
-    const uint32_t j = it % NP, r0 = (it / NP) * kRowBlock;
+  const FastDiv byNP(NP);
+  for (uint32_t it = threadIdx.x; it < items; it += kTileThreads) {
+    const uint32_t q = byNP.div(it), j = it - q * NP, r0 = q * kRowBlock;
     if (j >= N) continue;
     float acc[kRowBlock];
+    const float init = EPI == EPI_DTANH ? 0.0f : bias[j];
 #pragma unroll
-    for (int rr = 0; rr < kRowBlock; rr++) acc[rr] = 0.0f;
-    for (uint32_t k = 0; k < K; k++) {
-      const float wkj = W[k * N + j];
+    for (int rr = 0; rr < kRowBlock; rr++) acc[rr] = init;
+    uint32_t k = 0;
+    for (; k + 4 <= K; k += 4) {
+      const float w0 = Wkn[(k + 0) * N + j], w1 = Wkn[(k + 1) * N + j];
+      const float w2 = Wkn[(k + 2) * N + j], w3 = Wkn[(k + 3) * N + j];
 #pragma unroll
-      for (int rr = 0; rr < kRowBlock; rr++) acc[rr] += D[(r0 + rr) * K + k] * wkj;
+      for (int rr = 0; rr < kRowBlock; rr++) {
+        const float4 x = *reinterpret_cast<const float4*>(X + (r0 + rr) * ldx + k);
+        acc[rr] += w0 * x.x;
+        acc[rr] += w1 * x.y;
+        acc[rr] += w2 * x.z;
+        acc[rr] += w3 * x.w;
+      }
+    }
+    for (; k < K; k++) {
+      const float wk = Wkn[k * N + j];
+#pragma unroll
+      for (int rr = 0; rr < kRowBlock; rr++) acc[rr] += wk * X[(r0 + rr) * ldx + k];
     }
 #pragma unroll
     for (int rr = 0; rr < kRowBlock; rr++) {
-      const float a = H[(r0 + rr) * N + j];
-      DH[(r0 + rr) * N + j] = acc[rr] * (1.0f - a * a);
+      float y = acc[rr];
+      if (EPI == EPI_TANH) y = act_tanh(y);
+      if (EPI == EPI_DTANH) {
+        const float h = H[(r0 + rr) * ldh + j];
+        y = y * (1.0f - h * h);
+      }
+      Y[(r0 + rr) * ldy + j] = y;
     }
   }
 }
 
 // Tile partials of a linear layer's gradients: Gw[o][i] = sum_r D[r][o] X[r][i]
-// and Gb[o] = sum_r D[r][o] over the tile's valid rows, in f64 (the
-// reference's row loops accumulate in double, phyz_train.cu:226-260).
-__device__ void dense_grad(const float* __restrict__ D, uint32_t O, const float* __restrict__ X, uint32_t I,
-                           uint32_t rows, double* __restrict__ Gw, double* __restrict__ Gb) {
-  for (uint32_t it = threadIdx.x; it < O * I; it += kThreads) {
-    const uint32_t o = it / I, i = it % I;
-    double acc = 0.0;
-    for (uint32_t r = 0; r < rows; r++) acc += (double)D[r * O + o] * (double)X[r * I + i];
-    Gw[it] = acc;
+// and Gb[o] = sum_r D[r][o] over the tile's valid rows, each in f64 and in row
+// order (the reference's row loops accumulate in double, phyz_train.cu:226-260).
+// An item is a 2 x 4 block (two outputs by four inputs): per row, two D values
+// and one float4 of X feed eight sums; the items of the first input quad also
+// carry their outputs' bias sums. Rows of X are padded to whole float4s; sums
+// that fall in the padding are not stored.
+__device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O, const float* __restrict__ X,
+                           uint32_t ldx, uint32_t I, uint32_t rows, double* __restrict__ Gw, double* __restrict__ Gb) {
+  const uint32_t OP = (O + 1u) / 2u, IQ = (I + 3u) / 4u;
+  const FastDiv byIQ(IQ);
+  for (uint32_t it = threadIdx.x; it < OP * IQ; it += kTileThreads) {
+    const uint32_t op = byIQ.div(it), o0 = op * 2u, i0 = (it - op * IQ) * 4u;
+    const uint32_t o1 = o0 + 1u < O ? o0 + 1u : o0;  // an odd last output pairs with itself
+    double acc[2][4] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+    double bias[2] = {0.0, 0.0};
+#pragma unroll 4
+    for (uint32_t r = 0; r < rows; r++) {
+      const double dv[2] = {(double)D[r * ldd + o0], (double)D[r * ldd + o1]};
+      const float4 xq = *reinterpret_cast<const float4*>(X + r * ldx + i0);
+      const double xv[4] = {(double)xq.x, (double)xq.y, (double)xq.z, (double)xq.w};
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        bias[u] += dv[u];
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[u][v] += dv[u] * xv[v];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const uint32_t o = u == 0 ? o0 : o0 + 1u;
+      if (o >= O) break;
+      double* g = Gw + (size_t)o * I + i0;
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        if (i0 + v < I) g[v] = acc[u][v];
+      if (i0 == 0) Gb[o] = bias[u];
+    }
   }
-  for (uint32_t o = threadIdx.x; o < O; o += kThreads) {
-    double acc = 0.0;
-    for (uint32_t r = 0; r < rows; r++) acc += (double)D[r * O + o];
-    Gb[o] = acc;
+}
+
+// count floats from global memory into LDS, eight loads in flight per thread
+// (each from a clamped, in-bounds address) before any of them is stored.
+__device__ void copy_batched(float* __restrict__ dst, const float* __restrict__ src, uint32_t count) {
+  constexpr uint32_t U = 8;
+  for (uint32_t base = threadIdx.x; base < count; base += U * kTileThreads) {
+    float v[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t e = base + u * kTileThreads;
+      v[u] = src[e < count ? e : count - 1u];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t e = base + u * kTileThreads;
+      if (e < count) dst[e] = v[u];
+    }
   }
+}
+
+// One layer's [K][N] weights into the LDS staging buffer.
+__device__ void stage(float* __restrict__ WB, const float* __restrict__ src, uint32_t count) {
+  copy_batched(WB, src, count);
 }
 
 __device__ inline float clampf(float x, float lo, float hi) { return x < lo ? lo : (x > hi ? hi : x); }
 
-__global__ void __launch_bounds__(kThreads) ppo_tiles(TileArgs a) {
-  if (*a.stopped) return;
-  extern __shared__ float lds[];
+// One workgroup per (tile of R minibatch rows, network); MODE as above.
+template <int MODE>
+__global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
+  if (*a.skip) return;
+  extern __shared__ __align__(16) float lds[];
   const int net = blockIdx.y;
   const Dims d = a.dims[net];
   const uint32_t R = a.R;
   const uint32_t row0 = blockIdx.x * R;
   const uint32_t rows = row0 >= a.b ? 0u : std::min(R, a.b - row0);
-  const Lds L(d, R);
+  const Lds L(d, R, MODE);
   float* X = lds + L.X;
   float* H1 = lds + L.H1;
   float* H2 = lds + L.H2;
   float* DA = lds + L.DA;
   float* DB = lds + L.DB;
   float* OUT = lds + L.OUT;
+  float* ACT = lds + L.ACT;
   float* DLS = lds + L.DLS;
+  float* RV = lds + L.RV;
   float* RS = lds + L.RS;
   float* SD = lds + L.SD;
   float* LSD = lds + L.LSD;
+  float* WB = lds + L.WB;
   const float* w = a.w[net];
   const float* wt = a.wt[net];
   double* part = a.part[net] + (size_t)blockIdx.x * a.n_param[net];
   const float* x = a.x[net];
+  // Each matrix's source: its LDS copy (STAGE_ALL), the staging buffer
+  // (STAGE_LAYER, loaded just before use) or the mirror in HBM.
+  auto src = [&](uint32_t lds_off, const float* global) -> const float* {
+    return MODE == STAGE_ALL ? WB + lds_off : MODE == STAGE_LAYER ? WB : global;
+  };
+  auto stage_layer = [&](const float* global, uint32_t count) {
+    if (MODE == STAGE_LAYER) {
+      __syncthreads();
+      stage(WB, global, count);
+      __syncthreads();
+    }
+  };
 
-  // ── gather the tile's rows (the minibatch is an index list into the batch) ──
-  for (uint32_t e = threadIdx.x; e < R * d.n_in; e += kThreads) {
-    const uint32_t r = e / d.n_in, i = e % d.n_in;
-    X[e] = r < rows ? x[(size_t)a.idx[row0 + r] * d.n_in + i] : 0.0f;
-  }
+  // ── gather the tile's rows (the minibatch is an index list into the batch),
+  //    the rows' actions and scalars, and the weights: the row indices first,
+  //    then each copy with several loads in flight per thread ──
+  uint32_t* IDX = reinterpret_cast<uint32_t*>(RS);  // RS is free until the loss pass
+  for (uint32_t r = threadIdx.x; r < R; r += kTileThreads) IDX[r] = r < rows ? a.idx[row0 + r] : 0u;
   if (net == 0) {
-    for (uint32_t k = threadIdx.x; k < d.n_out; k += kThreads) {
-      const float s = expf(w[d.mlp_params() + k]);
-      SD[k] = s;
-      LSD[k] = logf(s);
+    for (uint32_t k = threadIdx.x; k < d.n_out; k += kTileThreads) {
+      const float sd = expf(w[d.mlp_params() + k]);
+      SD[k] = sd;
+      LSD[k] = logf(sd);
     }
   }
   __syncthreads();
+  // Rows: one wave per row, lanes over columns, four rows' loads in flight.
+  const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
+  constexpr uint32_t kWaves = kTileThreads / 64u;
+  for (uint32_t c0 = 0; c0 < L.lx; c0 += 64u) {
+    const uint32_t i = c0 + lane, ic = i < d.n_in ? i : d.n_in - 1u;
+    for (uint32_t r0 = wave; r0 < R; r0 += 4u * kWaves) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t r = r0 + q * kWaves;
+        v[q] = r < R ? x[(size_t)IDX[r < R ? r : 0u] * d.n_in + ic] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t r = r0 + q * kWaves;
+        if (r < R && i < L.lx) X[r * L.lx + i] = (r < rows && i < d.n_in) ? v[q] : 0.0f;
+      }
+    }
+  }
+  if (net == 0) {
+    for (uint32_t r0 = wave; r0 < R; r0 += 4u * kWaves) {
+      const uint32_t kc = lane < d.n_out ? lane : d.n_out - 1u;
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t r = r0 + q * kWaves;
+        v[q] = r < R ? a.act[(size_t)IDX[r < R ? r : 0u] * d.n_out + kc] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t r = r0 + q * kWaves;
+        if (r < R && lane < L.lo) ACT[r * L.lo + lane] = (r < rows && lane < d.n_out) ? v[q] : 0.0f;
+      }
+    }
+  }
+  for (uint32_t r = threadIdx.x; r < rows; r += kTileThreads) {
+    const uint32_t sidx = IDX[r];
+    if (net == 0) {
+      RV[r * 4 + 0] = a.adv[sidx];
+      RV[r * 4 + 1] = a.logp_old[sidx];
+    } else {
+      RV[r * 4 + 2] = a.ret[sidx];
+    }
+  }
+  if (MODE == STAGE_ALL) {
+    copy_batched(WB + L.w_1t, wt, d.n_in * d.n_h);
+    copy_batched(WB + L.w_2t, wt + d.tW2(), d.n_h * d.n_h);
+    copy_batched(WB + L.w_3t, wt + d.tW3(), d.n_h * d.n_out);
+    copy_batched(WB + L.w_3, w + d.oW3(), d.n_out * d.n_h);
+    copy_batched(WB + L.w_2, w + d.oW2(), d.n_h * d.n_h);
+  }
+  if (MODE == STAGE_LAYER) stage(WB, wt, d.n_in * d.n_h);
+  __syncthreads();
 
   // ── forward (phyz_train.cu:101-133) ──
-  dense_forward<true>(X, d.n_in, wt, w + d.ob1(), d.n_h, H1, R);
-  __syncthreads();
-  dense_forward<true>(H1, d.n_h, wt + d.tW2(), w + d.ob2(), d.n_h, H2, R);
-  __syncthreads();
-  dense_forward<false>(H2, d.n_h, wt + d.tW3(), w + d.ob3(), d.n_out, OUT, R);
+  dense<EPI_TANH>(X, L.lx, d.n_in, src(L.w_1t, wt), d.n_h, w + d.ob1(), nullptr, 0, H1, L.lh, R);
+  stage_layer(wt + d.tW2(), d.n_h * d.n_h);
+  if (MODE != STAGE_LAYER) __syncthreads();
+  dense<EPI_TANH>(H1, L.lh, d.n_h, src(L.w_2t, wt + d.tW2()), d.n_h, w + d.ob2(), nullptr, 0, H2, L.lh, R);
+  stage_layer(wt + d.tW3(), d.n_h * d.n_out);
+  if (MODE != STAGE_LAYER) __syncthreads();
+  dense<EPI_LINEAR>(H2, L.lh, d.n_h, src(L.w_3t, wt + d.tW3()), d.n_out, w + d.ob3(), nullptr, 0, OUT, L.lo, R);
   __syncthreads();
 
-  // ── loss gradient per row; OUT becomes dL/dout ──
+  // ── loss gradient; OUT becomes dL/dout ──
   const float fb = (float)a.b;
   if (net == 0) {
     // Clipped surrogate with the gradient through the active branch only and
-    // the entropy bonus folded into dlog_std (phyz_train.cu:150-196).
+    // the entropy bonus folded into dlog_std (phyz_train.cu:150-196), in three
+    // passes: the standardized actions z of every (row, dim) in parallel (DLS
+    // holds them), each row's log-prob summed over dims in order with its
+    // ratio and branch, then every (row, dim) gradient in parallel.
     const float LN_2PI = 1.8378770664093453f;
-    for (uint32_t r = threadIdx.x; r < R; r += kThreads) {
-      float* o = OUT + r * d.n_out;
-      float* dls = DLS + r * d.n_out;
+    const FastDiv byOut(d.n_out);
+    for (uint32_t e = threadIdx.x; e < rows * d.n_out; e += kTileThreads) {
+      const uint32_t r = byOut.div(e), k = e - r * d.n_out;
+      DLS[r * L.lo + k] = (ACT[r * L.lo + k] - OUT[r * L.lo + k]) / SD[k];
+    }
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < R; r += kTileThreads) {
       if (r >= rows) {
-        for (uint32_t k = 0; k < d.n_out; k++) { o[k] = 0.0f; dls[k] = 0.0f; }
         RS[r * 4 + 0] = RS[r * 4 + 1] = RS[r * 4 + 2] = 0.0f;
         continue;
       }
-      const uint32_t s = a.idx[row0 + r];
-      const float* act = a.act + (size_t)s * d.n_out;
+      const float* z = DLS + r * L.lo;
       float logp = 0.0f;
-      for (uint32_t k = 0; k < d.n_out; k++) {
-        const float z = (act[k] - o[k]) / SD[k];
-        logp += -0.5f * z * z - LSD[k] - 0.5f * LN_2PI;
-      }
-      const float adv = a.adv[s];
-      const float log_ratio = logp - a.logp_old[s];
+      for (uint32_t k = 0; k < d.n_out; k++) logp += -0.5f * z[k] * z[k] - LSD[k] - 0.5f * LN_2PI;
+      const float adv = RV[r * 4 + 0], lp_old = RV[r * 4 + 1];
+      const float log_ratio = logp - lp_old;
       const float ratio = expf(log_ratio);
       const float clipped = clampf(ratio, 1.0f - a.clip, 1.0f + a.clip);
       const float uo = ratio * adv, co = clipped * adv;
       RS[r * 4 + 0] = -(uo < co ? uo : co);
-      RS[r * 4 + 1] = a.logp_old[s] - logp;
+      RS[r * 4 + 1] = lp_old - logp;
       RS[r * 4 + 2] = ratio - 1.0f - log_ratio;
-      const bool active = uo <= co + 1e-12f;
-      const float coef = -adv * ratio / fb;
-      for (uint32_t k = 0; k < d.n_out; k++) {
-        if (!active) {
-          o[k] = 0.0f;
-          dls[k] = -a.entropy_coef / fb;
+      // The row's gradient scale, and whether the unclipped branch is the
+      // active one (an actor row has no use for the critic's column 3).
+      RV[r * 4 + 3] = -adv * ratio / fb;
+      RS[r * 4 + 3] = uo <= co + 1e-12f ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < R * d.n_out; e += kTileThreads) {
+      const uint32_t r = byOut.div(e), k = e - r * d.n_out;
+      float dm = 0.0f, dl = 0.0f;
+      if (r < rows) {
+        if (RS[r * 4 + 3] == 0.0f) {
+          dl = -a.entropy_coef / fb;
         } else {
-          const float z = (act[k] - o[k]) / SD[k];
-          o[k] = coef * (z / SD[k]);
-          dls[k] = coef * (z * z - 1.0f) - a.entropy_coef / fb;
+          const float coef = RV[r * 4 + 3], z = DLS[r * L.lo + k];
+          dm = coef * (z / SD[k]);
+          dl = coef * (z * z - 1.0f) - a.entropy_coef / fb;
         }
       }
+      OUT[r * L.lo + k] = dm;
+      DLS[r * L.lo + k] = dl;
     }
   } else {
     // Squared error to the return with the gradient Huber-clipped at vdelta;
     // the statistic stays the plain squared error (phyz_train.cu:198-208).
-    for (uint32_t r = threadIdx.x; r < R; r += kThreads) {
+    for (uint32_t r = threadIdx.x; r < R; r += kTileThreads) {
       if (r >= rows) {
-        OUT[r] = 0.0f;
+        OUT[r * L.lo] = 0.0f;
         RS[r * 4 + 3] = 0.0f;
         continue;
       }
-      const float err = OUT[r] - a.ret[a.idx[row0 + r]];
+      const float err = OUT[r * L.lo] - RV[r * 4 + 2];
       RS[r * 4 + 3] = err * err;
-      OUT[r] = 2.0f * clampf(err, -a.vdelta, a.vdelta) / fb;
+      OUT[r * L.lo] = 2.0f * clampf(err, -a.vdelta, a.vdelta) / fb;
     }
   }
+  if (MODE == STAGE_LAYER) stage(WB, w + d.oW3(), d.n_out * d.n_h);
   __syncthreads();
 
   // ── layer 3 gradients, tile statistics, dL/dh2 ──
-  dense_grad(OUT, d.n_out, H2, d.n_h, rows, part + d.oW3(), part + d.ob3());
+  dense_grad(OUT, L.lo, d.n_out, H2, L.lh, d.n_h, rows, part + d.oW3(), part + d.ob3());
+  // The column sums of dlog_std and of the statistics, on the last threads
+  // (the gradient items above start from thread 0).
+  const uint32_t back = kTileThreads - 1u - threadIdx.x;
   if (net == 0) {
-    for (uint32_t k = threadIdx.x; k < d.n_out; k += kThreads) {
+    for (uint32_t k = back; k < d.n_out; k += kTileThreads) {
       double acc = 0.0;
-      for (uint32_t r = 0; r < rows; r++) acc += (double)DLS[r * d.n_out + k];
+      for (uint32_t r = 0; r < rows; r++) acc += (double)DLS[r * L.lo + k];
       part[d.mlp_params() + k] = acc;
     }
   }
-  if (threadIdx.x < 4 && (net == 0) == (threadIdx.x < 3)) {
+  if (back >= 32u && back < 36u && (net == 0) == (back < 35u)) {
+    const uint32_t c = back - 32u;
     double acc = 0.0;
-    for (uint32_t r = 0; r < rows; r++) acc += (double)RS[r * 4 + threadIdx.x];
-    a.stats_part[(size_t)blockIdx.x * 4 + threadIdx.x] = acc;
+    for (uint32_t r = 0; r < rows; r++) acc += (double)RS[r * 4 + c];
+    a.stats_part[(size_t)blockIdx.x * 4 + c] = acc;
   }
-  dense_backward_hidden(OUT, d.n_out, w + d.oW3(), H2, d.n_h, DA, R);
-  __syncthreads();
+  dense<EPI_DTANH>(OUT, L.lo, d.n_out, src(L.w_3, w + d.oW3()), d.n_h, nullptr, H2, L.lh, DA, L.lh, R);
+  stage_layer(w + d.oW2(), d.n_h * d.n_h);
+  if (MODE != STAGE_LAYER) __syncthreads();
 
   // ── layer 2 gradients, dL/dh1 ──
-  dense_grad(DA, d.n_h, H1, d.n_h, rows, part + d.oW2(), part + d.ob2());
-  dense_backward_hidden(DA, d.n_h, w + d.oW2(), H1, d.n_h, DB, R);
+  dense_grad(DA, L.lh, d.n_h, H1, L.lh, d.n_h, rows, part + d.oW2(), part + d.ob2());
+  dense<EPI_DTANH>(DA, L.lh, d.n_h, src(L.w_2, w + d.oW2()), d.n_h, nullptr, H1, L.lh, DB, L.lh, R);
   __syncthreads();
 
   // ── layer 1 gradients (input: the gathered rows) ──
-  dense_grad(DB, d.n_h, X, d.n_in, rows, part + d.oW1(), part + d.ob1());
+  dense_grad(DB, L.lh, d.n_h, X, L.lx, d.n_in, rows, part + d.oW1(), part + d.ob1());
 }
+
+// The update's running sums on the device (train.rs:620-627).
+struct UpdateState {
+  double policy_acc, value_acc, brake_acc, kl_acc;
+  uint64_t kl_rows, batches;
+  int stopped;
+  int pad;
+};
 
 struct AdamArgs {
   const double* part[2];
@@ -323,21 +518,74 @@ struct AdamArgs {
   uint32_t n_param[2];
   uint32_t tiles;
   double lr[2], beta1[2], beta2[2], eps[2], wd[2], bc1[2], bc2[2];
-  const int* stopped;
+  // The minibatch's statistics and the KL brake (train.rs:757-777).
+  const double* stats_part;  // [tile][4]
+  uint32_t b;
+  int kl_mode;               // PHZ_KL_CUMULATIVE / PHZ_KL_MINIBATCH
+  double kl_scale, target_kl;
+  UpdateState* st;
+  int* skip;                 // skip[j]: minibatch j does not run; this one is skip[0], the next skip[1]
 };
 
+// Wave 0 of workgroup 0: the four statistic columns summed over the tiles
+// (lane l takes tiles l, l + 64, ..., then a fixed butterfly across lanes),
+// rounded to f32 as the reference's reduce_stats output is, into the running
+// sums; then the brake, which decides whether the next minibatch runs.
+__device__ void brake(const AdamArgs& a) {
+  const uint32_t lane = threadIdx.x;
+  double s[4] = {0.0, 0.0, 0.0, 0.0};
+  for (uint32_t k = lane; k < a.tiles; k += 64)
+    for (int c = 0; c < 4; c++) s[c] += a.stats_part[(size_t)k * 4 + c];
+  for (int c = 0; c < 4; c++)
+    for (int off = 32; off > 0; off >>= 1) s[c] += __shfl_xor(s[c], off, 64);
+  if (lane != 0) return;
+  UpdateState* st = a.st;
+  const double ploss = (double)(float)s[0], kl_sum = (double)(float)s[1];
+  const double k3_sum = (double)(float)s[2], vloss = (double)(float)s[3];
+  const double b = (double)a.b;
+  st->policy_acc += ploss / b;
+  st->value_acc += vloss / b;
+  st->kl_acc += kl_sum;
+  st->kl_rows += a.b;
+  const double rows = (double)(st->kl_rows > 0 ? st->kl_rows : 1);
+  const double reading = (a.kl_mode == PHZ_KL_CUMULATIVE ? fabs(st->kl_acc / rows) : k3_sum / b) / a.kl_scale;
+  st->brake_acc += reading;
+  st->batches += 1;
+  if (reading > a.target_kl) {
+    st->stopped = 1;
+    a.skip[1] = 1;
+  }
+}
+
 // tang's ModuleAdam step, elementwise (phyz_train.cu:268-288), on the sum of
-// the tile partials.
-__global__ void __launch_bounds__(kThreads) ppo_adam(AdamArgs a) {
-  if (*a.stopped) return;
-  const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-  if (t >= a.n_param[0] + a.n_param[1]) return;
-  const int net = t < a.n_param[0] ? 0 : 1;
-  const uint32_t q = net == 0 ? t : t - a.n_param[0];
+// the tile partials. Four lanes share a parameter: lane s sums tiles s, s + 4,
+// ... (two interleaved chains each), a fixed xor butterfly gives all four the
+// same total, and the first applies the step.
+__global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
+  if (*a.skip) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
+    return;
+  }
+  if (blockIdx.x == 0) brake(a);
+  const uint32_t gt = blockIdx.x * kAdamThreads + threadIdx.x;
+  const uint32_t t = gt / kAdamLanes, sub = gt % kAdamLanes;
+  const bool valid = t < a.n_param[0] + a.n_param[1];
+  const int net = valid && t >= a.n_param[0] ? 1 : 0;
+  const uint32_t q = valid ? (net == 0 ? t : t - a.n_param[0]) : 0u;
   const uint32_t np = a.n_param[net];
-  const double* part = a.part[net];
-  double g = 0.0;
-  for (uint32_t k = 0; k < a.tiles; k++) g += part[(size_t)k * np + q];
+  const double* part = a.part[net] + q;
+  double g0 = 0.0, g1 = 0.0;
+  if (valid) {
+    uint32_t k = sub;
+    for (; k + kAdamLanes < a.tiles; k += 2 * kAdamLanes) {
+      g0 += part[(size_t)k * np];
+      g1 += part[(size_t)(k + kAdamLanes) * np];
+    }
+    if (k < a.tiles) g0 += part[(size_t)k * np];
+  }
+  double g = g0 + g1;
+  for (int off = 1; off < kAdamLanes; off <<= 1) g += __shfl_xor(g, off, 64);
+  if (!valid || sub != 0) return;
   const double gr = (double)(float)g;
   double x = a.p[net][q];
   const double lr = a.lr[net];
@@ -361,49 +609,9 @@ __global__ void __launch_bounds__(kThreads) ppo_adam(AdamArgs a) {
     const uint32_t e = q - d.oW2(), j = e / d.n_h, i = e % d.n_h;
     a.wt[net][d.tW2() + i * d.n_h + j] = xf;
   } else if (q >= d.oW3() && q < d.ob3()) {
-    const uint32_t e = q - d.oW3(), k = e / d.n_h, i = e % d.n_h;
-    a.wt[net][d.tW3() + i * d.n_out + k] = xf;
+    const uint32_t e = q - d.oW3(), k2 = e / d.n_h, i = e % d.n_h;
+    a.wt[net][d.tW3() + i * d.n_out + k2] = xf;
   }
-}
-
-// The update's running sums on the device (train.rs:620-627).
-struct UpdateState {
-  double policy_acc, value_acc, brake_acc, kl_acc;
-  uint64_t kl_rows, batches;
-  int stopped;
-  int pad;
-};
-
-struct BrakeArgs {
-  const double* stats_part;
-  uint32_t tiles;
-  uint32_t b;
-  int kl_mode;  // PHZ_KL_CUMULATIVE / PHZ_KL_MINIBATCH
-  double kl_scale, target_kl;
-  UpdateState* st;
-};
-
-// The four statistic columns reduced (rounded to f32, as the reference's
-// reduce_stats output is), then the brake (train.rs:757-777).
-__global__ void ppo_brake(BrakeArgs a) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  UpdateState* st = a.st;
-  if (st->stopped) return;
-  double s[4] = {0.0, 0.0, 0.0, 0.0};
-  for (uint32_t k = 0; k < a.tiles; k++)
-    for (int c = 0; c < 4; c++) s[c] += a.stats_part[(size_t)k * 4 + c];
-  const double ploss = (double)(float)s[0], kl_sum = (double)(float)s[1];
-  const double k3_sum = (double)(float)s[2], vloss = (double)(float)s[3];
-  const double b = (double)a.b;
-  st->policy_acc += ploss / b;
-  st->value_acc += vloss / b;
-  st->kl_acc += kl_sum;
-  st->kl_rows += a.b;
-  const double rows = (double)(st->kl_rows > 0 ? st->kl_rows : 1);
-  const double brake = (a.kl_mode == PHZ_KL_CUMULATIVE ? fabs(st->kl_acc / rows) : k3_sum / b) / a.kl_scale;
-  st->brake_acc += brake;
-  st->batches += 1;
-  if (brake > a.target_kl) st->stopped = 1;
 }
 
 // ── host side ───────────────────────────────────────────────────────────────
@@ -442,6 +650,7 @@ struct phz_train {
   uint32_t n_param[2];   // the actor's includes log_std
   uint64_t capacity = 0, max_b = 0, n_rows = 0;
   uint32_t R = 0, max_tiles = 0;
+  int mode = STAGE_ALL;
   size_t lds_bytes = 0;
   phz_adam_cfg adam[2];
   uint64_t t[2] = {0, 0};
@@ -461,6 +670,8 @@ struct phz_train {
   UpdateState* state = nullptr;
   uint32_t* order = nullptr;
   uint64_t order_cap = 0;
+  int* skip = nullptr;      // per-minibatch stop flags of the current update
+  uint64_t skip_cap = 0;
   std::vector<void*> allocs;
 
   int fail(const std::string& e) { err = e; return 1; }
@@ -481,6 +692,7 @@ struct phz_train {
     if (stream) hipStreamSynchronize(stream);
     for (void* q : allocs) hipFree(q);
     if (order) hipFree(order);
+    if (skip) hipFree(skip);
     if (stream) hipStreamDestroy(stream);
   }
 };
@@ -489,24 +701,34 @@ namespace {
 
 bool set_device(phz_train* t) { return t->hip_ok(hipSetDevice(t->device), "hipSetDevice"); }
 
-// Rows per tile: the most (64, 32, 16 or 8) whose LDS fits 64 KiB, else the
-// most that fits the device's per-workgroup LDS.
+// Rows per tile and weight staging, the first option whose workgroup fits the
+// device's LDS: 32 rows with every weight matrix staged (one load phase), 16
+// rows likewise, then one layer at a time, then weights from HBM; and 8-row
+// tiles as the last resort. PHZ_TRAIN_TILE_ROWS=8|16|32|64 restricts the
+// choice to that row count (tuning, tests).
 bool choose_tile(phz_train* t, size_t lds_limit, std::string& e) {
-  auto bytes = [&](uint32_t R) {
+  auto bytes = [&](uint32_t R, int mode) {
     size_t worst = 0;
-    for (int n = 0; n < 2; n++) worst = std::max<size_t>(worst, Lds(t->dims[n], R).total);
+    for (int n = 0; n < 2; n++) worst = std::max<size_t>(worst, Lds(t->dims[n], R, mode).total);
     return worst * sizeof(float);
   };
-  for (size_t limit : {size_t(65536), lds_limit}) {
-    for (uint32_t R : {64u, 32u, 16u, 8u}) {
-      if (bytes(R) <= limit) {
-        t->R = R;
-        t->lds_bytes = bytes(R);
-        return true;
-      }
+  uint32_t only = 0;
+  if (const char* env = std::getenv("PHZ_TRAIN_TILE_ROWS")) only = (uint32_t)std::atoi(env);
+  struct Option { uint32_t R; int mode; };
+  const Option options[] = {{32, STAGE_ALL},  {16, STAGE_ALL},   {64, STAGE_ALL},  {32, STAGE_LAYER},
+                            {16, STAGE_LAYER}, {64, STAGE_LAYER}, {32, STAGE_NONE}, {16, STAGE_NONE},
+                            {8, STAGE_ALL},   {8, STAGE_LAYER},  {8, STAGE_NONE}};
+  for (const Option& o : options) {
+    if (only && o.R != only) continue;
+    if (bytes(o.R, o.mode) <= lds_limit) {
+      t->R = o.R;
+      t->mode = o.mode;
+      t->lds_bytes = bytes(o.R, o.mode);
+      return true;
     }
   }
-  e = fmt("networks too wide for one tile: 8 rows need %zu bytes of LDS, the device has %zu", bytes(8), lds_limit);
+  e = fmt("networks too wide for one tile: 8 rows need %zu bytes of LDS, the device has %zu", bytes(8, STAGE_NONE),
+          lds_limit);
   return false;
 }
 
@@ -574,7 +796,7 @@ int phz_train_create(phz_net_dims actor, phz_net_dims critic, uint64_t capacity,
       g_train_create_error = fmt("%s has a zero-width layer", what[n]);
       return 1;
     }
-    if (nd[n].n_in > (1u << 16)) {
+    if (nd[n].n_in > (1u << 14)) {  // keeps every in-kernel index product below 2^32
       g_train_create_error = fmt("%s input width %llu is too large", what[n], (unsigned long long)nd[n].n_in);
       return 1;
     }
@@ -612,10 +834,13 @@ int phz_train_create(phz_net_dims actor, phz_net_dims critic, uint64_t capacity,
     return bail(t->err);
   std::string e;
   if (!choose_tile(t, (size_t)lds_limit, e)) return bail(e);
-  if (t->lds_bytes > 65536 &&
-      !t->hip_ok(hipFuncSetAttribute((const void*)ppo_tiles, hipFuncAttributeMaxDynamicSharedMemorySize, (int)t->lds_bytes),
-                 "LDS attribute"))
-    return bail(t->err);
+  if (t->lds_bytes > 65536) {
+    const void* fns[3] = {(const void*)ppo_tiles<STAGE_ALL>, (const void*)ppo_tiles<STAGE_LAYER>,
+                          (const void*)ppo_tiles<STAGE_NONE>};
+    if (!t->hip_ok(hipFuncSetAttribute(fns[t->mode], hipFuncAttributeMaxDynamicSharedMemorySize, (int)t->lds_bytes),
+                   "LDS attribute"))
+      return bail(t->err);
+  }
   t->max_tiles = (uint32_t)((max_b + t->R - 1) / t->R);
   bool ok = true;
   for (int n = 0; n < 2 && ok; n++) {
@@ -699,8 +924,19 @@ int phz_train_upload_batch(phz_train* t, uint64_t n_rows, const float* obs_a, ui
   return 0;
 }
 
-int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
-                     const phz_ppo_cfg* cfg, phz_update_stats* out) {
+}  // extern "C"
+
+namespace {
+
+// Per-kernel hipEvent time over one update (measurement only).
+struct KernelTimes {
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  double ms[2] = {0.0, 0.0};
+  uint64_t launches = 0;
+};
+
+int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
+               const phz_ppo_cfg* cfg, phz_update_stats* out, KernelTimes* tm) {
   if (!t) return 1;
   t->err.clear();
   if (!cfg || !out) return t->fail("null configuration or output");
@@ -739,11 +975,21 @@ int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t*
     if (!t->hip_ok(hipMemcpyAsync(t->order + e * n, order[e], n * sizeof(uint32_t), hipMemcpyHostToDevice, t->stream),
                    "upload shuffles"))
       return 1;
-  if (!t->hip_ok(hipMemsetAsync(t->state, 0, sizeof(UpdateState), t->stream), "reset update state")) return 1;
+  uint64_t total = 0;  // minibatches this update can launch
+  for (uint64_t e = 0; e < epochs; e++) total += (n + cfg->minibatch - 1) / cfg->minibatch;
+  if (total + 1 > t->skip_cap) {
+    if (t->skip) hipFree(t->skip);
+    t->skip = nullptr;
+    t->skip_cap = 0;
+    if (!t->hip_ok(hipMalloc(&t->skip, (total + 1) * sizeof(int)), "alloc stop flags")) return 1;
+    t->skip_cap = total + 1;
+  }
+  if (!t->hip_ok(hipMemsetAsync(t->state, 0, sizeof(UpdateState), t->stream), "reset update state") ||
+      !t->hip_ok(hipMemsetAsync(t->skip, 0, (total + 1) * sizeof(int), t->stream), "reset stop flags"))
+    return 1;
 
   TileArgs ta{};
   AdamArgs aa{};
-  BrakeArgs ba{};
   for (int k = 0; k < 2; k++) {
     ta.x[k] = t->obs[k];
     ta.w[k] = t->w[k];
@@ -774,14 +1020,14 @@ int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t*
   ta.entropy_coef = (float)cfg->entropy_coef;
   ta.vdelta = (float)cfg->vdelta;
   ta.stats_part = t->stats_part;
-  ta.stopped = &t->state->stopped;
-  aa.stopped = &t->state->stopped;
-  ba.stats_part = t->stats_part;
-  ba.kl_mode = cfg->kl_mode;
-  ba.kl_scale = cfg->kl_scale;
-  ba.target_kl = cfg->target_kl;
-  ba.st = t->state;
+  aa.stats_part = t->stats_part;
+  aa.kl_mode = cfg->kl_mode;
+  aa.kl_scale = cfg->kl_scale;
+  aa.target_kl = cfg->target_kl;
+  aa.st = t->state;
   const uint32_t n_all = t->n_param[0] + t->n_param[1];
+  auto tiles_kernel = t->mode == STAGE_ALL ? ppo_tiles<STAGE_ALL>
+                      : t->mode == STAGE_LAYER ? ppo_tiles<STAGE_LAYER> : ppo_tiles<STAGE_NONE>;
   uint64_t j = 0;  // minibatch counter within this update
   for (uint64_t e = 0; e < epochs; e++) {
     for (uint64_t s = 0; s < n; s += cfg->minibatch, j++) {
@@ -789,17 +1035,30 @@ int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t*
       const uint32_t tiles = (b + t->R - 1) / t->R;
       ta.idx = t->order + e * n + s;
       ta.b = b;
-      hipLaunchKernelGGL(ppo_tiles, dim3(tiles, 2), dim3(kThreads), t->lds_bytes, t->stream, ta);
+      ta.skip = t->skip + j;
       aa.tiles = tiles;
+      aa.b = b;
+      aa.skip = t->skip + j;
       for (int k = 0; k < 2; k++) {
         // The step this minibatch would be, if it runs: every earlier one ran.
         aa.bc1[k] = 1.0 - powi(t->adam[k].beta1, t->t[k] + j + 1);
         aa.bc2[k] = 1.0 - powi(t->adam[k].beta2, t->t[k] + j + 1);
       }
-      hipLaunchKernelGGL(ppo_adam, dim3((n_all + kThreads - 1) / kThreads), dim3(kThreads), 0, t->stream, aa);
-      ba.tiles = tiles;
-      ba.b = b;
-      hipLaunchKernelGGL(ppo_brake, dim3(1), dim3(64), 0, t->stream, ba);
+      if (tm) hipEventRecord(tm->ev[0], t->stream);
+      hipLaunchKernelGGL(tiles_kernel, dim3(tiles, 2), dim3(kTileThreads), t->lds_bytes, t->stream, ta);
+      if (tm) hipEventRecord(tm->ev[1], t->stream);
+      hipLaunchKernelGGL(ppo_adam, dim3((n_all * kAdamLanes + kAdamThreads - 1) / kAdamThreads), dim3(kAdamThreads), 0,
+                         t->stream, aa);
+      if (tm) {
+        hipEventRecord(tm->ev[2], t->stream);
+        if (!t->hip_ok(hipEventSynchronize(tm->ev[2]), "time update")) return 1;
+        for (int k = 0; k < 2; k++) {
+          float ms = 0.0f;
+          if (!t->hip_ok(hipEventElapsedTime(&ms, tm->ev[k], tm->ev[k + 1]), "time update")) return 1;
+          tm->ms[k] += ms;
+        }
+        tm->launches++;
+      }
     }
   }
   if (!t->hip_ok(hipGetLastError(), "launch update")) return 1;
@@ -816,6 +1075,30 @@ int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t*
   t->t[0] += st.batches;
   t->t[1] += st.batches;
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int phz_train_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
+                     const phz_ppo_cfg* cfg, phz_update_stats* out) {
+  return run_update(t, order, order_lens, n_order, cfg, out, nullptr);
+}
+
+int phz_train_time_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
+                          const phz_ppo_cfg* cfg, phz_update_stats* out, double* ms_kernels, uint64_t* minibatches) {
+  if (!t) return 1;
+  if (!ms_kernels || !minibatches) return t->fail("null timing output");
+  if (!set_device(t)) return 1;
+  KernelTimes tm;
+  for (auto& e : tm.ev)
+    if (!t->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
+  const int rc = run_update(t, order, order_lens, n_order, cfg, out, &tm);
+  for (auto& e : tm.ev) hipEventDestroy(e);
+  for (int k = 0; k < 2; k++) ms_kernels[k] = tm.ms[k];
+  *minibatches = tm.launches;
+  return rc;
 }
 
 }  // extern "C"

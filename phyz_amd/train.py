@@ -177,16 +177,36 @@ class TrainPipeline:
             args += [c.ctypes.data_as(_lib.fp), c.size]
         self._check(self._L.phz_train_upload_batch(self._h, int(n_rows), *args))
 
-    def update(self, order: Sequence[Sequence[int]], cfg: PpoUpdateCfg) -> UpdateStats:
-        """cfg.epochs passes over the uploaded batch; order[e] is epoch e's shuffle
-        of 0..n_rows (the caller owns the PRNG, as in the reference)."""
+    @staticmethod
+    def _args(order, cfg):
         shuffles = [np.ascontiguousarray(np.asarray(o, dtype=np.uint32).reshape(-1)) for o in order]
         n = len(shuffles)
         ptrs = (_lib.u32p * max(n, 1))(*[s.ctypes.data_as(_lib.u32p) for s in shuffles])
         lens = (C.c_uint64 * max(n, 1))(*[s.size for s in shuffles])
         c = _lib.PpoCfg(float(cfg.clip), float(cfg.entropy_coef), float(cfg.vdelta), int(cfg.minibatch),
                         int(cfg.epochs), float(cfg.target_kl), float(cfg.kl_scale), int(cfg.kl_mode))
+        return shuffles, ptrs, lens, n, c
+
+    @staticmethod
+    def _stats(out) -> UpdateStats:
+        return UpdateStats(out.policy_loss, out.value_loss, out.kl, int(out.grad_steps), bool(out.stopped_early))
+
+    def update(self, order: Sequence[Sequence[int]], cfg: PpoUpdateCfg) -> UpdateStats:
+        """cfg.epochs passes over the uploaded batch; order[e] is epoch e's shuffle
+        of 0..n_rows (the caller owns the PRNG, as in the reference)."""
+        keep, ptrs, lens, n, c = self._args(order, cfg)
         out = _lib.UpdateStats()
         self._check(self._L.phz_train_update(self._h, ptrs, lens, n, C.byref(c), C.byref(out)))
-        return UpdateStats(out.policy_loss, out.value_loss, out.kl, int(out.grad_steps), bool(out.stopped_early))
+        return self._stats(out)
+
+    def time_update(self, order: Sequence[Sequence[int]], cfg: PpoUpdateCfg):
+        """An update with hipEvents around every launch: (stats, summed ms of the
+        tile kernel and of the Adam + brake kernel, minibatches launched)."""
+        keep, ptrs, lens, n, c = self._args(order, cfg)
+        out = _lib.UpdateStats()
+        ms = np.zeros(2)
+        mbs = C.c_uint64()
+        self._check(self._L.phz_train_time_update(self._h, ptrs, lens, n, C.byref(c), C.byref(out),
+                                                  ms.ctypes.data_as(_lib.dp), C.byref(mbs)))
+        return self._stats(out), ms, int(mbs.value)
 
