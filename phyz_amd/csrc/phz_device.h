@@ -57,6 +57,27 @@ constexpr int ndof_of(int jt) { return jt == J_FIXED ? 0 : (jt == J_BALL ? 3 : (
 // denominator can vanish divides by dmax(d, floor), with the floor below the
 // select's own threshold so that the bound cannot be folded back into d.
 __device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
+// sin and cos of r in [-pi/4, pi/4] (f32), then of k pi/2 + r: Taylor series
+// through r^9 and r^10 (truncation below 3e-9 on the interval) and the
+// quadrant's sign and swap. Used for the Box-Muller angle below; joint angles
+// take the library routine, whose small-argument path is as short.
+__device__ __forceinline__ void quadrant_sincos(float r, float k, float* s, float* c) {
+  const float r2 = r * r;
+  float ps = fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
+  ps = fmaf(r2, ps, 1.0f / 120.0f);
+  ps = fmaf(r2, ps, -1.0f / 6.0f);
+  const float sr = fmaf(r * r2, ps, r);
+  float pc = fmaf(r2, -1.0f / 3628800.0f, 1.0f / 40320.0f);
+  pc = fmaf(r2, pc, -1.0f / 720.0f);
+  pc = fmaf(r2, pc, 1.0f / 24.0f);
+  pc = fmaf(r2, pc, -0.5f);
+  const float cr = fmaf(r2, pc, 1.0f);
+  const int q = (int)k & 3;
+  const float a = (q & 1) ? cr : sr;
+  const float b = (q & 1) ? sr : cr;
+  *s = (q & 2) ? -a : a;
+  *c = ((q + 1) & 2) ? -b : b;
+}
 __device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
 // sin and cos of a Box-Muller angle x in [0, 2*pi] (f64). x = k*pi/2 + r with
@@ -96,7 +117,17 @@ __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
   *s = (q & 2) ? -a : a;
   *c = ((q + 1) & 2) ? -b : b;
 }
-__device__ __forceinline__ void angle_sincos(float x, float* s, float* c) { sincosf(x, s, c); }
+// sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1), in
+// turns: 4u and its nearest integer k are exact for the 24-bit uniforms, so
+// the only rounding before quadrant_sincos is r = (4u - k) pi/2.
+__device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
+  const float t = 4.0f * u;
+  const float k = rintf(t);
+  quadrant_sincos((t - k) * 0x1.921fb6p+0f, k, s, c);
+}
+__device__ __forceinline__ void turn_sincos(double u, double* s, double* c) {
+  angle_sincos(6.283185307179586 * u, s, c);
+}
 __device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double dlog(double x) { return log(x); }
 __device__ __forceinline__ float dlog(float x) { return logf(x); }
@@ -1150,7 +1181,7 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
         if constexpr (mine0 || mine1) {
           T r = dsqrt(T(-2) * dlog(T(1) - u1));
           T sn, cs;
-          angle_sincos(T(6.283185307179586) * u2, &sn, &cs);
+          turn_sincos(u2, &sn, &cs);
           if constexpr (mine0) ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
           if constexpr (mine1) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
         }
