@@ -214,44 +214,48 @@ __device__ void dense(const float* __restrict__ X, uint32_t ldx, uint32_t K, con
   }
 }
 
-// Tile partials of a linear layer's gradients: Gw[o][i] = sum_r D[r][o] X[r][i]
-// and Gb[o] = sum_r D[r][o] over the tile's valid rows, each in f64 and in row
-// order (the reference's row loops accumulate in double, phyz_train.cu:226-260).
-// An item is a 2 x 4 block (two outputs by four inputs): per row, two D values
-// and one float4 of X feed eight sums; the items of the first input quad also
-// carry their outputs' bias sums. Rows of X are padded to whole float4s; sums
-// that fall in the padding are not stored.
+typedef double double4_t __attribute__((ext_vector_type(4)));
+
+// Tile partials of a linear layer's gradients, Gw[o][i] = sum_r D[r][o] X[r][i]
+// and Gb[o] = sum_r D[r][o], in f64 (the reference's row loops accumulate in
+// double, phyz_train.cu:226-260), on the matrix cores: each wave takes 16 x 16
+// (o, i) blocks and runs one v_mfma_f64_16x16x4 per four rows over all R rows.
+// Lane l feeds A = D[r0 + l/16][o0 + l%16] and B = X[r0 + l/16][i0 + l%16] and
+// holds Gw[o0 + l/16 + 4v][i0 + l%16] in accumulator v. Rows past the
+// minibatch have D = 0 (and finite X), so they add nothing; outputs and
+// inputs past O and I read clamped in-range values and are not stored. Every
+// sum is an f64 sum in an order fixed by the hardware, so a tile's partials
+// are reproducible. The bias sums use four lanes per output: rows p, p + 4,
+// ... for lane p, combined by a fixed butterfly.
 __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O, const float* __restrict__ X,
-                           uint32_t ldx, uint32_t I, uint32_t rows, double* __restrict__ Gw, double* __restrict__ Gb) {
-  const uint32_t OP = (O + 1u) / 2u, IQ = (I + 3u) / 4u;
-  const FastDiv byIQ(IQ);
-  for (uint32_t it = threadIdx.x; it < OP * IQ; it += kTileThreads) {
-    const uint32_t op = byIQ.div(it), o0 = op * 2u, i0 = (it - op * IQ) * 4u;
-    const uint32_t o1 = o0 + 1u < O ? o0 + 1u : o0;  // an odd last output pairs with itself
-    double acc[2][4] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
-    double bias[2] = {0.0, 0.0};
-#pragma unroll 4
-    for (uint32_t r = 0; r < rows; r++) {
-      const double dv[2] = {(double)D[r * ldd + o0], (double)D[r * ldd + o1]};
-      const float4 xq = *reinterpret_cast<const float4*>(X + r * ldx + i0);
-      const double xv[4] = {(double)xq.x, (double)xq.y, (double)xq.z, (double)xq.w};
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        bias[u] += dv[u];
-#pragma unroll
-        for (int v = 0; v < 4; v++) acc[u][v] += dv[u] * xv[v];
-      }
+                           uint32_t ldx, uint32_t I, uint32_t R, double* __restrict__ Gw, double* __restrict__ Gb) {
+  const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
+  const uint32_t lr = lane / 16u, lc = lane % 16u;
+  const uint32_t OB = (O + 15u) / 16u, IB = (I + 15u) / 16u;
+  for (uint32_t blk = wave; blk < OB * IB; blk += kTileThreads / 64u) {
+    const uint32_t ob = blk / IB, o0 = ob * 16u, i0 = (blk - ob * IB) * 16u;
+    const uint32_t oa = o0 + lc < O ? o0 + lc : O - 1u;
+    const uint32_t ia = i0 + lc < I ? i0 + lc : I - 1u;
+    double4_t acc = {0.0, 0.0, 0.0, 0.0};
+    for (uint32_t r0 = 0; r0 < R; r0 += 4u) {
+      const double av = (double)D[(r0 + lr) * ldd + oa];
+      const double bv = (double)X[(r0 + lr) * ldx + ia];
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const uint32_t o = u == 0 ? o0 : o0 + 1u;
-      if (o >= O) break;
-      double* g = Gw + (size_t)o * I + i0;
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-        if (i0 + v < I) g[v] = acc[u][v];
-      if (i0 == 0) Gb[o] = bias[u];
+    for (int v = 0; v < 4; v++) {
+      const uint32_t o = o0 + lr + 4u * v, i = i0 + lc;
+      if (o < O && i < I) Gw[(size_t)o * I + i] = acc[v];
     }
+  }
+  for (uint32_t t = threadIdx.x; t < 4u * ((O + 15u) & ~15u); t += kTileThreads) {
+    const uint32_t o = t / 4u, p = t % 4u;
+    double acc = 0.0;
+    if (o < O)
+      for (uint32_t r = p; r < R; r += 4u) acc += (double)D[r * ldd + o];
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (p == 0 && o < O) Gb[o] = acc;
   }
 }
 
@@ -469,7 +473,7 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
   __syncthreads();
 
   // ── layer 3 gradients, tile statistics, dL/dh2 ──
-  dense_grad(OUT, L.lo, d.n_out, H2, L.lh, d.n_h, rows, part + d.oW3(), part + d.ob3());
+  dense_grad(OUT, L.lo, d.n_out, H2, L.lh, d.n_h, R, part + d.oW3(), part + d.ob3());
   // The column sums of dlog_std and of the statistics, on the last threads
   // (the gradient items above start from thread 0).
   const uint32_t back = kTileThreads - 1u - threadIdx.x;
@@ -491,12 +495,12 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
   if (MODE != STAGE_LAYER) __syncthreads();
 
   // ── layer 2 gradients, dL/dh1 ──
-  dense_grad(DA, L.lh, d.n_h, H1, L.lh, d.n_h, rows, part + d.oW2(), part + d.ob2());
+  dense_grad(DA, L.lh, d.n_h, H1, L.lh, d.n_h, R, part + d.oW2(), part + d.ob2());
   dense<EPI_DTANH>(DA, L.lh, d.n_h, src(L.w_2, w + d.oW2()), d.n_h, nullptr, H1, L.lh, DB, L.lh, R);
   __syncthreads();
 
   // ── layer 1 gradients (input: the gathered rows) ──
-  dense_grad(DB, L.lh, d.n_h, X, L.lx, d.n_in, rows, part + d.oW1(), part + d.ob1());
+  dense_grad(DB, L.lh, d.n_h, X, L.lx, d.n_in, R, part + d.oW1(), part + d.ob1());
 }
 
 // The update's running sums on the device (train.rs:620-627).
