@@ -49,7 +49,6 @@ namespace {
 constexpr int kTileThreads = 512;  // 8 waves per tile workgroup (2 per SIMD)
 constexpr int kAdamThreads = 64;   // one wave per Adam workgroup: spread over every CU
 constexpr int kAdamLanes = 4;      // lanes that share one parameter's sum over the tiles
-constexpr int kRowBlock = 4;       // rows a thread carries through one dense-layer item
 constexpr uint32_t kMaxHidden = 256;  // TRAIN_MAX_H (train.rs:46)
 constexpr uint32_t kMaxOut = 64;      // TRAIN_MAX_OUT (train.rs:50)
 
@@ -160,56 +159,51 @@ struct FastDiv {
 
 enum { EPI_TANH = 0, EPI_LINEAR = 1, EPI_DTANH = 2 };
 
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
 // Y[r][j] for rows r < R, columns j < N of
 //   EPI_TANH    tanh(b[j] + sum_k X[r][k] Wkn[k][j])
 //   EPI_LINEAR  b[j] + sum_k X[r][k] Wkn[k][j]
 //   EPI_DTANH   (sum_k X[r][k] Wkn[k][j]) (1 - H[r][j]^2)
 // Wkn is [K][N] row-major: the transposed mirror for a forward layer, the
-// row-major weights for a backprop. Lanes run over j (conflict-free Wkn reads,
-// broadcast float4 reads of X); each item carries kRowBlock rows. The sum
-// adds k in order, from the bias in the forward pass, as the reference's
-// per-row loops do (phyz_train.cu:115-132, 212-222).
+// row-major weights for a backprop. On the matrix cores: each wave takes 16 x
+// 16 (r, j) blocks, its accumulators start from the bias, and one
+// v_mfma_f32_16x16x4 per four inputs adds the products. Lane l feeds
+// A = X[r0 + l%16][k0 + l/16] and B = Wkn[k0 + l/16][j0 + l%16] and holds
+// Y[r0 + 4(l/16) + v][j0 + l%16] in accumulator v. Inputs past K are zero
+// (the rows' padding columns are never written, so they are masked, not
+// read); rows past R and columns past N read clamped in-range values and are
+// not stored.
 template <int EPI>
 __device__ void dense(const float* __restrict__ X, uint32_t ldx, uint32_t K, const float* __restrict__ Wkn,
                       uint32_t N, const float* __restrict__ bias, const float* __restrict__ H, uint32_t ldh,
                       float* __restrict__ Y, uint32_t ldy, uint32_t R) {
-  const uint32_t NP = (N + 63u) & ~63u;
-  const uint32_t items = (R / kRowBlock) * NP;
-  const FastDiv byNP(NP);
-  for (uint32_t it = threadIdx.x; it < items; it += kTileThreads) {
-    const uint32_t q = byNP.div(it), j = it - q * NP, r0 = q * kRowBlock;
-    if (j >= N) continue;
-    float acc[kRowBlock];
-    const float init = EPI == EPI_DTANH ? 0.0f : bias[j];
-#pragma unroll
-    for (int rr = 0; rr < kRowBlock; rr++) acc[rr] = init;
-    uint32_t k = 0;
-    for (; k + 4 <= K; k += 4) {
-      const float w0 = Wkn[(k + 0) * N + j], w1 = Wkn[(k + 1) * N + j];
-      const float w2 = Wkn[(k + 2) * N + j], w3 = Wkn[(k + 3) * N + j];
-#pragma unroll
-      for (int rr = 0; rr < kRowBlock; rr++) {
-        const float4 x = *reinterpret_cast<const float4*>(X + (r0 + rr) * ldx + k);
-        acc[rr] += w0 * x.x;
-        acc[rr] += w1 * x.y;
-        acc[rr] += w2 * x.z;
-        acc[rr] += w3 * x.w;
-      }
-    }
-    for (; k < K; k++) {
-      const float wk = Wkn[k * N + j];
-#pragma unroll
-      for (int rr = 0; rr < kRowBlock; rr++) acc[rr] += wk * X[(r0 + rr) * ldx + k];
+  const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
+  const uint32_t lr = lane / 16u, lc = lane % 16u;
+  const uint32_t RB = (R + 15u) / 16u, NB = (N + 15u) / 16u;
+  for (uint32_t blk = wave; blk < RB * NB; blk += kTileThreads / 64u) {
+    const uint32_t rb = blk / NB, r0 = rb * 16u, j0 = (blk - rb * NB) * 16u;
+    const uint32_t ra = r0 + lc < R ? r0 + lc : R - 1u;
+    const uint32_t jb = j0 + lc < N ? j0 + lc : N - 1u;
+    const float init = EPI == EPI_DTANH ? 0.0f : bias[jb];
+    float4_t acc = {init, init, init, init};
+    for (uint32_t k0 = 0; k0 < K; k0 += 4u) {
+      const uint32_t k = k0 + lr;
+      const float av = k < K ? X[ra * ldx + k] : 0.0f;
+      const float bv = k < K ? Wkn[k * N + jb] : 0.0f;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int rr = 0; rr < kRowBlock; rr++) {
-      float y = acc[rr];
+    for (int v = 0; v < 4; v++) {
+      const uint32_t r = r0 + 4u * lr + v, j = j0 + lc;
+      if (r >= R || j >= N) continue;
+      float y = acc[v];
       if (EPI == EPI_TANH) y = act_tanh(y);
       if (EPI == EPI_DTANH) {
-        const float h = H[(r0 + rr) * ldh + j];
+        const float h = H[r * ldh + j];
         y = y * (1.0f - h * h);
       }
-      Y[(r0 + rr) * ldy + j] = y;
+      Y[r * ldy + j] = y;
     }
   }
 }
