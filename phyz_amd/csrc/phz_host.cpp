@@ -160,6 +160,9 @@ struct Features {
   int dist = 0;
   double a = 0, b = 1;
   std::vector<int> noise_dofs;
+  // The launch's workgroups of 64 worlds and the device's CUs (phz_sim_create),
+  // for the partition plan.
+  int wgs = 0, cus = 256;
   // Terms of the CPU model that the device body table has no slots for
   // (joint.rs:27-104, model.rs:18-82): the soft position limit and dry friction
   // of one-DOF joints (one entry per body; empty: none), and actuators (empty:
@@ -279,14 +282,68 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   const bool forced = want == "1" || want == "2";
   if (parts.size() < 2) return lane_per_world();
   if (mode == 2 && !forced && nb < 14) return lane_per_world();
-  // At most 8 waves: merge the two smallest parts while there are more.
-  while (parts.size() > 8) {
-    std::sort(parts.begin(), parts.end(), [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); });
-    parts[1].insert(parts[1].end(), parts[0].begin(), parts[0].end());
-    parts.erase(parts.begin());
+  // Waves per world group. pack(cap) puts the parts into at most cap groups
+  // by body count: with more parts than cap, largest first into the lightest
+  // group, group 0 starting from the floating trunk's bodies (it runs the
+  // trunk's passes 2 and 3); otherwise one part per group, the smallest in
+  // group 0. The plan is the one of caps 8, 4, 2 whose busiest SIMD carries
+  // the fewest bodies per step, for the launch's workgroups per CU with waves
+  // dealt to the 4 SIMDs in turn; ties keep more waves. Every plan measured on
+  // MI355X ranks as this predicts (humanoid, 32768 worlds: 2 waves 2.43e9
+  // world-steps/s, 4 waves 2.00e9; hand, 16384 worlds: 4 waves 2.02e9 f32 /
+  // 1.35e9 f64, 5 waves 1.93e9 / 1.05e9; ModelBuilder humanoid with balanced
+  // limbs: 4 waves 3.05e9, 2 waves 2.83e9; welded-palm hand without a
+  // barrier: 5 waves 5.12e9 f64, 4 waves 4.35e9). PHZ_MAX_GROUPS forces a cap.
+  int ntrunk = 0;
+  for (int i = 0; i < nb; i++) ntrunk += trunk[i];
+  const long t0 = mode == 2 ? ntrunk : 0;
+  auto by_size = [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); };
+  auto pack = [&](int cap) {
+    std::vector<std::vector<int>> g = parts;
+    if ((int)g.size() <= cap) {
+      std::stable_sort(g.begin(), g.end(), by_size);
+      return g;
+    }
+    std::stable_sort(g.begin(), g.end(), [&](const std::vector<int>& a, const std::vector<int>& b) { return by_size(b, a); });
+    std::vector<std::vector<int>> bins(cap);
+    std::vector<long> load(cap, 0);
+    load[0] = t0;
+    for (auto& p : g) {
+      const int k = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+      bins[k].insert(bins[k].end(), p.begin(), p.end());
+      load[k] += (long)p.size();
+    }
+    if (bins[0].empty()) {  // group 0 still takes a part: the lightest group's
+      int k = 0;
+      for (int j = 1; j < cap; j++)
+        if (!bins[j].empty() && (k == 0 || load[j] < load[k])) k = j;
+      bins[0].swap(bins[k]);
+    }
+    g.clear();
+    for (auto& b : bins) if (!b.empty()) g.push_back(b);
+    return g;
+  };
+  auto busiest = [&](const std::vector<std::vector<int>>& g) {
+    const int ng = (int)g.size(), cus = std::max(f.cus, 1);
+    const int rounds = std::max(1, (f.wgs + cus - 1) / cus);
+    long load[4] = {0, 0, 0, 0};
+    for (int r = 0; r < rounds; r++)
+      for (int k = 0; k < ng; k++) load[(r * ng + k) % 4] += (long)g[k].size() + (k == 0 ? t0 : 0);
+    return *std::max_element(load, load + 4);
+  };
+  if (const char* e = std::getenv("PHZ_MAX_GROUPS")) {
+    parts = pack(std::max(1, std::min(8, std::atoi(e))));
+  } else {
+    std::vector<std::vector<int>> best;
+    long best_load = -1;
+    for (int cap : {8, 4, 2}) {
+      std::vector<std::vector<int>> g = pack(cap);
+      const long l = busiest(g);
+      if (best_load < 0 || l < best_load) { best_load = l; best = g; }
+    }
+    parts = best;
   }
-  // Group 0 carries the trunk (floating trunk), so it takes the smallest part.
-  std::stable_sort(parts.begin(), parts.end(), [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); });
+  if (parts.size() < 2) return lane_per_world();
   pl.mode = mode;
   for (int i = 0; i < nb; i++) if (trunk[i]) pl.trunk.push_back(i);
   for (auto& p : parts) {
@@ -592,9 +649,26 @@ struct CodeObject {
 std::mutex g_compile_mu;
 std::unordered_map<uint64_t, std::shared_ptr<CodeObject>> g_code_cache;
 
+// The compiler that hiprtc calls resolve to. A process that loaded another
+// ROCm's libhiprtc.so.7 first (a Python wheel may bundle one under the same
+// soname) compiles with that one, which generates different code for the same
+// source: the cache key includes it, so code objects from two compilers never
+// meet in one process.
+const std::string& compiler_id() {
+  static const std::string id = [] {
+    int major = 0, minor = 0;
+    std::string s = hiprtcVersion(&major, &minor) == HIPRTC_SUCCESS ? fmt("hiprtc %d.%d", major, minor) : "hiprtc ?";
+    Dl_info info;
+    if (dladdr((void*)&hiprtcCompileProgram, &info) && info.dli_fname) s += std::string(" ") + info.dli_fname;
+    return s;
+  }();
+  return id;
+}
+
 std::shared_ptr<CodeObject> compile_source(const std::string& src, Build build, std::string& err) {
   std::string key_text = src;
   for (const auto& o : compile_options(build)) key_text += "\n" + o;
+  key_text += "\n" + compiler_id();
   const uint64_t key = fnv1a(key_text);
   std::lock_guard<std::mutex> lk(g_compile_mu);
   auto it = g_code_cache.find(key);
@@ -1401,6 +1475,13 @@ int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t 
       return 1;
     }
     s->ctrl_rows = (int)std::max(nv, 1u);
+  }
+  {
+    int cus = 256;
+    if (device_ordinal >= 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_ordinal) != hipSuccess)
+      cus = 256;
+    s->feat.wgs = s->stride / 64;
+    s->feat.cus = std::max(cus, 1);
   }
   *out = s.release();
   return 0;

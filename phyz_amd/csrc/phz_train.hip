@@ -927,10 +927,17 @@ int phz_train_upload_batch(phz_train* t, uint64_t n_rows, const float* obs_a, ui
 namespace {
 
 // Per-kernel hipEvent time over one update (measurement only).
+// An event-timed update: three events per minibatch (before the tile kernel,
+// between the two kernels, after the Adam kernel), all recorded as the
+// launches are queued and read after the update's final synchronisation, so
+// no host wait falls between a launch and its events.
 struct KernelTimes {
-  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  std::vector<hipEvent_t> ev;
   double ms[2] = {0.0, 0.0};
   uint64_t launches = 0;
+  ~KernelTimes() {
+    for (auto e : ev) hipEventDestroy(e);
+  }
 };
 
 int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order_lens, uint64_t n_order,
@@ -962,6 +969,12 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
                            (unsigned long long)n));
   }
   if (!set_device(t)) return 1;
+  if (tm) {
+    const uint64_t total = epochs * ((n + cfg->minibatch - 1) / cfg->minibatch);
+    tm->ev.assign(3 * total, nullptr);
+    for (auto& e : tm->ev)
+      if (!t->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
+  }
   if (epochs * n > t->order_cap) {
     if (t->order) hipFree(t->order);
     t->order = nullptr;
@@ -1042,21 +1055,12 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
         aa.bc1[k] = 1.0 - powi(t->adam[k].beta1, t->t[k] + j + 1);
         aa.bc2[k] = 1.0 - powi(t->adam[k].beta2, t->t[k] + j + 1);
       }
-      if (tm) hipEventRecord(tm->ev[0], t->stream);
+      if (tm) hipEventRecord(tm->ev[3 * j], t->stream);
       hipLaunchKernelGGL(tiles_kernel, dim3(tiles, 2), dim3(kTileThreads), t->lds_bytes, t->stream, ta);
-      if (tm) hipEventRecord(tm->ev[1], t->stream);
+      if (tm) hipEventRecord(tm->ev[3 * j + 1], t->stream);
       hipLaunchKernelGGL(ppo_adam, dim3((n_all * kAdamLanes + kAdamThreads - 1) / kAdamThreads), dim3(kAdamThreads), 0,
                          t->stream, aa);
-      if (tm) {
-        hipEventRecord(tm->ev[2], t->stream);
-        if (!t->hip_ok(hipEventSynchronize(tm->ev[2]), "time update")) return 1;
-        for (int k = 0; k < 2; k++) {
-          float ms = 0.0f;
-          if (!t->hip_ok(hipEventElapsedTime(&ms, tm->ev[k], tm->ev[k + 1]), "time update")) return 1;
-          tm->ms[k] += ms;
-        }
-        tm->launches++;
-      }
+      if (tm) hipEventRecord(tm->ev[3 * j + 2], t->stream);
     }
   }
   if (!t->hip_ok(hipGetLastError(), "launch update")) return 1;
@@ -1064,6 +1068,15 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
   if (!t->hip_ok(hipMemcpyAsync(&st, t->state, sizeof st, hipMemcpyDeviceToHost, t->stream), "read update state") ||
       !t->hip_ok(hipStreamSynchronize(t->stream), "update"))
     return 1;
+  if (tm) {
+    for (uint64_t i = 0; i < j; i++)
+      for (int k = 0; k < 2; k++) {
+        float ms = 0.0f;
+        if (!t->hip_ok(hipEventElapsedTime(&ms, tm->ev[3 * i + k], tm->ev[3 * i + k + 1]), "time update")) return 1;
+        tm->ms[k] += ms;
+      }
+    tm->launches = j;
+  }
   const double nb = (double)std::max<uint64_t>(st.batches, 1);
   out->policy_loss = st.policy_acc / nb;
   out->value_loss = st.value_acc / nb;
@@ -1090,10 +1103,7 @@ int phz_train_time_update(phz_train* t, const uint32_t* const* order, const uint
   if (!ms_kernels || !minibatches) return t->fail("null timing output");
   if (!set_device(t)) return 1;
   KernelTimes tm;
-  for (auto& e : tm.ev)
-    if (!t->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
   const int rc = run_update(t, order, order_lens, n_order, cfg, out, &tm);
-  for (auto& e : tm.ev) hipEventDestroy(e);
   for (int k = 0; k < 2; k++) ms_kernels[k] = tm.ms[k];
   *minibatches = tm.launches;
   return rc;

@@ -8,7 +8,6 @@ import math
 import numpy as np
 import pytest
 import scipy.stats
-import torch
 
 from oracle import policy_ref as PR
 from oracle.oracle import Oracle, world_seed as c_world_seed
@@ -63,7 +62,11 @@ def test_mlp_forward_known_answer_one_hot():
 
 def test_mlp_forward_matches_torch_linear_stack():
     """The flat order is PyTorch's parameter order of Linear-Tanh-Linear-Tanh-Linear
-    (weight [out][in], then bias, per layer)."""
+    (weight [out][in], then bias, per layer). torch is imported here, not at
+    module level: collecting this file for a device run would otherwise load
+    torch's bundled HIP runtime and hiprtc (same sonames as the system ROCm's)
+    before the library, and its kernels would be compiled by that hiprtc."""
+    import torch
     torch.manual_seed(0)
     n_in, n_h, n_out = 7, 11, 3
     net = torch.nn.Sequential(torch.nn.Linear(n_in, n_h), torch.nn.Tanh(), torch.nn.Linear(n_h, n_h), torch.nn.Tanh(),
