@@ -1,9 +1,9 @@
 """HIP step kernel against the f64 oracle, through the C ABI (BatchSim).
 
 Per-step parity follows the reference's GPU-vs-CPU suites
-(crates/phyz-gpu/tests/cuda_vs_cpu.rs:183-397) with the tolerances of the
-north star: qdd normwise relative error <= 1e-10 per step on the f64 kernels,
-<= 1e-4 on the f32 kernels. Inputs are the workloads' seeded states, plus
+(crates/phyz-gpu/tests/cuda_vs_cpu.rs:183-397), held to qdd normwise
+relative error <= 1e-10 per step on the f64 kernels and <= 1e-4 on the f32
+kernels. Inputs are the workloads' seeded states, plus
 states taken from an oracle rollout so that contact, PD saturation and fast
 joints are exercised.
 """
