@@ -711,7 +711,13 @@ bool choose_tile(phz_train* t, size_t lds_limit, std::string& e) {
     return worst * sizeof(float);
   };
   uint32_t only = 0;
-  if (const char* env = std::getenv("PHZ_TRAIN_TILE_ROWS")) only = (uint32_t)std::atoi(env);
+  if (const char* env = std::getenv("PHZ_TRAIN_TILE_ROWS")) {
+    only = (uint32_t)std::atoi(env);
+    if (only != 8 && only != 16 && only != 32 && only != 64) {
+      e = fmt("PHZ_TRAIN_TILE_ROWS must be 8, 16, 32 or 64, not '%s'", env);
+      return false;
+    }
+  }
   struct Option { uint32_t R; int mode; };
   const Option options[] = {{32, STAGE_ALL},  {16, STAGE_ALL},   {64, STAGE_ALL},  {32, STAGE_LAYER},
                             {16, STAGE_LAYER}, {64, STAGE_LAYER}, {32, STAGE_NONE}, {16, STAGE_NONE},
@@ -725,7 +731,8 @@ bool choose_tile(phz_train* t, size_t lds_limit, std::string& e) {
       return true;
     }
   }
-  e = fmt("networks too wide for one tile: 8 rows need %zu bytes of LDS, the device has %zu", bytes(8, STAGE_NONE),
+  const uint32_t R = only ? only : 8;
+  e = fmt("networks too wide for one tile: %u rows need %zu bytes of LDS, the device has %zu", R, bytes(R, STAGE_NONE),
           lds_limit);
   return false;
 }
