@@ -492,7 +492,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's rollout length)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: one timed span)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: five timed spans)")
     ap.add_argument("--workload", type=int, default=2)
     ap.add_argument("--reps", type=int, default=7)
     ap.add_argument("--no-cpu", action="store_true")
@@ -535,7 +535,10 @@ def main():
     if args.steps is None:
         args.steps = w.nsteps
     if args.warmup is None:
-        args.warmup = args.steps
+        # Five spans: a freshly idle MI355X takes about five chain7 launches
+        # (~20 ms) to reach its steady clocks (rocprof: 4.9, 4.7, 3.5, 3.5,
+        # 3.4, then 3.2-3.3 ms per 1000-step launch).
+        args.warmup = 5 * args.steps
     precs = [args.precision] if args.precision else list(w.precisions)
     r = measure(w, precs, args.steps, args.warmup, args.reps, not args.no_cpu)
     primary = r["primary"]
