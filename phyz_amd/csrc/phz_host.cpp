@@ -293,7 +293,8 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   // world-steps/s, 4 waves 2.00e9; hand, 16384 worlds: 4 waves 2.02e9 f32 /
   // 1.35e9 f64, 5 waves 1.93e9 / 1.05e9; ModelBuilder humanoid with balanced
   // limbs: 4 waves 3.05e9, 2 waves 2.83e9; welded-palm hand without a
-  // barrier: 5 waves 5.12e9 f64, 4 waves 4.35e9). PHZ_MAX_GROUPS forces a cap.
+  // barrier: 5 waves 5.12e9 f64, 4 waves 4.35e9). PHZ_MAX_GROUPS forces a cap
+  // (rounded down to 1, 2, 4 or 8).
   int ntrunk = 0;
   for (int i = 0; i < nb; i++) ntrunk += trunk[i];
   const long t0 = mode == 2 ? ntrunk : 0;
@@ -332,7 +333,11 @@ Plan plan_partition(const ModelD& m, const Features& f) {
     return *std::max_element(load, load + 4);
   };
   if (const char* e = std::getenv("PHZ_MAX_GROUPS")) {
-    parts = pack(std::max(1, std::min(8, std::atoi(e))));
+    // Rounded down to 1, 2, 4 or 8, the caps the planner itself tries (a
+    // 3-wave f64 humanoid kernel gave launch-varying values; see the skipped
+    // case of test_mjcf_merged_groups_match).
+    const int want = std::atoi(e);
+    parts = pack(want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1);
   } else {
     std::vector<std::vector<int>> best;
     long best_load = -1;

@@ -185,7 +185,8 @@ def test_mjcf_hand_partitioned_equals_lane_per_world():
 THREE_WAVE_F64 = ("the humanoid's 3-wave f64 kernel with control noise (512 VGPR+AGPR, 364 B scratch) "
                   "returned launch-varying values of order 1e67 from the first step, while the same plan "
                   "without noise equals the one-lane-per-world kernel over 50 steps; no cause found in the "
-                  "source, so launches never get this plan (the planner picks among caps 8, 4 and 2)")
+                  "source, so launches never get this plan (the planner picks among caps 8, 4 and 2, and "
+                  "PHZ_MAX_GROUPS rounds down to 1, 2, 4 or 8)")
 
 
 @pytest.mark.parametrize("name,groups", [("shadow_hand", 4), ("shadow_hand", 2), ("humanoid", 2),
