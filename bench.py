@@ -338,6 +338,15 @@ def ppo_flops(b, nets):
     return f
 
 
+def ppo_traffic():
+    """HBM bytes per tile-kernel launch from the committed FETCH_SIZE / WRITE_SIZE
+    counters (profiles/ppo_update_kernel_stats.txt), or None."""
+    if not os.path.exists(TRAFFIC_JSON):
+        return None
+    entry = json.load(open(TRAFFIC_JSON)).get("ppo_tiles")
+    return entry["hbm_bytes_per_launch"] if entry else None
+
+
 def run_ppo_update(reps: int, with_cpu: bool):
     """The PPO update pass (phyz_amd.train) at the reference's timing shape:
     wall time per update with the batch resident, and the tile kernel's
@@ -385,7 +394,7 @@ def run_ppo_update(reps: int, with_cpu: bool):
         "roofline": {"bound": "valu", "kernel": "ppo_tiles",
                      "achieved": round(flops / (tiles_ms / 1e3) / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(flops / (tiles_ms / 1e3) / 1e12 / 157.3, 4), "flops_per_update": flops,
-                     "launch_ms": round(tiles_ms / nmb, 5), "traffic": None},
+                     "launch_ms": round(tiles_ms / nmb, 5), "traffic": ppo_traffic()},
         "reference_published": {**PPO_REFERENCE_S, "speedup_vs_published_device": round(PPO_REFERENCE_S["device"] / med, 1)},
     }
     log(f"[bench] ppo update: {med * 1e3:.3f} ms per update ({out['ms_per_minibatch'] * 1e3:.1f} us per minibatch), "
