@@ -29,3 +29,44 @@ def test_waves_per_world_group(index, nworld, prec, block):
     s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
     s.compile()
     assert s.kernel_info()["block"] == block
+
+
+def _three_limb_model(base_joint: str, links: int):
+    """A root with three limbs of `links` revolute links each: the planner sees
+    exactly three parts below the trunk."""
+    import numpy as np
+    from phyz_amd.model import FIXED, FREE, Joint, ModelBuilder, SpatialInertia, SpatialTransform
+
+    b = ModelBuilder().gravity([0.0, 0.0, -9.81]).dt(0.001)
+    jt = FREE if base_joint == "free" else FIXED
+    b.add_body("root", -1, Joint(jt, SpatialTransform.identity(), np.zeros(3)),
+               SpatialInertia.new(1.0, [0.0, 0.0, 0.0], np.eye(3) * 0.01))
+    for limb in range(3):
+        parent = 0
+        for k in range(links):
+            ptj = SpatialTransform.from_translation([0.1, 0.05 * (limb - 1), 0.0] if k == 0 else [0.2, 0.0, 0.0])
+            idx = len(b._bodies)
+            b.add_revolute_body(f"l{limb}_{k}", parent, ptj,
+                                SpatialInertia.new(0.5, [0.1, 0.0, 0.0], np.diag([1e-3, 2e-3, 2e-3])),
+                                axis=(0.0, 1.0, 0.0) if k % 2 else (0.0, 0.0, 1.0))
+            parent = idx
+    return b.build()
+
+
+@pytest.mark.parametrize("base,links", [("fixed", 2), ("fixed", 6), ("free", 5)])
+@pytest.mark.parametrize("nworld", [64, 65536])
+@pytest.mark.parametrize("max_groups", [None, "4", "8"])
+def test_no_three_wave_plan(base, links, nworld, max_groups, monkeypatch):
+    """A tree with exactly three subtrees below its trunk (a welded base, any
+    size; a floating base with 14 or more bodies) is never given a 3-wave
+    (192-thread) kernel, whatever the planner's cap or PHZ_MAX_GROUPS."""
+    from phyz_amd.sim import BatchSim
+
+    if max_groups is None:
+        monkeypatch.delenv("PHZ_MAX_GROUPS", raising=False)
+    else:
+        monkeypatch.setenv("PHZ_MAX_GROUPS", max_groups)
+    m = _three_limb_model(base, links)
+    s = BatchSim(m, nworld, "f64", device=-1)
+    s.compile()
+    assert s.kernel_info()["block"] in (64, 128), s.kernel_info()
