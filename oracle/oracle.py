@@ -303,3 +303,60 @@ class ContactCfg:
             heights = np.ascontiguousarray(np.asarray(hh, dtype=np.float64).ravel())
         L.orc_set_contact_cfg(h, self.solve_mode, self.sweeps, _d(self.prm), pb, _d(pl), int(nx), int(ny), _d(hf),
                               _d(heights))
+
+
+# ── chaos classification (crates/phyz/src/determinism.rs:164-382) ───────────
+def ulp_offset(x: float, n: int) -> float:
+    """x moved n representable f64 steps toward +inf (n < 0: toward -inf), on
+    the sign-magnitude total order; NaN and infinities unchanged
+    (determinism.rs:180-224)."""
+    x = float(x)
+    if n == 0 or not np.isfinite(x):
+        return x
+    bits = int(np.array(x, dtype=np.float64).view(np.int64))
+    key = bits if bits >= 0 else -(1 << 63) - bits
+    lo, hi = -0x7FEFFFFFFFFFFFFF, 0x7FEFFFFFFFFFFFFF  # -f64::MAX, f64::MAX on the ordered line
+    key = min(max(key + int(n), lo), hi)
+    bits = key if key >= 0 else -(1 << 63) - key
+    return float(np.array(bits, dtype=np.int64).view(np.float64))
+
+
+def ulps_between(a: float, b: float) -> int:
+    """Representable f64 steps from a to b (determinism.rs:201-207); i64::MAX
+    when either is not finite."""
+    if not (np.isfinite(a) and np.isfinite(b)):
+        return (1 << 63) - 1
+
+    def key(x):
+        bits = int(np.array(float(x), dtype=np.float64).view(np.int64))
+        return bits if bits >= 0 else -(1 << 63) - bits
+    return max(min(key(b) - key(a), (1 << 63) - 1), -(1 << 63))
+
+
+def state_distance(q0, v0, q1, v1) -> np.ndarray:
+    """Per-world Euclidean distance over the stacked (q, v) vector; inf for a
+    world where either state is not finite (determinism.rs:235-253)."""
+    d = np.concatenate([np.asarray(q0) - np.asarray(q1), np.asarray(v0) - np.asarray(v1)], axis=-1)
+    out = np.sqrt(np.sum(d * d, axis=-1))
+    return np.where(np.isfinite(d).all(axis=-1), out, np.inf)
+
+
+def one_ulp_divergence(orc: "Oracle", q, v, ctrl, nsteps: int, q_index=None, targets=None, ulps: int = 1,
+                       threads: int = 8):
+    """Two oracle rollouts of every world, nsteps each: one from (q, v), one
+    with q[:, q_index] moved `ulps` representable steps (determinism.rs:333-382,
+    per world, both rollouts replaying the same control stream). q_index None
+    moves every coordinate of q, so no symmetry direction of the model (a
+    hinge about the gravity axis) can hide a growing one. Returns (initial
+    distance, final distance, final q, final v of the unperturbed rollout),
+    one entry per world."""
+    qa, va, ca = (np.array(a, dtype=np.float64, order="C") for a in (q, v, ctrl))
+    qb, vb, cb = qa.copy(), va.copy(), ca.copy()
+    cols = range(qb.shape[1]) if q_index is None else [q_index]
+    for j in cols:
+        qb[:, j] = [ulp_offset(x, ulps) for x in qb[:, j]]
+    d0 = state_distance(qa, va, qb, vb)
+    n = qa.shape[0]
+    orc.step_batch(qa, va, ca, nsteps, targets=targets, rng=orc.rng_states(n), threads=threads)
+    orc.step_batch(qb, vb, cb, nsteps, targets=targets, rng=orc.rng_states(n), threads=threads)
+    return d0, state_distance(qa, va, qb, vb), qa, va
