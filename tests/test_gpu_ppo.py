@@ -15,7 +15,7 @@ import os
 import numpy as np
 import pytest
 
-from oracle.ppo_ref import CpuPpo, Dims, RefHostPipeline, init_flat, policy_logp, ref_available
+from oracle.ppo_ref import CpuPpo, Dims, init_flat, policy_logp
 from phyz_amd.train import (AdamCfg, KlMode, NetDims, PpoUpdateCfg, SampleBatch, TrainError, TrainPipeline)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ppo_ref_vectors.npz")
@@ -148,8 +148,8 @@ def test_shapes_against_the_f64_cpu_update(a_in, c_in, h, act, n, mb):
     that nearly cancels), and the reference's own kernels exceed 2e-4 on two of
     these three (4e-4 and 3.8e-3). So the check is on the distribution: the
     median, p99 and p99.9 of the per-parameter gaps, where the reference's
-    kernels sit at <= 2.2e-7, 2.1e-6 and 6.4e-6 on these shapes, and, where
-    oracle/_ref is present, the device's p99 against the reference kernels'."""
+    kernels sit at <= 2.2e-7, 2.1e-6 and 6.4e-6 on these shapes (measured on
+    their host build, which stays off the GPU box)."""
     ad, cd = Dims(a_in, h, act), Dims(c_in, h, 1)
     a0, c0 = init_flat(11, ad, act, -0.5), init_flat(12, cd)
     batch = synthetic(n, ad, c_in, 3, a0)
@@ -165,21 +165,12 @@ def test_shapes_against_the_f64_cpu_update(a_in, c_in, h, act, n, mb):
                    act, 1)
     assert s.grad_steps == w.grad_steps == math.ceil(n / mb)
     assert rel(s.policy_loss, w.policy_loss) < 1e-4 and rel(s.value_loss, w.value_loss) < 1e-4
-    ref = None
-    if ref_available():
-        ref = RefHostPipeline(ad, cd, a0, c0, mb)
-        ref.update(batch, order, 0.2, 0.003, 6.0, mb, 1, math.inf, act, 1)
-    for net, x0, xc, xd, xr in (("actor", a0, cpu.actor, pipe.actor_params(), ref and ref.actor_params()),
-                                ("critic", c0, cpu.critic, pipe.critic_params(), ref and ref.critic_params())):
+    for net, x0, xc, xd in (("actor", a0, cpu.actor, pipe.actor_params()),
+                            ("critic", c0, cpu.critic, pipe.critic_params())):
         e = delta_errors(x0, xc, xd)
         q = [np.median(e), np.percentile(e, 99), np.percentile(e, 99.9)]
-        line = (f"{a_in}/{c_in}-{h}-{act} n {n} mb {mb} (tile rows {pipe.rows_per_tile}) {net}: gap median {q[0]:.2e} "
-                f"p99 {q[1]:.2e} p99.9 {q[2]:.2e} max {e.max():.2e}")
-        if xr is not None:
-            er = delta_errors(x0, xc, xr)
-            line += f"; reference kernels p99 {np.percentile(er, 99):.2e} max {er.max():.2e}"
-            assert q[1] <= 2.0 * np.percentile(er, 99) + 1e-7
-        print(line, flush=True)
+        print(f"{a_in}/{c_in}-{h}-{act} n {n} mb {mb} (tile rows {pipe.rows_per_tile}) {net}: gap median {q[0]:.2e} "
+              f"p99 {q[1]:.2e} p99.9 {q[2]:.2e} max {e.max():.2e}", flush=True)
         assert q[0] < 1e-6 and q[1] < 1e-5 and q[2] < 5e-5
 
 
