@@ -15,7 +15,6 @@ the force range, the gated limit damping and the tanh friction.
 """
 import math
 import os
-import struct
 
 import numpy as np
 import pytest
@@ -23,7 +22,7 @@ import pytest
 from oracle.oracle import Oracle
 from phyz_amd import workloads as W
 from phyz_amd.mjcf import MjcfError, MjcfLoader, quat_to_matrix, shape_principal_inertia, shape_volume
-from phyz_amd.model import (FIXED, FREE, G_CAPSULE, G_MESH, G_SPHERE, REVOLUTE, pack_actuators, pack_bodies,
+from phyz_amd.model import (FIXED, FREE, G_CAPSULE, G_SPHERE, REVOLUTE, pack_actuators, pack_bodies,
                             pack_geometries, pack_joint_terms)
 
 REF_MODELS = "/root/reference/models"
@@ -157,6 +156,19 @@ def test_capsule_inertia_against_voxel_integration():
     np.testing.assert_allclose(shape_principal_inertia("capsule", [r, 0.0], 1.0), s, rtol=1e-14)
 
 
+@pytest.mark.parametrize("r,h", [(0.08, 0.28), (0.046, 0.0), (0.5, 0.01), (0.01, 3.0)])
+def test_capsule_inertia_is_cylinder_plus_two_hemispheres(r, h):
+    """The textbook composition: a cylinder of length 2h plus two solid
+    hemispheres, each with 83/320 m r^2 about its own centroid, which sits 3r/8
+    beyond the shaft's end (parallel-axis theorem), at one density."""
+    rho = 1.0 / shape_volume("capsule", [r, h])
+    mc, ms = rho * math.pi * r * r * 2 * h, rho * 2 / 3 * math.pi * r ** 3
+    assert mc + 2 * ms == pytest.approx(1.0, rel=1e-14)
+    izz = mc * r * r / 2 + 2 * (2 / 5) * ms * r * r
+    ixx = mc * (3 * r * r + (2 * h) ** 2) / 12 + 2 * (83 / 320 * ms * r * r + ms * (h + 3 * r / 8) ** 2)
+    np.testing.assert_allclose(shape_principal_inertia("capsule", [r, h], 1.0), [ixx, ixx, izz], rtol=1e-13)
+
+
 def test_box_and_cylinder_inertia_closed_forms():
     np.testing.assert_allclose(shape_principal_inertia("box", [0.1, 0.2, 0.3], 6.0),
                                [6 / 12 * (0.4 ** 2 + 0.6 ** 2), 6 / 12 * (0.2 ** 2 + 0.6 ** 2), 6 / 12 * (0.2 ** 2 + 0.4 ** 2)])
@@ -236,7 +248,7 @@ def test_euler_sequences_intrinsic_and_extrinsic():
         np.testing.assert_allclose(load(xml).build_model().bodies[0].joint.parent_to_joint.rot, want, atol=1e-12)
 
 
-@pytest.mark.parametrize("attr,msg", [('euler="1 2"', "expected 3 numbers"), ('quat="0 0 0 0"', "zero norm"),
+@pytest.mark.parametrize("attr,msg", [('euler="1 2"', "needs 3 numbers"), ('quat="0 0 0 0"', "zero norm"),
                                       ('axisangle="0 0 0 1"', "zero vector"), ('xyaxes="1 0 0 2 0 0"', "parallel")])
 def test_degenerate_orientations_are_errors(attr, msg):
     with pytest.raises(MjcfError) as e:
@@ -301,46 +313,19 @@ def test_unsupported_features_are_reported():
     assert tags == {"hfield", "joint", "tendon", "equality"}
 
 
-def test_includes_splice_defaults_and_bodies(tmp_path):
-    (tmp_path / "child.xml").write_text("""<mujoco><default><joint damping="3.25"/></default>
-        <worldbody><body name="included_child"><joint/></body></worldbody></mujoco>""")
-    (tmp_path / "main.xml").write_text("""<mujoco><include file="child.xml"/>
-        <worldbody><body name="own"><joint/></body></worldbody></mujoco>""")
-    m = MjcfLoader.from_file(str(tmp_path / "main.xml")).build_model()
-    assert {b.name for b in m.bodies} == {"included_child", "own"}
-    assert all(b.joint.damping == 3.25 for b in m.bodies)
-    (tmp_path / "a.xml").write_text('<mujoco><include file="b.xml"/></mujoco>')
-    (tmp_path / "b.xml").write_text('<mujoco><include file="a.xml"/></mujoco>')
-    with pytest.raises(MjcfError, match="cyclic"):
-        MjcfLoader.from_file(str(tmp_path / "a.xml"))
-    with pytest.raises(MjcfError, match="does_not_exist.xml"):
-        MjcfLoader.from_xml_str('<mujoco><include file="does_not_exist.xml"/></mujoco>')
-    with pytest.raises(MjcfError, match="missing required attribute 'file'"):
-        MjcfLoader.from_xml_str("<mujoco><include/></mujoco>")
-
-
-def test_mesh_assets_obj_and_binary_stl(tmp_path):
-    tet = np.array([[0, 0, 0], [1, 0, 0], [0, 1, 0], [0, 0, 1]], dtype=float)
-    faces = [(0, 2, 1), (0, 1, 3), (0, 3, 2), (1, 2, 3)]
-    (tmp_path / "t.obj").write_text("".join(f"v {a} {b} {c}\n" for a, b, c in tet) +
-                                    "".join(f"f {a + 1} {b + 1} {c + 1}\n" for a, b, c in faces))
-    with open(tmp_path / "t.stl", "wb") as f:
-        f.write(b"\0" * 80 + struct.pack("<I", 4))
-        for tri in faces:
-            f.write(struct.pack("<3f", 0, 0, 0) + b"".join(struct.pack("<3f", *tet[k] * 2) for k in tri) + b"\0\0")
-    (tmp_path / "m.xml").write_text("""<mujoco><asset><mesh file="t.obj"/><mesh name="s" file="t.stl"/>
-        <mesh name="gone" file="missing.stl"/></asset>
-        <worldbody><body><joint/><geom type="mesh" mesh="t"/></body><body><joint/><geom type="mesh" mesh="s"/></body>
-        <body><joint/><geom type="mesh" mesh="gone"/><geom type="sphere" size="0.1"/></body></worldbody></mujoco>""")
-    L = MjcfLoader.from_file(str(tmp_path / "m.xml"))
-    ms = {m.name: m for m in L.meshes()}
-    assert ms["t"].vertices.shape == (4, 3) and ms["t"].faces.shape == (4, 3)
-    assert ms["s"].vertices.shape == (12, 3) and ms["gone"].load_error is not None
+def test_includes_and_meshes_are_reported_and_skipped():
+    """<include>, mesh assets and mesh geoms are outside this loader: each is
+    reported, and the rest of the model still loads (the unloadable mesh geom
+    gives its body no shape and no mass)."""
+    xml = """<mujoco><include file="other.xml"/><asset><mesh name="m" file="m.stl"/></asset>
+        <worldbody><body><joint/><geom type="mesh" mesh="m"/><geom type="sphere" size="0.1"/></body>
+        <body><joint/><geom mesh="m"/></body></worldbody></mujoco>"""
+    L = load(xml)
+    assert {u.tag for u in L.unsupported()} == {"include", "mesh", "geom"}
     m = L.build_model()
-    assert m.bodies[0].geometry.kind == G_MESH and m.bodies[0].geometry.params == (0, 0, 0, 1, 1, 1)
-    assert m.bodies[1].geometry.params == (0, 0, 0, 2, 2, 2)
-    assert m.bodies[2].geometry.kind == G_SPHERE  # the unloadable mesh geom is dropped
-    assert {u.tag for u in L.unsupported()} == {"mesh", "geom"}
+    assert m.bodies[0].geometry.kind == G_SPHERE and len(m.bodies[0].collisions) == 1
+    assert m.bodies[0].inertia.mass == pytest.approx(1000 * 4 / 3 * math.pi * 1e-3)
+    assert m.bodies[1].geometry is None and m.bodies[1].inertia.mass == 1.0
 
 
 # ── force terms in the oracle ───────────────────────────────────────────────
