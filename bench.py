@@ -3,22 +3,34 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2] [--no-cpu]
 
 A "step" is one physics step (control noise, PD, contact, ABA, integrate) of
-every world of the workload. The default workload is the 7-link chain, 65536
-worlds, f32 and f64 (the f32 run is the headline `value`; the f64 run is
-reported under "f64"). W warmup steps run untimed, then exactly K steps are
-timed with the device synchronized on both sides; the kernel's own time comes
-from hipEvents recorded on the sim's stream around the same span. State stays
-resident in HBM for the whole measurement.
+every world of the workload. The headline `value` is the 7-link chain, 65536
+worlds, f32: W warmup steps run untimed, then spans of exactly K steps are
+timed by the host clock with the device synchronized on both sides (the median
+of --reps spans, each from the workload's seeded initial state, reloaded
+untimed); the kernel's own time comes from hipEvents recorded on the sim's
+stream around the same spans. Before the warmup the device runs the same span
+untimed for --settle-ms, so a short span is not timed at the idle clock. State
+stays resident in HBM for the whole measurement.
+
+configs (unless --no-configs): every benchmark configuration (the double
+pendulum, chain7, ant, humanoid and hand) at its own worlds x rollout length,
+in each precision it names, each with its roofline, its CPU baseline and the
+device's parity at the rollout's late state.
 
 roofline: algorithmic FLOPs per launch (tests/golden/flops_per_world_step.json,
 counted on the oracle's structure-exploiting formulation x worlds x steps per
 launch) over the event-timed launch duration, against MI355X's vector peak
-(FP64 78.6 TFLOP/s; FP32 157.3 TFLOP/s published). `traffic` is read from the
-committed rocprofv3 --pmc summary when one matches the workload.
+(FP64 78.6 TFLOP/s; FP32 157.3 TFLOP/s published). `traffic` is the kernel's
+measured HBM bytes per launch (profiles/hbm_traffic.json, rocprofv3 --pmc
+FETCH_SIZE and WRITE_SIZE scaled by a plain copy's readings): one state round
+trip per launch, whatever its step count.
 
-cpu_baseline: the f64 CPU oracle (a port of the reference's CPU step), threaded
-over worlds on the host cores, timed on a bounded sample of the same workload;
-it also checks one device step of the sampled worlds against the oracle.
+cpu_baseline: the f64 CPU oracle (a restatement of the reference's CPU step),
+threaded over worlds on the host's cores (the CPUs this process may use,
+capped by the cgroup quota), timed on a bounded sample of the same workload.
+parity: one more device step from the timed rollout's late state against the
+oracle on 64 sampled worlds, with the bound (qdd normwise relative error 1e-10
+f64, 1e-4 f32), pass or fail, and the share of worlds within it.
 
 terrain_impulse (unless --no-impulse): the same measurement of workload 6, the
 ant on a rolling heightfield with impulse-mode contact (16 sweeps per step),
@@ -58,42 +70,100 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def run_gpu(w, prec, steps, warmup, reps):
+def host_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on, capped by
+    the cgroup's CPU quota where one is set. Returns (threads, details)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(period))
+    except (OSError, ValueError):
+        pass
+    threads = min(aff, quota) if quota else aff
+    return threads, {"os_cpu_count": os.cpu_count(), "affinity_cpus": aff, "cgroup_quota_cpus": quota}
+
+
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def run_gpu(w, prec, steps, warmup, reps, settle_ms=0.0):
+    """W = warmup untimed steps (whole spans of the timed length), then `reps`
+    wall-clock spans of exactly `steps` steps, each from the workload's seeded
+    initial state (reloaded untimed) and bracketed by a device synchronization
+    on both sides, plus the same number of spans timed by hipEvents on the
+    sim's stream. settle_ms: untimed spans run first until the device has been
+    busy that long, so that a short timed span does not run at the idle clock."""
     from phyz_amd.sim import from_workload
     sim = from_workload(w, prec, nworld=w.nworld, device=0)
     q, v, c, tg = w.initial_state()
-    sim.load_states(q, v, c)
-    if tg is not None:
-        sim.set_position_targets(tg)
-    sim.compile()
-    # Warm up with whole spans of the timed length so the timed span replays a
-    # captured graph.
-    span = steps
-    done = 0
-    while done < warmup:
-        sim.step_many(span)
-        done += span
-    # Every timed span is the workload's own rollout from its seeded initial
-    # state (reloaded untimed), so the state stays on the configured horizon.
-    sim.load_states(q, v, c)
-    sim.synchronize()
-    t0 = time.perf_counter()
-    sim.step_many(steps)
-    sim.synchronize()
-    wall = time.perf_counter() - t0
-    ev = []
-    for _ in range(reps):  # hipEvents on the sim's stream around each span
+
+    def reload():
         sim.load_states(q, v, c)
+        if tg is not None:
+            sim.set_position_targets(tg)
+
+    reload()
+    sim.compile()
+    settle = {"spans": 0, "ms": 0.0}
+    if settle_ms > 0:
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < settle_ms:
+            sim.step_many(steps)
+            sim.synchronize()
+            settle["spans"] += 1
+        settle["ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        reload()
+    done = 0
+    while done < warmup:  # captures the span's graph, so the timed spans replay it
+        sim.step_many(steps)
+        done += steps
+    walls = []
+    for _ in range(reps):
+        reload()
+        sim.synchronize()
+        t0 = time.perf_counter()
+        sim.step_many(steps)
+        sim.synchronize()
+        walls.append(time.perf_counter() - t0)
+    ev = []
+    for _ in range(reps):
+        reload()
         ev.extend(sim.time_step_many(steps, 1))
-    sim.load_states(q, v, c)
+    reload()
     sim.step_many(steps)
     info = sim.kernel_info()
-    return sim, wall, np.array(ev), info, done
+    return sim, np.array(walls), np.array(ev), info, done, settle
 
 
 def launches_per_span(steps, info):
     per = max(1, int(info["max_steps_per_launch"]))
     return (steps + per - 1) // per
+
+
+def traffic_for(traffic_tab, name, prec, steps_per_launch):
+    """Measured HBM bytes per launch of this kernel. The step kernels load the
+    state once and store it once per launch whatever its step count, so a
+    figure measured at another span length applies; the entry for the exact
+    span is used where one was measured."""
+    if not traffic_tab:
+        return None, None
+    exact = traffic_tab.get(f"{name}_{prec}_{int(steps_per_launch)}")
+    if exact:
+        return exact["hbm_bytes_per_launch"], exact["steps_per_launch"]
+    for k in sorted(traffic_tab):
+        e = traffic_tab[k]
+        if k.startswith(f"{name}_{prec}_") and "steps_per_launch" in e:
+            return e["hbm_bytes_per_launch"], e["steps_per_launch"]
+    return None, None
 
 
 def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
@@ -103,10 +173,7 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
     flops_per_launch = f["flops_per_world_step"] * w.nworld * steps_per_launch
     launch_s = float(np.median(ev_ms)) / 1e3 / nl
     achieved = flops_per_launch / launch_s / 1e12
-    traffic = None
-    key = f"{w.name}_{prec}_{int(steps_per_launch)}"
-    if traffic_tab and key in traffic_tab:
-        traffic = traffic_tab[key]["hbm_bytes_per_launch"]
+    traffic, measured_at = traffic_for(traffic_tab, w.name, prec, steps_per_launch)
     algo_bytes = f["bytes_per_world_step"][prec] * w.nworld  # one state round trip per launch
     return {
         "bound": "valu",
@@ -115,6 +182,8 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_TFLOPS[prec], 5),
         "traffic": traffic,
+        "traffic_measured_steps_per_launch": measured_at,
+        "algorithmic_bytes_per_launch": int(algo_bytes),
         "flops_per_world_step": f["flops_per_world_step"],
         "launch_ms": round(launch_s * 1e3, 4),
         "steps_per_launch": int(steps_per_launch),
@@ -122,48 +191,38 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
     }
 
 
+# Per-step qdd bounds, normwise relative to max|qdd| of the f64 oracle; f32
+# impulse-mode contact is held to 2e-4, the deviation of the reference's own f32
+# contact pass from the f64 law in that mode.
+QDD_BOUND = {"f64": 1e-10, "f32": 1e-4}
+QDD_BOUND_F32_IMPULSE = 2e-4
+
+
 def device_step_parity(w, sim, prec):
     """One more device step from the benchmark's late states against the oracle,
-    on 64 sampled worlds: the device's own noisy torques (read back after the
-    step) drive an oracle without the noise stream; impulse mode also starts
-    from the device's carried contact forces and warm-start impulses."""
-    import dataclasses
-    from tests.helpers import as_precision, oracle_for, rel_err_rows
-    imp = w.impulse_sweeps > 0
+    on 64 sampled finite worlds (tests.helpers.late_step_errors). Reports the
+    largest error, the bound, pass or fail, and the share of worlds within the
+    bound."""
+    from tests.helpers import late_step_errors
     qg, vg = sim.readback_states()
     finite = np.flatnonzero(np.isfinite(qg).all(axis=1) & np.isfinite(vg).all(axis=1))
+    if finite.size == 0:
+        return {"worlds_checked": 0, "pass": False, "note": "no finite world left after the timed spans"}
     idx = finite[np.linspace(0, len(finite) - 1, 64).astype(int)]
-    if imp:
-        cs0, ext0 = sim.readback_contact_state()
-        cs0, ext0 = np.ascontiguousarray(cs0[idx]), np.ascontiguousarray(ext0[idx])
-    sim.step()
-    ctrl = as_precision(sim.readback_controls(), prec)
-    qdd = sim.readback_qdd()
-    if not imp and w.heightfield is None:
-        orc = oracle_for(w)
-        ext = [orc.contact(qg[k], vg[k])[0] if w.contact is not None else None for k in idx]
-        want = np.stack([orc.aba(qg[k], vg[k], ctrl[k], ext[i]) for i, k in enumerate(idx)])
-        return {"worlds_checked": len(idx), "qdd_rel_err_max": float(rel_err_rows(qdd[idx], want).max())}
-    orc = oracle_for(dataclasses.replace(w, noise=None))
-    q, v, c = (np.ascontiguousarray(a[idx]) for a in (qg, vg, ctrl))
-    want, _ = orc.step_batch(q, v, c, 1, threads=8, ext_state=ext0 if imp else None, cs_state=cs0 if imp else None)
-    out = {"worlds_checked": len(idx), "qdd_rel_err_max": float(rel_err_rows(qdd[idx], want).max())}
-    if imp:
-        cs1, ext1 = sim.readback_contact_state()
-        es = max(float(np.abs(ext0).max()), 1.0)
-        out["contact_force_rel_err_max"] = float(np.abs(ext1[idx] - ext0).max() / es)
-        isc = max(float(np.abs(cs0[:, :, 8:]).max()), 1e-6)
-        out["impulse_rel_err_max"] = float(np.abs(cs1[idx, :, 8:] - cs0[:, :, 8:]).max() / isc)
-    return out
+    e, extra = late_step_errors(w, sim, prec, idx)
+    bound = QDD_BOUND_F32_IMPULSE if prec == "f32" and w.impulse_sweeps > 0 else QDD_BOUND[prec]
+    return {"worlds_checked": len(idx), "qdd_rel_err_max": float(e.max()), "qdd_rel_err_median": float(np.median(e)),
+            "bound": bound, "pass": bool(e.max() <= bound), "share_within_bound": round(float(np.mean(e <= bound)), 4),
+            **extra}
 
 
-def cpu_baseline(w, sim, prec, budget_s=20.0):
-    """budget_s: seconds of multi-threaded oracle time for the timed sample."""
-    """Oracle (f64 port of the reference CPU step) on the host cores, on a bounded
-    sample of the workload; plus a one-step parity check of the sampled worlds."""
+def cpu_baseline(w, budget_s=8.0):
+    """The f64 oracle (a restatement of the reference's CPU step) threaded over
+    worlds on the host's cores, on a bounded sample of the same workload (its
+    seeded initial states, replayed control stream): `budget_s` seconds of
+    multi-threaded work, plus a single-thread rate on a smaller sample."""
     from tests.helpers import oracle_for
-    threads = max(1, min(16, os.cpu_count() or 1))
-    parity = device_step_parity(w, sim, prec)
+    threads, host = host_threads()
     orc = oracle_for(w)
     imp = w.impulse_sweeps > 0
     nb = w.model.nbodies
@@ -171,46 +230,75 @@ def cpu_baseline(w, sim, prec, budget_s=20.0):
     def carried(n):
         return (np.zeros((n, nb, 6)), np.zeros((n, nb, 56))) if imp else (None, None)
 
-    # Timing: the same workload's initial states, n worlds x s steps within the budget.
-    n = min(w.nworld, 4096)
-    q, v, c, tg = w.initial_state(n)
-    rng = orc.rng_states(n)
-    e, cs = carried(n)
-    t0 = time.perf_counter()
-    orc.step_batch(q, v, c, 2, targets=tg, rng=rng, threads=threads, ext_state=e, cs_state=cs)
-    probe = time.perf_counter() - t0
-    rate = 2 * n / max(probe, 1e-6)
-    s = max(2, int(budget_s * rate / n))
-    q, v, c, tg = w.initial_state(n)
-    rng = orc.rng_states(n)
-    e, cs = carried(n)
-    t0 = time.perf_counter()
-    orc.step_batch(q, v, c, s, targets=tg, rng=rng, threads=threads, ext_state=e, cs_state=cs)
-    dt = time.perf_counter() - t0
+    def run(n, steps, nthreads):
+        q, v, c, tg = w.initial_state(n)
+        e, cs = carried(n)
+        t0 = time.perf_counter()
+        orc.step_batch(q, v, c, steps, targets=tg, rng=orc.rng_states(n), threads=nthreads, ext_state=e, cs_state=cs)
+        return time.perf_counter() - t0
+
+    n = min(w.nworld, max(1024, 256 * threads))
+    probe = run(n, 2, threads)
+    s = max(2, int(budget_s * 2 / max(probe, 1e-6)))
+    dt = run(n, s, threads)
     n1 = min(n, 256)
-    q1, v1, c1, tg1 = w.initial_state(n1)
-    e, cs = carried(n1)
-    t1 = time.perf_counter()
-    orc.step_batch(q1, v1, c1, max(2, s // 16), targets=tg1, rng=orc.rng_states(n1), threads=1, ext_state=e,
-                   cs_state=cs)
-    dt1 = time.perf_counter() - t1
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    s1 = max(2, int(0.1 * budget_s * n * s / dt / n1 / max(threads, 1)))
+    dt1 = run(n1, s1, 1)
     return {
         "value": round(n * s / dt, 1),
         "unit": "world-steps/s",
         "cores": threads,
         "kind": "port",
         "sample": f"{w.name}: first {n} worlds x {s} steps, f64 oracle, {threads} threads ({dt:.1f} s)",
-        "single_thread_value": round(n1 * max(2, s // 16) / dt1, 1),
-        "cpu": cpu_model,
-    }, parity
+        "single_thread_value": round(n1 * s1 / dt1, 1),
+        "host": {**host, "cpu": cpu_model_name()},
+    }
+
+
+def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=8.0, settle_ms=0.0):
+    """Wall-clock and event-timed spans of `steps` steps per precision, the
+    roofline of the step kernel, the device's parity at the late state, and
+    (with_cpu) the oracle's CPU rate."""
+    flops_tab = json.load(open(FLOPS_JSON))
+    traffic_tab = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else None
+    results = {}
+    for prec in precs:
+        log(f"[bench] {w.name} {prec}: {w.nworld} worlds, warmup {warmup}, timed {steps} steps x {reps}")
+        sim, walls, ev, info, warm_done, settle = run_gpu(w, prec, steps, warmup, reps, settle_ms)
+        wall = float(np.median(walls))
+        med = float(np.median(ev))
+        spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
+        qf, vf = sim.readback_states()
+        finite = float(np.mean(np.isfinite(qf).all(axis=1) & np.isfinite(vf).all(axis=1)))
+        r = {
+            "value": round(w.nworld * steps / wall, 1),
+            "unit": "world-steps/s",
+            "ms_per_step": round(wall * 1e3 / steps, 6),
+            "wall_ms_per_span": {"median": round(wall * 1e3, 4), "min": round(float(walls.min()) * 1e3, 4),
+                                 "max": round(float(walls.max()) * 1e3, 4), "reps": len(walls)},
+            "event_ms_per_span": {"median": round(med, 4), "min": round(float(min(ev)), 4),
+                                  "max": round(float(max(ev)), 4), "reps": len(ev), "noisy": bool(spread > 0.25)},
+            "world_steps_per_s_event_median": round(w.nworld * steps / (med / 1e3), 1),
+            "finite_worlds": round(finite, 4),
+            "roofline": roofline(w, prec, steps, ev, info, flops_tab, traffic_tab),
+            "kernel": info,
+            "warmup_steps_run": warm_done,
+        }
+        if settle["spans"]:
+            r["clock_settle"] = settle
+        if with_cpu:
+            r["parity"] = device_step_parity(w, sim, prec)
+        sim.close()
+        results[prec] = r
+        log(f"[bench] {w.name} {prec}: {r['value']:.4g} world-steps/s, {r['roofline']['achieved']:.3f} TFLOP/s "
+            f"({100 * r['roofline']['frac']:.2f}% of peak)"
+            + (f"; parity qdd {r['parity']['qdd_rel_err_max']:.2e} ({'pass' if r['parity']['pass'] else 'FAIL'})"
+               if with_cpu else ""))
+    cpu = None
+    if with_cpu:
+        log(f"[bench] {w.name}: cpu_baseline")
+        cpu = cpu_baseline(w, cpu_budget_s)
+    return {"results": results, "cpu": cpu}
 
 
 def run_control_loop(prec: str, reps: int, with_cpu: bool):
@@ -296,9 +384,10 @@ def control_parity(cl, sim, q, v):
 
 
 def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
-    """The oracle's rollout (observe + policy per world, then the f64 physics
-    steps) on a bounded sample, single-threaded Python/C++."""
+    """The oracle's rollout (observe + policy per world in Python, then the f64
+    physics steps threaded over worlds) on a bounded sample."""
     from oracle import policy_ref as PR
+    threads, _ = host_threads()
     m = cl.base.model
     q, v, c, _ = cl.base.initial_state(nworld)
     base = cl.base_targets(nworld)
@@ -310,11 +399,12 @@ def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
         for w in range(nworld):
             o = np.array(PR.observe_reference(m, orc, q[w], v[w], cl.spec.obs))
             PR.policy_reference(cl.spec, cl.weights, cl.std, rngs[w], o, zs[w], base[w], tg[w])
-        orc.step_batch(q, v, c, cl.control_every, targets=tg, threads=1)
+        orc.step_batch(q, v, c, cl.control_every, targets=tg, threads=threads)
     dt = time.perf_counter() - t0
-    return {"value": round(nworld * n_control * cl.control_every / dt, 1), "unit": "world-steps/s", "cores": 1,
+    return {"value": round(nworld * n_control * cl.control_every / dt, 1), "unit": "world-steps/s", "cores": threads,
             "kind": "port", "sample": f"{nworld} worlds x {n_control} control steps x {cl.control_every} physics steps, "
-                                      f"f64 oracle (Python observation/policy, C++ physics), {dt:.1f} s",
+                                      f"f64 oracle (observation and policy per world in one Python thread, C++ physics "
+                                      f"on {threads} threads), {dt:.1f} s",
             "control_steps_per_s": round(nworld * n_control / dt, 1)}
 
 
@@ -408,7 +498,7 @@ def run_ppo_update(reps: int, with_cpu: bool):
 
 def ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg, n_mb: int = 128):
     """The f64 CPU update (the oracle's restatement of tang's) on the first
-    n_mb minibatches of the same batch, one BLAS thread, as samples/s; and
+    n_mb minibatches of the same batch, BLAS on the host's cores, as samples/s; and
     the device's update of that sample against it (per-parameter weight-delta
     gaps over the largest delta)."""
     from threadpoolctl import threadpool_limits
@@ -418,7 +508,8 @@ def ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg, n_mb: int = 128):
     cols = {k: getattr(batch, k)[:rows] for k in ("obs_a", "obs_c", "act", "logp_old", "adv", "ret")}
     order = [np.random.default_rng(7).permutation(rows).astype(np.uint32)]
     cpu = CpuPpo(Dims(ad.n_in, ad.n_h, ad.n_out), Dims(cd.n_in, cd.n_h, 1), a0, c0)
-    with threadpool_limits(1):
+    threads, _ = host_threads()
+    with threadpool_limits(threads):
         t0 = time.perf_counter()
         cpu.update({k: v.astype(np.float64) for k, v in cols.items()}, order, cfg.clip, cfg.entropy_coef, cfg.vdelta,
                    cfg.minibatch, 1, cfg.target_kl, cfg.kl_scale, int(cfg.kl_mode))
@@ -433,9 +524,9 @@ def ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg, n_mb: int = 128):
         e = np.abs((xd - x0) - (xc - x0)) / np.abs(xc - x0).max()
         gaps[net] = {"median": float(f"{np.median(e):.3g}"), "p99": float(f"{np.percentile(e, 99):.3g}"),
                      "max": float(f"{e.max():.3g}")}
-    base = {"value": round(rows / dt, 1), "unit": "samples/s", "cores": 1, "kind": "port",
+    base = {"value": round(rows / dt, 1), "unit": "samples/s", "cores": threads, "kind": "port",
             "sample": f"{n_mb} minibatches x {cfg.minibatch} rows, f64 numpy update (tang's arithmetic), "
-                      f"one BLAS thread ({dt:.2f} s)",
+                      f"{threads} BLAS threads ({dt:.2f} s)",
             "seconds_per_update_extrapolated": round(dt * PPO_SHAPE["samples"] / rows, 2)}
     return base, {"rows": rows, "weight_delta_gap": gaps}
 
@@ -453,67 +544,32 @@ def config_of(w, r):
     return c
 
 
-def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=20.0):
-    """Event-timed spans of `steps` steps per precision, the roofline of the step
-    kernel, and (with_cpu) the oracle's CPU rate plus a one-step parity check."""
-    flops_tab = json.load(open(FLOPS_JSON))
-    traffic_tab = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else None
-    primary = "f32" if "f32" in precs else precs[0]
-    results = {}
-    sims = {}
-    for prec in precs:
-        log(f"[bench] {w.name} {prec}: {w.nworld} worlds, warmup {warmup}, timed {steps} steps")
-        sim, wall, ev, info, warm_done = run_gpu(w, prec, steps, warmup, reps)
-        sims[prec] = sim
-        ws = w.nworld * steps / wall
-        med = float(np.median(ev))
-        spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
-        qf, vf = sim.readback_states()
-        finite = float(np.mean(np.isfinite(qf).all(axis=1) & np.isfinite(vf).all(axis=1)))
-        results[prec] = {
-            "value": round(ws, 1),
-            "finite_worlds": round(finite, 4),
-            "ms_per_step": round(wall * 1e3 / steps, 6),
-            "event_ms_per_span": {"median": round(med, 4), "min": round(float(min(ev)), 4),
-                                  "max": round(float(max(ev)), 4), "reps": len(ev), "noisy": bool(spread > 0.25)},
-            "world_steps_per_s_event_median": round(w.nworld * steps / (med / 1e3), 1),
-            "roofline": roofline(w, prec, steps, ev, info, flops_tab, traffic_tab),
-            "kernel": info,
-            "warmup_steps_run": warm_done,
-        }
-        log(f"[bench] {w.name} {prec}: {ws:.4g} world-steps/s, {results[prec]['roofline']['achieved']:.3f} TFLOP/s "
-            f"({100 * results[prec]['roofline']['frac']:.2f}% of peak)")
-    cpu = None
-    parity = {}
-    if with_cpu:
-        for prec in precs:
-            log(f"[bench] {w.name}: cpu_baseline + parity check ({prec})")
-            c, p = cpu_baseline(w, sims[prec], prec, cpu_budget_s)
-            parity[prec] = p
-            if prec == primary:
-                cpu = c
-    for sim in sims.values():
-        sim.close()
-    return {"primary": primary, "results": results, "cpu": cpu, "parity": parity}
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's rollout length)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: five timed spans)")
-    ap.add_argument("--workload", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps of the headline workload (default: its rollout length)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps of the headline workload (default: five timed spans)")
+    ap.add_argument("--workload", type=int, default=2, help="headline workload (default 2: chain7)")
     ap.add_argument("--reps", type=int, default=7)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=60.0,
+                    help="untimed device time before the headline's warmup, so a short timed span runs at "
+                         "steady clocks (0: none)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines and the parity checks")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the measurement of every benchmark configuration at its own rollout length")
     ap.add_argument("--no-control", action="store_true", help="skip the on-device control-loop measurement")
     ap.add_argument("--no-impulse", action="store_true",
                     help="skip the terrain + impulse-contact measurement (workload 6)")
     ap.add_argument("--no-mjcf", action="store_true",
                     help="skip the MJCF-model measurements (workloads 7-9)")
+    ap.add_argument("--only", action="store_true", help="measure the headline workload only (profiling runs)")
     ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
     ap.add_argument("--no-ppo", action="store_true", help="skip the PPO update pass measurement")
     ap.add_argument("--ppo-only", action="store_true", help="measure only the PPO update pass")
-    ap.add_argument("--precision", choices=["f32", "f64"], default=None, help="run one precision only")
+    ap.add_argument("--precision", choices=["f32", "f64"], default=None,
+                    help="headline precision (default: f32 where the workload runs it)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (HBM counter calibration)")
     args = ap.parse_args()
@@ -540,6 +596,7 @@ def main():
         return
 
     from phyz_amd import workloads as W
+    with_cpu = not args.no_cpu
     w = W.config(args.workload)
     if args.steps is None:
         args.steps = w.nsteps
@@ -548,10 +605,11 @@ def main():
         # (~20 ms) to reach its steady clocks (rocprof: 4.9, 4.7, 3.5, 3.5,
         # 3.4, then 3.2-3.3 ms per 1000-step launch).
         args.warmup = 5 * args.steps
-    precs = [args.precision] if args.precision else list(w.precisions)
-    r = measure(w, precs, args.steps, args.warmup, args.reps, not args.no_cpu)
-    primary = r["primary"]
-    p = r["results"][primary]
+    prec = args.precision or ("f32" if "f32" in w.precisions else w.precisions[0])
+
+    # ── headline: the workload at the requested span ──
+    r = measure(w, [prec], args.steps, args.warmup, args.reps, with_cpu, settle_ms=args.settle_ms)
+    p = r["results"][prec]
     line = {
         "metric": METRIC,
         "value": p["value"],
@@ -563,45 +621,63 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": primary,
+        "dtype": prec,
         "data": "synthetic",
         "config": config_of(w, p),
         "roofline": p["roofline"],
         "cpu_baseline": r["cpu"],
+        "wall_ms_per_span": p["wall_ms_per_span"],
         "event_ms_per_span": p["event_ms_per_span"],
         "kernel": p["kernel"],
     }
+    if "clock_settle" in p:
+        line["clock_settle"] = p["clock_settle"]
     if r["cpu"]:
         line["gpu_over_cpu"] = round(p["value"] / r["cpu"]["value"], 1)
-    for prec in precs:
-        if prec != primary:
-            line[prec] = r["results"][prec]
-    if r["parity"]:
-        line["parity"] = r["parity"]
+    if with_cpu:
+        line["parity"] = p["parity"]
+    if args.only:
+        print(json.dumps(line), flush=True)
+        return
+
+    # ── every benchmark configuration at its own rollout length, in each of its precisions ──
+    if not args.no_configs:
+        line["configs"] = {}
+        for idx in W.ALL:
+            wc = W.config(idx)
+            rc = measure(wc, list(wc.precisions), wc.nsteps, 5 * wc.nsteps, 5, with_cpu)
+            entry = {"config": config_of(wc, next(iter(rc["results"].values()))), "cpu_baseline": rc["cpu"]}
+            for pr, res in rc["results"].items():
+                entry[pr] = {k: res[k] for k in ("value", "unit", "ms_per_step", "world_steps_per_s_event_median",
+                                                 "event_ms_per_span", "finite_worlds", "roofline", "kernel")}
+                if with_cpu:
+                    entry[pr]["parity"] = res["parity"]
+                    entry[pr]["gpu_over_cpu"] = round(res["value"] / rc["cpu"]["value"], 1)
+            line["configs"][f"{idx}_{wc.name}"] = entry
     if not args.no_impulse and args.workload != 6:
         wi = W.config(6)
-        ri = measure(wi, ["f32"], wi.nsteps, wi.nsteps, min(args.reps, 5), not args.no_cpu)
+        ri = measure(wi, ["f32"], wi.nsteps, wi.nsteps, min(args.reps, 5), with_cpu)
         pi = ri["results"]["f32"]
         line["terrain_impulse"] = {"value": pi["value"], "unit": "world-steps/s", "dtype": "f32",
                                    "ms_per_step": pi["ms_per_step"], "config": config_of(wi, pi),
                                    "roofline": pi["roofline"], "cpu_baseline": ri["cpu"],
                                    "event_ms_per_span": pi["event_ms_per_span"], "kernel": pi["kernel"],
-                                   "parity": ri["parity"].get("f32")}
+                                   "parity": pi.get("parity")}
     if not args.no_mjcf and args.workload not in W.MJCF_WORKLOADS:
         line["mjcf"] = {}
         for idx in sorted(W.MJCF_WORKLOADS):
             wm = W.config(idx)
-            rm = measure(wm, ["f32"], wm.nsteps, wm.nsteps, 3, not args.no_cpu, cpu_budget_s=8.0)
+            rm = measure(wm, ["f32"], wm.nsteps, wm.nsteps, 3, with_cpu, cpu_budget_s=5.0)
             pm = rm["results"]["f32"]
             line["mjcf"][wm.name] = {"value": pm["value"], "unit": "world-steps/s", "dtype": "f32",
                                      "finite_worlds": pm["finite_worlds"], "config": config_of(wm, pm),
                                      "roofline": pm["roofline"], "cpu_baseline": rm["cpu"],
                                      "event_ms_per_span": pm["event_ms_per_span"], "kernel": pm["kernel"],
-                                     "parity": rm["parity"].get("f32")}
+                                     "parity": pm.get("parity")}
     if not args.no_control:
-        line["control_loop"] = run_control_loop("f32", min(args.reps, 5), not args.no_cpu)
+        line["control_loop"] = run_control_loop("f32", min(args.reps, 5), with_cpu)
     if not args.no_ppo:
-        line["ppo_update"] = run_ppo_update(min(args.reps, 5), not args.no_cpu)
+        line["ppo_update"] = run_ppo_update(min(args.reps, 5), with_cpu)
     print(json.dumps(line), flush=True)
 
 

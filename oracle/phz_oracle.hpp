@@ -1258,8 +1258,9 @@ template <class S> S terrain(const Model& m, const S& px, const S& py, V3<S>& n_
   auto locate = [&](const S& w, double o, int n, int& i, S& t) {
     if (n < 2) { i = 0; t = S(0.0); return; }
     S u = s_clamp((w - S(o)) / S(c.hf_cell), S(0.0), S(double(n - 1)));
-    int ii = (int)s_val(u);
-    if (ii > n - 2) ii = n - 2;
+    const double uv = s_val(u);
+    int ii = std::isfinite(uv) ? (int)uv : 0;  // a diverged world reads cell 0
+    ii = std::max(0, std::min(ii, n - 2));
     i = ii;
     t = u - S(double(ii));
   };

@@ -56,6 +56,21 @@ constexpr int ndof_of(int jt) { return jt == J_FIXED ? 0 : (jt == J_BALL ? 3 : (
 // no expression may produce one even on a discarded path: a division whose
 // denominator can vanish divides by dmax(d, floor), with the floor below the
 // select's own threshold so that the bound cannot be folded back into d.
+// Truncation to int by the hardware conversion, which saturates and maps NaN
+// to 0. A C cast of a NaN or out-of-range value is undefined, and under
+// -ffinite-math-only the float clamps before it may be dropped, so an index
+// that addresses memory or selects a quadrant is converted here and clamped as an integer.
+__device__ __forceinline__ int cvt_sat_i32(float x) {
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+__device__ __forceinline__ int cvt_sat_i32(double x) {
+  int r;
+  asm("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 __device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
 // sin and cos of r in [-pi/4, pi/4] (f32), then of k pi/2 + r: Taylor series
 // through r^9 and r^10 (truncation below 3e-9 on the interval) and the
@@ -127,6 +142,34 @@ __device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
 }
 __device__ __forceinline__ void turn_sincos(double u, double* s, double* c) {
   angle_sincos(6.283185307179586 * u, s, c);
+}
+// sin and cos of a joint angle in f64 for the f32 kernels' penetration chain:
+// the reduction of angle_sincos (exact for |x| < 1.6e6), Taylor series through
+// r^13 and r^14, truncation below 3e-14 on |r| <= pi/4.
+__device__ __forceinline__ void joint_sincos64(double x, double* s, double* c) {
+  const double k = rint(x * 0x1.45f306dc9c883p-1);
+  const double r = (x - k * 0x1.921fb54400000p+0) - k * 0x1.0b4611a626331p-34;
+  const double r2 = r * r;
+  double ps = 1.0 / 6227020800.0;  // 1/13!
+  ps = fma(ps, -r2, 1.0 / 39916800.0);
+  ps = fma(ps, -r2, 1.0 / 362880.0);
+  ps = fma(ps, -r2, 1.0 / 5040.0);
+  ps = fma(ps, -r2, 1.0 / 120.0);
+  ps = fma(ps, -r2, 1.0 / 6.0);
+  const double sr = fma(-r * r2, ps, r);
+  double pc = 1.0 / 87178291200.0;  // 1/14!
+  pc = fma(pc, -r2, 1.0 / 479001600.0);
+  pc = fma(pc, -r2, 1.0 / 3628800.0);
+  pc = fma(pc, -r2, 1.0 / 40320.0);
+  pc = fma(pc, -r2, 1.0 / 720.0);
+  pc = fma(pc, -r2, 1.0 / 24.0);
+  pc = fma(pc, -r2, 0.5);
+  const double cr = fma(-r2, pc, 1.0);
+  const int q = cvt_sat_i32(k) & 3;  // a diverged world's NaN selects quadrant 0
+  const double a = (q & 1) ? cr : sr;
+  const double b = (q & 1) ? sr : cr;
+  *s = (q & 2) ? -a : a;
+  *c = ((q + 1) & 2) ? -b : b;
 }
 __device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double dlog(double x) { return log(x); }
@@ -379,6 +422,21 @@ template <class M, int i> struct BodyK {
   static constexpr int parent = M::parent[i];
 };
 
+// ── f64 penetration chain of the f32 kernels ────────────────────────────────
+// A contact's penetration depth is the small difference of two heights of
+// order a metre: the ground's and the contact point's, which sums the joint
+// offsets of the whole chain from the root. At a penalty stiffness of 1e4 N/m
+// the f32 rounding of that sum (1e-7 m) is a force error of 1e-3 N, and on
+// light feet at rest a per-step qdd error above 1e-4 of max|qdd|. So the f32
+// kernels with contact carry, beside their f32 transforms, the world z-axis in
+// each contact-path body's frame (the third row of its body->world rotation)
+// and the world height of its origin in f64, and evaluate the depth from
+// them. Everything else about the contact, and the dynamics, stays f32.
+// Off in impulse mode, whose f32 kernel is at its register limit: there the
+// chain's live values (436 B of spills instead of 244) gave a kernel whose
+// results changed from launch to launch, cause not found; see DESIGN.
+template <class M, class T> constexpr bool pen64() { return M::HAS_CONTACT && M::CMODE == 0 && sizeof(T) == 4; }
+
 template <class M, class T, int i> __device__ __forceinline__ Sym<T> rigid_inertia() {
   Sym<T> s;
 #pragma unroll
@@ -420,12 +478,13 @@ template <class T> struct Terrain {
   int nx, ny;
 };
 
-// Cell and fraction along one axis, clamped to the grid (NaN lands on cell 0).
+// Cell and fraction along one axis, clamped to the grid. The cell index is in
+// [0, n - 2] whatever w holds (a diverged world's NaN or inf included).
 template <class T> __device__ __forceinline__ void hf_locate(T w, T o, int n, T cell, int& i, T& t) {
   if (n < 2) { i = 0; t = T(0); return; }
   const T u = dmin(dmax((w - o) / cell, T(0)), T(n - 1));
-  int ii = (int)u;
-  ii = ii > n - 2 ? n - 2 : ii;
+  int ii = cvt_sat_i32(u);
+  ii = ii < 0 ? 0 : (ii > n - 2 ? n - 2 : ii);
   i = ii;
   t = u - T(ii);
 }
@@ -570,8 +629,8 @@ __device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_n
 // `write` is set, stores the readback row (touching, deepest penetration,
 // point (x, y, h), summed world force) at out[k * S], k = 8 i .. 8 i + 7.
 template <class M, class T, int i>
-__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const Terrain<T>& tr, T* out,
-                                              int S, bool write) {
+__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const double* cz64,
+                                              const Terrain<T>& tr, T* out, int S, bool write) {
   constexpr int gt = M::gtype[i];
   constexpr int npts = gt == G_BOX ? 8 : 1;
   constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
@@ -588,7 +647,12 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     V3<T> supw = pw + mul(Rw, sup);
     V3<T> nw;
     const T th = terrain_at<M, T>(tr, supw.x, supw.y, nw);
-    T pen = nw.z * (th - supw.z);
+    T pen;
+    if constexpr (pen64<M, T>()) {
+      pen = T(double(nw.z) * (double(th) - cz64[cp]));
+    } else {
+      pen = nw.z * (th - supw.z);
+    }
     const V3<T> nb = M::HAS_HF ? tmul(Rw, nw) : zb;
     const bool in = pen > T(0);
     V3<T> vpt = vel.l + cross(vel.a, sup);
@@ -660,8 +724,8 @@ template <class M, class T> struct GroundPrep {
 // Body i's contact geometry; writes the position part of its readback row
 // (touching, deepest penetration, deepest point) when `write`.
 template <class M, class T, int i>
-__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const Terrain<T>& tr, GroundPrep<M, T>& gp,
-                                               T* out, int S, bool write) {
+__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const double* cz64,
+                                               const Terrain<T>& tr, GroundPrep<M, T>& gp, T* out, int S, bool write) {
   constexpr int n = ground_pts<M>(i), o = ground_off<M>(i);
   const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
   const V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);  // world +Z in the body frame
@@ -674,7 +738,11 @@ __device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const 
     supw[cp] = pw + mul(Rw, gp.sup[o + cp]);
     V3<T> nw;
     const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw);
-    pen[cp] = nw.z * (th - supw[cp].z);
+    if constexpr (pen64<M, T>()) {
+      pen[cp] = T(double(nw.z) * (double(th) - cz64[cp]));
+    } else {
+      pen[cp] = nw.z * (th - supw[cp].z);
+    }
     gp.in[o + cp] = pen[cp] > T(-M::c_margin);
     gp.nb[o + cp] = M::HAS_HF ? tmul(Rw, nw) : zb;
     nact += gp.in[o + cp] ? 1 : 0;
@@ -848,6 +916,9 @@ template <class M, class T> struct WS {
   T Dinv[M::NB][M::MAXD];
   T uu[M::NB][M::MAXD];
   bool ok[M::NB];
+  V3<double> zb64[M::NB];  // f64 penetration chain (f32 kernels with contact)
+  double pz64[M::NB];
+  double cz64[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];  // contact points' world heights
 };
 
 // Joint transform X = X_J(q) X_ptj of body i and its joint velocity S qd
@@ -891,13 +962,93 @@ __device__ __forceinline__ void joint_xf(const T* q, const T* v, Xf<T>& X, SV<T>
   }
 }
 
+
+template <class T> __device__ __forceinline__ Q<double> quat_exp64(V3<T> wf) {
+  const V3<double> w = v3(double(wf.x), double(wf.y), double(wf.z));
+  const double ang = sqrt(dot(w, w));
+  double s, c;
+  joint_sincos64(0.5 * ang, &s, &c);
+  const bool small = ang < Eps<double>::v;
+  const double f = small ? 0.5 : s / dmax(ang, 0.5 * Eps<double>::v);
+  return {small ? 1.0 : c, w.x * f, w.y * f, w.z * f};
+}
+
+// Body i's joint rotation and offset (joint_xf's X.E and X.r) in f64.
+template <class M, class T, int i> __device__ __forceinline__ void joint_xf64(const T* q, R3<double>& E, V3<double>& r) {
+  constexpr int jt = M::jtype[i];
+  constexpr int qo = M::qoff[i];
+  const R3<double> Rp = R3<double>{{M::ptj_rot[i][0], M::ptj_rot[i][1], M::ptj_rot[i][2], M::ptj_rot[i][3],
+                                    M::ptj_rot[i][4], M::ptj_rot[i][5], M::ptj_rot[i][6], M::ptj_rot[i][7],
+                                    M::ptj_rot[i][8]}};
+  const V3<double> pp = v3(M::ptj_pos[i][0], M::ptj_pos[i][1], M::ptj_pos[i][2]);
+  if constexpr (jt == J_REV) {
+    double s, c;
+    joint_sincos64(-double(q[qo]), &s, &c);
+    const double omc = 1.0 - c;
+    R3<double> EJ;
+#pragma unroll
+    for (int k = 0; k < 9; k++) EJ.m[k] = (k % 4 == 0 ? 1.0 : 0.0) + M::rev_k[i][k] * s + M::rev_k2[i][k] * omc;
+    E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+    r = pp;
+  } else if constexpr (jt == J_PRIS) {
+    E = Rp;
+    r = pp + tmul(Rp, v3(M::axis[i][0], M::axis[i][1], M::axis[i][2]) * double(q[qo]));
+  } else if constexpr (jt == J_BALL || jt == J_FREE) {
+    R3<double> EJ = transpose(quat_mat(quat_exp64(v3(q[qo], q[qo + 1], q[qo + 2]))));
+    E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+    if constexpr (jt == J_FREE) r = pp + tmul(Rp, v3(double(q[qo + 3]), double(q[qo + 4]), double(q[qo + 5])));
+    else r = pp;
+  } else {
+    E = Rp;
+    r = pp;
+  }
+}
+
+// Body i's joint velocity S qd (joint_xf's vj).
+template <class M, class T, int i> __device__ __forceinline__ SV<T> joint_vel(const T* v) {
+  constexpr int jt = M::jtype[i];
+  constexpr int vo = M::voff[i];
+  SV<T> vj = {v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+  if constexpr (jt == J_REV) vj.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+  else if constexpr (jt == J_PRIS) vj.l = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+  else if constexpr (jt == J_BALL || jt == J_FREE) {
+    vj.a = v3(v[vo], v[vo + 1], v[vo + 2]);
+    if constexpr (jt == J_FREE) vj.l = v3(v[vo + 3], v[vo + 4], v[vo + 5]);
+  }
+  return vj;
+}
+
 template <class M, class T, int i>
 __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v, T* rows, int S, bool write_rows,
                                            bool do_contact, const Terrain<T>& tr) {
   constexpr int p = M::parent[i];
   Xf<T>& X = ws.X[i];
   SV<T> vj;
-  joint_xf<M, T, i>(q, v, X, vj);
+  if constexpr (pen64<M, T>() && M::need_world[i]) {
+    // The joint transform once, in f64: the height chain uses it as it is and
+    // the f32 dynamics its rounding (so no f32 sincos of this joint).
+    // Rw_i = Rw_p X.E^T: third row zb_i = X.E zb_p; Pw_i = Pw_p + Rw_p X.r.
+    R3<double> E64;
+    V3<double> r64;
+    joint_xf64<M, T, i>(q, E64, r64);
+#pragma unroll
+    for (int k = 0; k < 9; k++) X.E.m[k] = T(E64.m[k]);
+    X.r = v3(T(r64.x), T(r64.y), T(r64.z));
+    vj = joint_vel<M, T, i>(v);
+    if constexpr (p < 0) {
+      ws.zb64[i] = v3(E64.m[2], E64.m[5], E64.m[8]);
+      ws.pz64[i] = r64.z;
+    } else {
+      ws.zb64[i] = mul(E64, ws.zb64[p]);
+      ws.pz64[i] = ws.pz64[p] + dot(ws.zb64[p], r64);
+    }
+    // Only the contact points' heights outlive the body's children.
+#pragma unroll
+    for (int cp = 0; cp < ground_pts<M>(i); cp++)
+      ws.cz64[ground_off<M>(i) + cp] = ws.pz64[i] + dot(ws.zb64[i], contact_point<M, double, i>(cp, ws.zb64[i]));
+  } else {
+    joint_xf<M, T, i>(q, v, X, vj);
+  }
   if constexpr (p < 0) {
     ws.vel[i] = vj;
     ws.cb[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
@@ -917,7 +1068,7 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
   }
   if constexpr (M::gtype[i] != G_NONE) {
     if (do_contact) {
-      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], tr, rows, S, write_rows);
+      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], ws.cz64 + ground_off<M>(i), tr, rows, S, write_rows);
       ws.pA[i] = ws.pA[i] - f;
     }
   }
@@ -1463,7 +1614,8 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
   GroundPrep<M, T> gp;
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
-    if constexpr (M::gtype[i] != G_NONE) ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], tr, gp, rows, S, write_rows);
+    if constexpr (M::gtype[i] != G_NONE)
+      ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws.cz64 + ground_off<M>(i), tr, gp, rows, S, write_rows);
   });
   // A plain loop: compact, spill-free, and exact at every sweep count. Left to
   // the compiler's own unrolling choice, the f64 kernel of an 8-corner box gave

@@ -5,8 +5,12 @@ pass is pinned in tests/test_oracle_contact_modes.py).
 Per step: qdd, the carried contact forces and the warm-start impulses, from
 the same states. Over several steps (several launches, graph replay on and
 off): the state and the contact state. f64 kernels are held to 1e-10 (one
-step) and 1e-8 (rollouts); f32 kernels to the f32 floor the oracle itself shows
-against the reference (2e-4 relative).
+step) and 1e-8 (rollouts). f32 kernels: qdd to 1e-4 per step in penalty mode,
+where the kernel evaluates penetration depths from an f64 height chain. In
+impulse mode (whose f32 kernel evaluates them in f32) and on the body-attached
+plane (a depth between two bodies' f32 world positions) qdd is held to 2e-4,
+the deviation the reference's own f32 contact pass shows from the f64 law
+(tests/golden/ref_contact_modes.npz); carried impulses and forces to 2e-4.
 """
 import dataclasses
 
@@ -146,7 +150,7 @@ def test_contact_mode_matches_oracle(name, kind, mode, terr, prec):
     e1, s1 = ext.copy(), cs.copy()
     want_qdd, rows = orc.step_batch(q1, v1, c1, 1, threads=8, want_contacts=True, ext_state=e1, cs_state=s1)
     err = rel_err_rows(qdd, want_qdd).max()
-    tol = 1e-10 if prec == "f64" else 2e-4
+    tol = 1e-10 if prec == "f64" else (2e-4 if kind == "deck" or mode == 1 else 1e-4)
     print(f"{name} {prec}: qdd {err:.2e}", flush=True)
     assert err <= tol
     touch = dcs[:, :, 0] > 0
@@ -245,7 +249,8 @@ def test_impulse_sweep_counts(kind, prec):
         err = rel_err_rows(qdd, want).max()
         ierr = np.abs(dcs[:, :, 8:] - s1[:, :, 8:]).max() / max(np.abs(s1[:, :, 8:]).max(), 1e-6)
         print(f"{kind} {prec} sweeps {sweeps}: qdd {err:.2e} impulses {ierr:.2e}", flush=True)
-        assert err <= (1e-10 if prec == "f64" else 2e-4) and ierr <= (1e-9 if prec == "f64" else 2e-4)
+        assert err <= (1e-10 if prec == "f64" else 2e-4)
+        assert ierr <= (1e-9 if prec == "f64" else 2e-4)
 
 
 @pytest.mark.parametrize("prec", ["f64", "f32"])

@@ -114,8 +114,7 @@ def _step_matches_oracle(name, prec, groups=None):
     if prec == "f64":
         assert e.max() <= 1e-10
     else:
-        floor = np.array([rel_err_rows(orc.qdd_f32(q[k], v[k], ctrl[k]), want[k]) for k in range(n)])
-        assert np.all(e <= np.maximum(1e-4, 4 * floor))
+        assert e.max() <= 1e-4
     # The control stream is identical whatever the partition.
     s0 = _sim(m, n, prec, "0", contact, noise)
     s0.load_states(q, v, np.zeros((n, m.nv)))
