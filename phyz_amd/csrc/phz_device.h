@@ -432,10 +432,7 @@ template <class M, int i> struct BodyK {
 // each contact-path body's frame (the third row of its body->world rotation)
 // and the world height of its origin in f64, and evaluate the depth from
 // them. Everything else about the contact, and the dynamics, stays f32.
-// Off in impulse mode, whose f32 kernel is at its register limit: there the
-// chain's live values (436 B of spills instead of 244) gave a kernel whose
-// results changed from launch to launch, cause not found; see DESIGN.
-template <class M, class T> constexpr bool pen64() { return M::HAS_CONTACT && M::CMODE == 0 && sizeof(T) == 4; }
+template <class M, class T> constexpr bool pen64() { return M::HAS_CONTACT && sizeof(T) == 4; }
 
 template <class M, class T, int i> __device__ __forceinline__ Sym<T> rigid_inertia() {
   Sym<T> s;
@@ -715,7 +712,7 @@ template <class M> constexpr int ground_off(int i) {
 }
 template <class M, class T> struct GroundPrep {
   static constexpr int N = ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1;
-  V3<T> sup[N], nb[N], tu[N], tw[N];  // body frame
+  V3<T> sup[N], nb[N], tu[N];  // body frame; the second tangent is nb x tu (tangent_frame)
   T mn[N], cu[N], cw[N], bias[N];
   bool in[N];
   bool any[M::NB];
@@ -754,10 +751,11 @@ __device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const 
 #pragma unroll
   for (int cp = 0; cp < n; cp++) {
     const int k = o + cp;
-    tangent_frame(gp.nb[k], gp.tu[k], gp.tw[k]);
+    V3<T> tw;
+    tangent_frame(gp.nb[k], gp.tu[k], tw);
     gp.mn[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.nb[k]) / na, T(1e-9));
     gp.cu[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.tu[k]), T(1e-9)) / na;
-    gp.cw[k] = dmax(eff_mass<M, T, i>(gp.sup[k], gp.tw[k]), T(1e-9)) / na;
+    gp.cw[k] = dmax(eff_mass<M, T, i>(gp.sup[k], tw), T(1e-9)) / na;
     gp.bias[k] = impedance_at<M, T>(pen[cp]) * T(M::c_erp) * dmax(pen[cp], T(0)) / T(dtc);
     const bool in = gp.in[k];
     any = any || in;
@@ -787,11 +785,12 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
   for (int cp = 0; cp < n; cp++) {
     const int k = o + cp;
     const V3<T> vpt = vel.l + cross(vel.a, gp.sup[k]);
+    const V3<T> gtw = cross(gp.nb[k], gp.tu[k]);  // as tangent_frame forms it
     const T b_n = dot(vpt, gp.nb[k]);
     const T e = restitution_at<M, T>(dmin(b_n, T(0)));
     const T fn = dmax((gp.bias[k] - b_n * (T(1) + e)) * gp.mn[k] + slot[3 * cp], T(0));
     const T tu = slot[3 * cp + 1] - dot(vpt, gp.tu[k]) * gp.cu[k];
-    const T tw = slot[3 * cp + 2] - dot(vpt, gp.tw[k]) * gp.cw[k];
+    const T tw = slot[3 * cp + 2] - dot(vpt, gtw) * gp.cw[k];
     const T limit = T(M::mu) * fn;
     const T tn = dsqrt(tu * tu + tw * tw);
     const T sc = tn > limit ? (tn > T(0) ? limit / dmax(tn, T(1e-30)) : T(0)) : T(1);
@@ -799,7 +798,7 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
     slot[3 * cp] = in ? fn : T(0);
     slot[3 * cp + 1] = in ? tu * sc : T(0);
     slot[3 * cp + 2] = in ? tw * sc : T(0);
-    const V3<T> fb = (gp.nb[k] * slot[3 * cp] + gp.tu[k] * slot[3 * cp + 1] + gp.tw[k] * slot[3 * cp + 2]) * T(1.0 / dtc);
+    const V3<T> fb = (gp.nb[k] * slot[3 * cp] + gp.tu[k] * slot[3 * cp + 1] + gtw * slot[3 * cp + 2]) * T(1.0 / dtc);
     ext.a = ext.a + cross(gp.sup[k], fb);
     ext.l = ext.l + fb;
   }
@@ -920,6 +919,14 @@ template <class M, class T> struct WS {
   double pz64[M::NB];
   double cz64[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];  // contact points' world heights
 };
+
+// Column k, entry r of U = I_A S of body i. A free joint's S is the identity,
+// so its U is I_A itself, read from the symmetric storage (21 values live
+// through the impulse sweeps instead of 36).
+template <class M, class T, int i> __device__ __forceinline__ T Uv(const WS<M, T>& ws, int k, int r) {
+  if constexpr (M::jtype[i] == J_FREE) return sym_get(ws.IA[i], r, k);
+  else return ws.U[i][k][r];
+}
 
 // Joint transform X = X_J(q) X_ptj of body i and its joint velocity S qd
 // (crates/phyz-model/src/joint.rs:253-360 maps; the same for FK and ABA).
@@ -1130,9 +1137,11 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
   if constexpr (nd > 0) {
     sfor<0, nd>([&](auto K) {
       constexpr int k = decltype(K)::value;
-      SV<T> uk = sym_mul(ws.IA[i], subspace<M, T, i>(k));
-      ws.U[i][k][0] = uk.a.x; ws.U[i][k][1] = uk.a.y; ws.U[i][k][2] = uk.a.z;
-      ws.U[i][k][3] = uk.l.x; ws.U[i][k][4] = uk.l.y; ws.U[i][k][5] = uk.l.z;
+      if constexpr (M::jtype[i] != J_FREE) {
+        SV<T> uk = sym_mul(ws.IA[i], subspace<M, T, i>(k));
+        ws.U[i][k][0] = uk.a.x; ws.U[i][k][1] = uk.a.y; ws.U[i][k][2] = uk.a.z;
+        ws.U[i][k][3] = uk.l.x; ws.U[i][k][4] = uk.l.y; ws.U[i][k][5] = uk.l.z;
+      }
       ws.uu[i][k] = dof_force<M, T, i, k>(q, v, ctrl) - dot(subspace<M, T, i>(k), ws.pA[i]);
     });
     T D[MAXD][MAXD];
@@ -1141,7 +1150,7 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
 #pragma unroll
       for (int c = 0; c <= r; c++) {
         SV<T> sr = subspace<M, T, i>(r);
-        SV<T> ucol = {v3(ws.U[i][c][0], ws.U[i][c][1], ws.U[i][c][2]), v3(ws.U[i][c][3], ws.U[i][c][4], ws.U[i][c][5])};
+        SV<T> ucol = {v3(Uv<M, T, i>(ws, c, 0), Uv<M, T, i>(ws, c, 1), Uv<M, T, i>(ws, c, 2)), v3(Uv<M, T, i>(ws, c, 3), Uv<M, T, i>(ws, c, 4), Uv<M, T, i>(ws, c, 5))};
         D[r][c] = dot(sr, ucol) + (r == c ? T(M::armature[i] + M::dt * M::damping[i]) : T(0));
       }
     // LDL^T with the pivots stored inverted (same singular test as aba.rs:210).
@@ -1170,7 +1179,7 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
         T y[MAXD];
 #pragma unroll
         for (int k = 0; k < nd; k++) {
-          y[k] = ws.U[i][k][r];
+          y[k] = Uv<M, T, i>(ws, k, r);
 #pragma unroll
           for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
         }
@@ -1187,9 +1196,9 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
       for (int r = 0; r < 3; r++)
 #pragma unroll
         for (int c = r; c < 3; c++) {
-          T s0 = W[0][r] * ws.U[i][0][c], s1 = W[0][3 + r] * ws.U[i][0][3 + c];
+          T s0 = W[0][r] * Uv<M, T, i>(ws, 0, c), s1 = W[0][3 + r] * Uv<M, T, i>(ws, 0, 3 + c);
 #pragma unroll
-          for (int k = 1; k < nd; k++) { s0 = s0 + W[k][r] * ws.U[i][k][c]; s1 = s1 + W[k][3 + r] * ws.U[i][k][3 + c]; }
+          for (int k = 1; k < nd; k++) { s0 = s0 + W[k][r] * Uv<M, T, i>(ws, k, c); s1 = s1 + W[k][3 + r] * Uv<M, T, i>(ws, k, 3 + c); }
           Ia.a[sx(r, c)] = Ia.a[sx(r, c)] - s0;
           Ia.c[sx(r, c)] = Ia.c[sx(r, c)] - s1;
         }
@@ -1197,9 +1206,9 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
       for (int r = 0; r < 3; r++)
 #pragma unroll
         for (int c = 0; c < 3; c++) {
-          T s0 = W[0][r] * ws.U[i][0][3 + c];
+          T s0 = W[0][r] * Uv<M, T, i>(ws, 0, 3 + c);
 #pragma unroll
-          for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * ws.U[i][k][3 + c];
+          for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * Uv<M, T, i>(ws, k, 3 + c);
           Ia.b[r * 3 + c] = Ia.b[r * 3 + c] - s0;
         }
       SV<T> wu;
@@ -1231,8 +1240,8 @@ template <class M, class T, int i> __device__ __forceinline__ void body_pass3(WS
     T y[MAXD];
 #pragma unroll
     for (int k = 0; k < nd; k++) {
-      T uta = ws.U[i][k][0] * ap.a.x + ws.U[i][k][1] * ap.a.y + ws.U[i][k][2] * ap.a.z + ws.U[i][k][3] * ap.l.x +
-              ws.U[i][k][4] * ap.l.y + ws.U[i][k][5] * ap.l.z;
+      T uta = Uv<M, T, i>(ws, k, 0) * ap.a.x + Uv<M, T, i>(ws, k, 1) * ap.a.y + Uv<M, T, i>(ws, k, 2) * ap.a.z + Uv<M, T, i>(ws, k, 3) * ap.l.x +
+              Uv<M, T, i>(ws, k, 4) * ap.l.y + Uv<M, T, i>(ws, k, 5) * ap.l.z;
       y[k] = ws.uu[i][k] - uta;
 #pragma unroll
       for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
@@ -1515,7 +1524,7 @@ template <class M, class T, int i> __device__ __forceinline__ void body_delta_up
         for (int t = k + 1; t < nd; t++) y[k] = y[k] - ws.Lm[i][t][k] * y[t];
 #pragma unroll
       for (int k = 0; k < nd; k++) {
-        const SV<T> uk = {v3(ws.U[i][k][0], ws.U[i][k][1], ws.U[i][k][2]), v3(ws.U[i][k][3], ws.U[i][k][4], ws.U[i][k][5])};
+        const SV<T> uk = {v3(Uv<M, T, i>(ws, k, 0), Uv<M, T, i>(ws, k, 1), Uv<M, T, i>(ws, k, 2)), v3(Uv<M, T, i>(ws, k, 3), Uv<M, T, i>(ws, k, 4), Uv<M, T, i>(ws, k, 5))};
         pa = pa + uk * y[k];
       }
     }
@@ -1536,8 +1545,8 @@ template <class M, class T, int i> __device__ __forceinline__ void body_delta_do
     T y[MAXD];
 #pragma unroll
     for (int k = 0; k < nd; k++) {
-      T uta = ws.U[i][k][0] * ap.a.x + ws.U[i][k][1] * ap.a.y + ws.U[i][k][2] * ap.a.z + ws.U[i][k][3] * ap.l.x +
-              ws.U[i][k][4] * ap.l.y + ws.U[i][k][5] * ap.l.z;
+      T uta = Uv<M, T, i>(ws, k, 0) * ap.a.x + Uv<M, T, i>(ws, k, 1) * ap.a.y + Uv<M, T, i>(ws, k, 2) * ap.a.z + Uv<M, T, i>(ws, k, 3) * ap.l.x +
+              Uv<M, T, i>(ws, k, 4) * ap.l.y + Uv<M, T, i>(ws, k, 5) * ap.l.z;
       y[k] = ws.uu[i][k] - uta;
 #pragma unroll
       for (int t = 0; t < k; t++) y[k] = y[k] - ws.Lm[i][k][t] * y[t];
@@ -1602,23 +1611,18 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     }
   });
   sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
-  // qdd at the carried forces ext0; the sweeps add the response to ext - ext0.
-  T qdd0[M::NV];
-  SV<T> ext0[NB];
-#pragma unroll
-  for (int j = 0; j < M::NV; j++) qdd0[j] = qdd[j];
-  sfor<0, NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    if constexpr (HasExt<M>::template at<i>()) ext0[i] = ext[i];
-  });
   GroundPrep<M, T> gp;
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
     if constexpr (M::gtype[i] != G_NONE)
       ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws.cz64 + ground_off<M>(i), tr, gp, rows, S, write_rows);
   });
-  // A plain loop: compact, spill-free, and exact at every sweep count. Left to
-  // the compiler's own unrolling choice, the f64 kernel of an 8-corner box gave
+  // Each sweep moves qdd by the ABA's response to that sweep's change of the
+  // contact forces (the solve is affine in them): qdd and ext carry from one
+  // sweep to the next, so neither the step's first qdd nor its first forces
+  // stay live through the loop.
+  // A plain loop: compact and exact at every sweep count. Left to the
+  // compiler's own unrolling choice, the f64 kernel of an 8-corner box gave
   // wrong impulses from the fourth sweep on (checked across sweep counts in
   // tests/test_gpu_contact_modes.py).
 #pragma unroll 1
@@ -1631,13 +1635,17 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int p = M::parent[i];
-      Xf<T> Xd;
-      SV<T> vj;
-      joint_xf<M, T, i>(q, vv, Xd, vj);
+      const SV<T> vj = joint_vel<M, T, i>(vv);
       if constexpr (p < 0) vf[i] = vj;
       else vf[i] = apply_motion(ws.X[i], vf[p]) + vj;
     });
     const bool wr = write_rows && sw == M::SWEEPS - 1;
+    SV<T> dp[NB];  // the previous sweep's forces, then their change
+    sfor<0, NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (HasExt<M>::template at<i>()) dp[i] = ext[i];
+      else dp[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+    });
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if constexpr (M::gtype[i] != G_NONE) {
@@ -1650,30 +1658,54 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
 #pragma unroll
             for (int k = 0; k < 3 * ground_pts<M>(i); k++) impp[i][k] = T(0);
           }
-        }
-        if (wr) {
-          const V3<T> ft = mul(ws.Rw[i], ext[i].l);  // summed ground force, world frame
-          T* r = rows + 8 * i * S;
-          r[5 * S] = gp.any[i] ? ft.x : T(0);
-          r[6 * S] = gp.any[i] ? ft.y : T(0);
-          r[7 * S] = gp.any[i] ? ft.z : T(0);
+          if (wr) {
+            const V3<T> ft = mul(ws.Rw[i], ext[i].l);  // summed ground force, world frame
+            T* r = rows + 8 * i * S;
+            r[5 * S] = gp.any[i] ? ft.x : T(0);
+            r[6 * S] = gp.any[i] ? ft.y : T(0);
+            r[7 * S] = gp.any[i] ? ft.z : T(0);
+          }
         }
       } else if constexpr (i == M::PLANE) {
         ext[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
       }
     });
     if constexpr (M::PLANE >= 0) plane_contacts<M, T, true>(ws.Rw, ws.Pw, vf, impp, ext);
-    SV<T> dp[NB];
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      if constexpr (HasExt<M>::template at<i>()) dp[i] = ext0[i] - ext[i];
-      else dp[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
+      if constexpr (HasExt<M>::template at<i>()) dp[i] = dp[i] - ext[i];
     });
     rfor<NB>([&](auto I) { body_delta_up<M, T, decltype(I)::value>(ws, dp); });
     T dqdd[M::NV];
     sfor<0, NB>([&](auto I) { body_delta_down<M, T, decltype(I)::value>(ws, dqdd); });
 #pragma unroll
-    for (int j = 0; j < M::NV; j++) qdd[j] = qdd0[j] + dqdd[j];
+    for (int j = 0; j < M::NV; j++) qdd[j] = qdd[j] + dqdd[j];
+  }
+  if constexpr (M::PLANE < 0) {
+    // Without a plane, ext holds the last sweep's ground forces: the readback
+    // rows' world force, with the body rotations recomputed here (rows are
+    // written on a launch's last step only, and the rotations do not stay live
+    // through the sweeps).
+    if (write_rows) {
+      R3<T> Rw[NB];
+      sfor<0, NB>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        constexpr int p = M::parent[i];
+        if constexpr (M::need_world[i]) {
+          R3<T> E = ws.X[i].E;
+#pragma unroll
+          for (int k = 0; k < 9; k++) asm volatile("" : "+v"(E.m[k]));  // recompute, not reuse pass 1's
+          Rw[i] = p < 0 ? transpose(E) : mul_bt(Rw[p < 0 ? 0 : p], E);
+        }
+        if constexpr (M::gtype[i] != G_NONE) {
+          const V3<T> ft = mul(Rw[i], ext[i].l);
+          T* r = rows + 8 * i * S;
+          r[5 * S] = gp.any[i] ? ft.x : T(0);
+          r[6 * S] = gp.any[i] ? ft.y : T(0);
+          r[7 * S] = gp.any[i] ? ft.z : T(0);
+        }
+      });
+    }
   }
   sfor<0, NB>([&](auto I) { body_integrate<M, T, decltype(I)::value>(q, v, qdd); });
 }
@@ -1747,6 +1779,7 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
     if (live) {
       T* he = (T*)a.ext;
       T* hi = (T*)a.imp;
+      asm volatile("" : "+s"(he), "+s"(hi));  // fresh addresses (see below)
       sfor<0, M::NB>([&](auto I) {
         constexpr int i = decltype(I)::value;
         constexpr int np3 = 3 * (M::gtype[i] == G_BOX ? 8 : 1);
@@ -1770,6 +1803,9 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
     }
   }
   if (!live) return;
+  // Addresses for the final stores computed afresh: reusing the loads' per-DOF
+  // addresses would keep them live through every step of the launch.
+  asm volatile("" : "+s"(gq), "+s"(gv), "+s"(gc));
   sfor<0, M::NQ>([&](auto J) {
     constexpr int j = decltype(J)::value;
     if constexpr (M::dof_group[j] == G || (G == 0 && M::dof_group[j] == -1)) {
