@@ -66,6 +66,7 @@ SIGNATURES = {
     "phz_graphs_enabled": (C.c_int, [SIM]),
     "phz_synchronize": (C.c_int, [SIM]),
     "phz_readback_states": (C.c_int, [SIM, dp, dp]),
+    "phz_readback_states_noalloc": (C.c_int, [SIM, dp, dp]),
     "phz_readback_contacts": (C.c_int, [SIM, dp]),
     "phz_readback_controls": (C.c_int, [SIM, dp]),
     "phz_readback_qdd": (C.c_int, [SIM, dp]),

@@ -44,6 +44,7 @@ hipError_t phz_io_unpack(const void* src, double* dst, int nworld, int width, in
 hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s);
 hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s);
 hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+hipError_t phz_io_scratch(void** ptr, size_t* bytes);
 }
 
 namespace {
@@ -1848,6 +1849,35 @@ int phz_readback_states(phz_sim* s, double* q, double* v) {
   if (v && !s->download_rows(s->v, v, s->model.nv, "readback v")) return 1;
   return 0;
 }
+// phz_readback_states through the library's static per-GPU scratch array
+// instead of the sim's staging buffer: no device allocation on any call.
+int phz_readback_states_noalloc(phz_sim* s, double* q, double* v) {
+  if (!s) return 1;
+  if (!s->has_device()) return s->fail("host-only sim has no device buffers");
+  if (!set_device(s)) return 1;
+  void* scr = nullptr;
+  size_t cap = 0;
+  if (!s->hip_ok(phz_io_scratch(&scr, &cap), "readback_states_noalloc: scratch lookup")) return 1;
+  const int width = std::max(s->model.nq, s->model.nv);
+  const size_t need = (size_t)s->nworld * (size_t)width * sizeof(double);
+  if (need > cap)
+    return s->fail(fmt("readback_states_noalloc: %d worlds x %d values need %zu bytes of staging, above the %zu-byte "
+                       "scratch; use phz_readback_states", s->nworld, width, need, cap));
+  const std::pair<const void*, double*> parts[2] = {{s->q, q}, {s->v, v}};
+  const int widths[2] = {s->model.nq, s->model.nv};
+  for (int k = 0; k < 2; k++) {
+    if (!parts[k].second || widths[k] <= 0 || s->nworld == 0) continue;
+    const size_t bytes = (size_t)s->nworld * widths[k] * sizeof(double);
+    if (!s->hip_ok(phz_io_unpack(parts[k].first, (double*)scr, s->nworld, widths[k], s->stride, s->f64 ? 1 : 0,
+                                 s->stream), "readback_states_noalloc: unpack") ||
+        !s->hip_ok(hipMemcpyAsync(parts[k].second, scr, bytes, hipMemcpyDeviceToHost, s->stream),
+                   "readback_states_noalloc: copy") ||
+        !s->hip_ok(hipStreamSynchronize(s->stream), "readback_states_noalloc: sync"))
+      return 1;
+  }
+  return 0;
+}
+
 int phz_readback_controls(phz_sim* s, double* ctrl) {
   if (!s || !ctrl) return 1;
   if (!s->has_device()) return s->fail("host-only sim has no device buffers");

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace {
 
 // dst[j * stride + w] = (T) src[w * width + j]
@@ -52,7 +54,19 @@ __global__ void copy_words(uint32_t* __restrict__ dst, const uint32_t* __restric
 constexpr int kBlock = 256;
 inline int blocks(size_t n) { return (int)((n + kBlock - 1) / kBlock); }
 
+constexpr size_t kScratchBytes = size_t(32) << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
+
+// Staging rows for callers that cannot allocate device memory
+// (phz_readback_states_noalloc): 32 MiB per GPU, held until the process ends.
+// Every call on a GPU shares that GPU's copy, so calls that overlap on one GPU
+// race. In host code `scratch` names a host-side stand-in, never the device
+// memory: use the address phz_io_scratch returns.
+static __device__ __align__(256) double scratch[kScratchBytes / sizeof(double)];
 
 extern "C" {
 
@@ -83,6 +97,26 @@ hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s) 
   const size_t n = bytes / 4;
   hipLaunchKernelGGL(copy_words, dim3(blocks(n)), dim3(kBlock), 0, s, (uint32_t*)dst, (const uint32_t*)src, n);
   return hipGetLastError();
+}
+
+// The device address of the current device's scratch array and its size,
+// looked up once per device (with that device current) and kept.
+hipError_t phz_io_scratch(void** ptr, size_t* bytes) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  *bytes = kScratchBytes;
+  return hipSuccess;
 }
 
 hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s) {

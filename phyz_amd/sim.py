@@ -218,6 +218,14 @@ class BatchSim:
         self._check(self._L.phz_readback_states(self._h, _dp(q), _dp(v)))
         return q, v
 
+    def readback_states_noalloc(self):
+        """readback_states through the library's static per-GPU scratch (no
+        device allocation); worlds x max(nq, nv) x 8 bytes at most 32 MiB."""
+        q = np.zeros((self.nworld, self.nq))
+        v = np.zeros((self.nworld, self.nv))
+        self._check(self._L.phz_readback_states_noalloc(self._h, _dp(q), _dp(v)))
+        return q, v
+
     def readback_contacts(self) -> np.ndarray:
         rows = np.zeros((self.nworld, self.nb, 8))
         self._check(self._L.phz_readback_contacts(self._h, _dp(rows)))
