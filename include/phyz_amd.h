@@ -180,6 +180,12 @@ int phz_time_step_many(phz_sim* sim, uint32_t n, uint32_t reps, double* ms_per_r
  * [1] AGPRs, [2] SGPRs, [3] private (scratch) bytes per lane, [4] block size,
  * [5] max steps per launch. */
 int phz_kernel_info(phz_sim* sim, int64_t* info);
+/* Lanes per world of the compiled step kernel: 1, or 2 or 4 when a small
+ * launch splits each world's revolute-joint sincos over several lanes; -1 on
+ * error. No counterpart in the reference (its kernel is one thread per world,
+ * crates/phyz-gpu/cuda/phyz_kernels.cu); it reports this build's launch
+ * layout. Works on host-only sims. */
+int phz_lanes_per_world(phz_sim* sim);
 
 /* ── Device-resident control loop (mod.rs:1004-1376; policy_pipeline.rs) ──── */
 

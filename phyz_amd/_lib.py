@@ -76,6 +76,7 @@ SIGNATURES = {
     "phz_compile": (C.c_int, [SIM]),
     "phz_time_step_many": (C.c_int, [SIM, C.c_uint32, C.c_uint32, dp]),
     "phz_kernel_info": (C.c_int, [SIM, i64p]),
+    "phz_lanes_per_world": (C.c_int, [SIM]),
     "phz_enable_contact_terrain": (C.c_int, [SIM, C.c_double, C.c_double, dp, dp, dp, u32p, C.c_uint32, dp, dp, u32p]),
     "phz_enable_contact_impulse": (C.c_int, [SIM, C.c_double, C.c_double, dp, dp, dp, u32p, C.c_uint32, dp, dp, dp,
                                              u32p]),

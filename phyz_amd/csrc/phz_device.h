@@ -71,7 +71,10 @@ __device__ __forceinline__ int cvt_sat_i32(double x) {
   return r;
 }
 
-__device__ __forceinline__ void dsincos(double x, double* s, double* c) { sincos(x, s, c); }
+__device__ __forceinline__ void angle_sincos(double x, double* s, double* c);
+// f64 joint angles take the closed form below (reduction exact for |x| < 1.6e6)
+// rather than the library routine and its large-argument branch.
+__device__ __forceinline__ void dsincos(double x, double* s, double* c) { angle_sincos(x, s, c); }
 // sin and cos of r in [-pi/4, pi/4] (f32), then of k pi/2 + r: Taylor series
 // through r^9 and r^10 (truncation below 3e-9 on the interval) and the
 // quadrant's sign and swap. Used for the Box-Muller angle below; joint angles
@@ -95,42 +98,48 @@ __device__ __forceinline__ void quadrant_sincos(float r, float k, float* s, floa
 }
 __device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
-// sin and cos of a Box-Muller angle x in [0, 2*pi] (f64). x = k*pi/2 + r with
-// k = rint(2x/pi) in 0..4 and pi/2 split as hi + lo, hi holding 33 significant
-// bits so that k*hi and x - k*hi are exact; |r| <= pi/4 and the split's residual
-// is 3.5e-27. sin r and cos r are their Taylor series through r^17 and r^18,
-// whose truncation stays below 1e-19 on |r| <= pi/4. In an IEEE build of the
-// chain kernel the library sincos gave one of these sines a sign that varied
-// from launch to launch (its optimised IR was correct); this closed form has
-// no such dependence and costs less than the general reduction.
+// sin and cos of x (f64): x = k*pi/2 + r with k the integer nearest 2x/pi,
+// taken as t - M for t = 2x/pi + M, M = 1.5 * 2^52 (the addition rounds to
+// an integer; the low word of t then holds k mod 2^32, the quadrant, with no
+// conversion). pi/2 is split as hi + lo, hi holding 33 significant bits, so
+// that k*hi and x - k*hi are exact for |k| < 2^20 (|x| < 1.6e6); |r| <= pi/4
+// and the split's residual is 3.5e-27. With u = -r^2: sin r = r + r u P(u),
+// P through u^7 (the Taylor series through r^17), and cos r = 1 + u Q(u), Q
+// through u^7 (through r^16); the truncations stay below 1e-19 and 3e-18 of
+// the value on |r| <= pi/4. P and Q are evaluated in Estrin's form (pairs,
+// then u^2, then u^4), about half the dependent chain of Horner's form.
+// Used for the Box-Muller angle (in an IEEE build of the chain kernel the
+// library sincos gave one of those sines a sign that varied from launch to
+// launch, its optimised IR correct) and for every f64 joint angle.
 __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
-  const double k = rint(x * 0x1.45f306dc9c883p-1);
-  const double r = (x - k * 0x1.921fb54400000p+0) - k * 0x1.0b4611a626331p-34;
-  const double r2 = r * r;
-  double ps = 1.0 / 355687428096000.0;  // 1/17!
-  ps = fma(ps, -r2, 1.0 / 1307674368000.0);
-  ps = fma(ps, -r2, 1.0 / 6227020800.0);
-  ps = fma(ps, -r2, 1.0 / 39916800.0);
-  ps = fma(ps, -r2, 1.0 / 362880.0);
-  ps = fma(ps, -r2, 1.0 / 5040.0);
-  ps = fma(ps, -r2, 1.0 / 120.0);
-  ps = fma(ps, -r2, 1.0 / 6.0);
-  const double sr = fma(-r * r2, ps, r);
-  double pc = 1.0 / 6402373705728000.0;  // 1/18!
-  pc = fma(pc, -r2, 1.0 / 20922789888000.0);
-  pc = fma(pc, -r2, 1.0 / 87178291200.0);
-  pc = fma(pc, -r2, 1.0 / 479001600.0);
-  pc = fma(pc, -r2, 1.0 / 3628800.0);
-  pc = fma(pc, -r2, 1.0 / 40320.0);
-  pc = fma(pc, -r2, 1.0 / 720.0);
-  pc = fma(pc, -r2, 1.0 / 24.0);
-  pc = fma(pc, -r2, 0.5);
-  const double cr = fma(-r2, pc, 1.0);
-  const int q = (int)k & 3;
-  const double a = (q & 1) ? cr : sr;
-  const double b = (q & 1) ? sr : cr;
-  *s = (q & 2) ? -a : a;
-  *c = ((q + 1) & 2) ? -b : b;
+  constexpr double M = 6755399441055744.0;  // 1.5 * 2^52
+  const double t = fma(x, 0x1.45f306dc9c883p-1, M);
+  const double k = t - M;
+  const double r = fma(-k, 0x1.0b4611a626331p-34, fma(-k, 0x1.921fb54400000p+0, x));
+  const double u = -(r * r);
+  const double u2 = u * u;
+  const double u4 = u2 * u2;
+  // P(u) = sum_j u^j / (2j+3)!, Q(u) = sum_j u^j / (2j+2)!  (j = 0..7)
+  const double p01 = fma(u, 1.0 / 120.0, 1.0 / 6.0);
+  const double p23 = fma(u, 1.0 / 362880.0, 1.0 / 5040.0);
+  const double p45 = fma(u, 1.0 / 6227020800.0, 1.0 / 39916800.0);
+  const double p67 = fma(u, 1.0 / 355687428096000.0, 1.0 / 1307674368000.0);
+  const double q01 = fma(u, 1.0 / 24.0, 0.5);
+  const double q23 = fma(u, 1.0 / 40320.0, 1.0 / 720.0);
+  const double q45 = fma(u, 1.0 / 479001600.0, 1.0 / 3628800.0);
+  const double q67 = fma(u, 1.0 / 20922789888000.0, 1.0 / 87178291200.0);
+  const double p = fma(u4, fma(u2, p67, p45), fma(u2, p23, p01));
+  const double q = fma(u4, fma(u2, q67, q45), fma(u2, q23, q01));
+  const double sr = fma(r * u, p, r);
+  const double cr = fma(u, q, 1.0);
+  // Quadrant n = k mod 4: sin x = +-(n odd ? cos r : sin r), negative for
+  // n = 2, 3; cos x = +-(n odd ? sin r : cos r), negative for n = 1, 2.
+  const unsigned n = (unsigned)__builtin_bit_cast(unsigned long long, t);
+  const bool odd = n & 1u;
+  const unsigned long long ss = (unsigned long long)(n & 2u) << 62;
+  const unsigned long long cs = (unsigned long long)((n + 1u) & 2u) << 62;
+  *s = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? cr : sr) ^ ss);
+  *c = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? sr : cr) ^ cs);
 }
 // sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1), in
 // turns: 4u and its nearest integer k are exact for the 24-bit uniforms, so
@@ -918,6 +927,7 @@ template <class M, class T> struct WS {
   V3<double> zb64[M::NB];  // f64 penetration chain (f32 kernels with contact)
   double pz64[M::NB];
   double cz64[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];  // contact points' world heights
+  T ts[M::NB], tc[M::NB];  // revolute joints' sin and cos of -q (split-lane kernels)
 };
 
 // Column k, entry r of U = I_A S of body i. A free joint's S is the identity,
@@ -926,6 +936,22 @@ template <class M, class T> struct WS {
 template <class M, class T, int i> __device__ __forceinline__ T Uv(const WS<M, T>& ws, int k, int r) {
   if constexpr (M::jtype[i] == J_FREE) return sym_get(ws.IA[i], r, k);
   else return ws.U[i][k][r];
+}
+
+// A revolute joint's transform from s, c = sin, cos of -q (Rodrigues' form
+// with the axis terms precomputed on the host) and its joint velocity.
+template <class M, class T, int i>
+__device__ __forceinline__ void rev_xf(T s, T c, const T* v, Xf<T>& X, SV<T>& vj) {
+  const R3<T> Rp = R3<T>{{T(M::ptj_rot[i][0]), T(M::ptj_rot[i][1]), T(M::ptj_rot[i][2]), T(M::ptj_rot[i][3]),
+                          T(M::ptj_rot[i][4]), T(M::ptj_rot[i][5]), T(M::ptj_rot[i][6]), T(M::ptj_rot[i][7]),
+                          T(M::ptj_rot[i][8])}};
+  const T omc = T(1) - c;
+  R3<T> EJ;
+#pragma unroll
+  for (int k = 0; k < 9; k++) EJ.m[k] = T(k % 4 == 0 ? 1.0 : 0.0) + T(M::rev_k[i][k]) * s + T(M::rev_k2[i][k]) * omc;
+  X.E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
+  X.r = v3(T(M::ptj_pos[i][0]), T(M::ptj_pos[i][1]), T(M::ptj_pos[i][2]));
+  vj = SV<T>{v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[M::voff[i]], v3(T(0), T(0), T(0))};
 }
 
 // Joint transform X = X_J(q) X_ptj of body i and its joint velocity S qd
@@ -942,13 +968,7 @@ __device__ __forceinline__ void joint_xf(const T* q, const T* v, Xf<T>& X, SV<T>
   if constexpr (jt == J_REV) {
     T s, c;
     dsincos(-q[qo], &s, &c);
-    const T omc = T(1) - c;
-    R3<T> EJ;
-#pragma unroll
-    for (int k = 0; k < 9; k++) EJ.m[k] = T(k % 4 == 0 ? 1.0 : 0.0) + T(M::rev_k[i][k]) * s + T(M::rev_k2[i][k]) * omc;
-    X.E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
-    X.r = pp;
-    vj.a = v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * v[vo];
+    rev_xf<M, T, i>(s, c, v, X, vj);
   } else if constexpr (jt == J_PRIS) {
     X.E = Rp;
     X.r = pp + tmul(Rp, v3(T(M::axis[i][0]), T(M::axis[i][1]), T(M::axis[i][2])) * q[qo]);
@@ -1053,6 +1073,8 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
 #pragma unroll
     for (int cp = 0; cp < ground_pts<M>(i); cp++)
       ws.cz64[ground_off<M>(i) + cp] = ws.pz64[i] + dot(ws.zb64[i], contact_point<M, double, i>(cp, ws.zb64[i]));
+  } else if constexpr (M::LANES > 1 && M::jtype[i] == J_REV) {
+    rev_xf<M, T, i>(ws.ts[i], ws.tc[i], v, X, vj);
   } else {
     joint_xf<M, T, i>(q, v, X, vj);
   }
@@ -1359,6 +1381,53 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
 
 }
 
+// Value x of lane o of each aligned group of L lanes (L = 2 or 4), for every
+// lane of the group: one DPP quad permutation per 32-bit half.
+template <int L, int o> __device__ __forceinline__ int lane_bcast32(int x) {
+  static_assert(L == 2 || L == 4, "lane groups of 2 or 4");
+  constexpr int a = o, b = L == 2 ? 2 + o : o;
+  return __builtin_amdgcn_mov_dpp(x, a | (a << 2) | (b << 4) | (b << 6), 0xf, 0xf, false);
+}
+template <int L, int o> __device__ __forceinline__ float lane_bcast(float x) {
+  return __builtin_bit_cast(float, lane_bcast32<L, o>(__builtin_bit_cast(int, x)));
+}
+template <int L, int o> __device__ __forceinline__ double lane_bcast(double x) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+  const int lo = lane_bcast32<L, o>((int)(unsigned)u), hi = lane_bcast32<L, o>((int)(unsigned)(u >> 32));
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Split-lane kernels (LANES > 1: small launches, one lane per world would
+// leave most SIMDs idle): a world's LANES lanes hold its whole state and run
+// the whole step redundantly, except the revolute joints' sines and cosines,
+// the step's transcendental work: lane o of the group takes joints o, o +
+// LANES, ... and the results are broadcast within the group. Every lane then
+// holds the same bits as the one-lane kernel computes.
+template <class M, class T> __device__ __forceinline__ void trig_prepass(WS<M, T>& ws, const T* q, int lane) {
+  constexpr int L = M::LANES;
+  const int sub = lane & (L - 1);
+  sfor<0, (M::NREV + L - 1) / L>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    T ang = -q[M::qoff[M::rev_body[u * L]]];
+    sfor<1, L>([&](auto O) {
+      constexpr int o = decltype(O)::value;
+      if constexpr (u * L + o < M::NREV) {
+        if (sub == o) ang = -q[M::qoff[M::rev_body[u * L + o]]];
+      }
+    });
+    T sn, cs;
+    dsincos(ang, &sn, &cs);
+    sfor<0, L>([&](auto O) {
+      constexpr int o = decltype(O)::value;
+      if constexpr (u * L + o < M::NREV) {
+        constexpr int b = M::rev_body[u * L + o];
+        ws.ts[b] = lane_bcast<L, o>(sn);
+        ws.tc[b] = lane_bcast<L, o>(cs);
+      }
+    });
+  });
+}
+
 // One step of group G for one world (lane). State arrays are in registers; a
 // group reads and writes only the DOFs of its own bodies (plus the trunk's).
 template <class M, class T, int G>
@@ -1372,6 +1441,7 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
   apply_controls<M, T, G>(q, v, ctrl, tgt, rng);
 
   WS<M, T> ws;
+  if constexpr (M::LANES > 1) trig_prepass<M, T>(ws, q, lane);
   // ── pass 1: trunk (every group), then own bodies ──
   sfor<0, NT>([&](auto K) {
     constexpr int i = M::tlist[decltype(K)::value];
@@ -1714,7 +1784,8 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
 // loads the DOFs it owns and the trunk's; it stores only the DOFs it owns
 // (group 0 also stores the trunk's and the RNG state).
 template <class M, class T, int G> __device__ __forceinline__ void run_group(const StepArgs& a, int lane, T* lds) {
-  const int w = blockIdx.x * 64 + lane;
+  // Split-lane kernels give each world LANES consecutive lanes.
+  const int w = (int)(blockIdx.x * 64 + lane) / M::LANES;
   const bool live = w < a.nworld;
   if constexpr (M::PMODE != 2) {
     if (!live) return;
@@ -1803,6 +1874,9 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
     }
   }
   if (!live) return;
+  if constexpr (M::LANES > 1) {
+    if ((lane & (M::LANES - 1)) != 0) return;  // the group's first lane stores
+  }
   // Addresses for the final stores computed afresh: reusing the loads' per-DOF
   // addresses would keep them live through every step of the launch.
   asm volatile("" : "+s"(gq), "+s"(gv), "+s"(gc));

@@ -164,6 +164,7 @@ struct Features {
   // The launch's workgroups of 64 worlds and the device's CUs (phz_sim_create),
   // for the partition plan.
   int wgs = 0, cus = 256;
+  bool f64 = false;  // the sim's precision (the planner keeps f64 subtrees one per wave)
   // Terms of the CPU model that the device body table has no slots for
   // (joint.rs:27-104, model.rs:18-82): the soft position limit and dry friction
   // of one-DOF joints (one entry per body; empty: none), and actuators (empty:
@@ -342,6 +343,7 @@ Plan plan_partition(const ModelD& m, const Features& f) {
     std::vector<std::vector<int>> g = pack(cap);
     return g.size() == 3 ? pack(2) : g;
   };
+  const std::vector<std::vector<int>> unmerged = pack((int)parts.size());
   if (const char* e = std::getenv("PHZ_MAX_GROUPS")) {
     // Rounded down to 1, 2, 4 or 8, the caps the planner itself tries.
     const int want = std::atoi(e);
@@ -358,6 +360,19 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   }
   if (parts.size() == 3) return lane_per_world();  // unreachable: pack(2) holds at most two
   if (parts.size() < 2) return lane_per_world();
+  // f64: no wave runs two subtrees. Merged f64 plans of the MJCF humanoid (two
+  // and three waves) gave NaN or launch-varying results from launches of many
+  // steps while the same binaries stepped one step per launch matched the
+  // lane-per-world kernel; their kernels spill several hundred bytes per lane.
+  // The unmerged plan (one subtree per wave) is taken instead when it has a
+  // wave count the planner uses, else one lane per world.
+  if (f.f64 && parts.size() < unmerged.size()) {
+    if (unmerged.size() == 2 || unmerged.size() == 4 || (unmerged.size() > 4 && unmerged.size() <= 8)) {
+      parts = unmerged;
+    } else {
+      return lane_per_world();
+    }
+  }
   pl.mode = mode;
   for (int i = 0; i < nb; i++) if (trunk[i]) pl.trunk.push_back(i);
   for (auto& p : parts) {
@@ -365,6 +380,25 @@ Plan plan_partition(const ModelD& m, const Features& f) {
     pl.groups.push_back(p);
   }
   return pl;
+}
+
+// Lanes per world of the step kernel. A launch of few worlds leaves most SIMDs
+// idle (4096 worlds are 64 waves on 1024 SIMDs), and a one-lane kernel then
+// runs at the latency of its own instruction stream: such launches give each
+// world 2 or 4 lanes that split the revolute joints' sincos (see
+// trig_prepass in phz_device.h) when the split waves still fit one per SIMD.
+// Contact, partitioned plans and trees with fewer than two revolute joints
+// keep one lane. PHZ_LANES=1 turns the split off.
+int lanes_per_world(const ModelD& m, const Features& f, const Plan& pl) {
+  if (const char* e = std::getenv("PHZ_LANES"))
+    if (std::atoi(e) <= 1) return 1;
+  if (pl.mode != 0 || pl.groups.size() != 1 || f.contact) return 1;
+  int nrev = 0;
+  for (int i = 0; i < m.nb; i++) nrev += m.b[i].jtype == 0;
+  if (nrev < 2) return 1;
+  const int L = nrev == 2 ? 2 : 4;
+  if ((long)std::max(f.wgs, 1) * L > 4L * std::max(f.cus, 1)) return 1;
+  return L;
 }
 
 std::string gen_model(const ModelD& m, const Features& f) {
@@ -460,6 +494,14 @@ std::string gen_model(const ModelD& m, const Features& f) {
     << ", MAXD = " << std::max(maxnd, 1) << ";\n";
   o << "  static constexpr int PMODE = " << pl.mode << ", NG = " << ng << ", NTRUNK = " << pl.trunk.size()
     << ", MAXG = " << maxg << ", NSLOT = " << nslot << ", slot_state = " << slot_state << ";\n";
+  {
+    std::vector<int> rev;
+    for (int i = 0; i < nb; i++) if (m.b[i].jtype == 0) rev.push_back(i);
+    const int nr = std::max((int)rev.size(), 1);
+    o << "  static constexpr int LANES = " << lanes_per_world(m, f, pl) << ", NREV = " << rev.size() << ";\n";
+    o << "  static constexpr int rev_body[" << nr << "] = "
+      << arr1(nr, [&](int k) { return std::to_string(rev.empty() ? 0 : rev[k]); }) << ";\n";
+  }
   const int nta = std::max((int)pl.trunk.size(), 1);
   o << "  static constexpr int tlist[" << nta << "] = "
     << arr1(nta, [&](int k) { return std::to_string(pl.trunk.empty() ? 0 : pl.trunk[k]); }) << ";\n";
@@ -594,9 +636,11 @@ std::string gen_model(const ModelD& m, const Features& f) {
 }
 
 // One workgroup = NG waves over the same 64 worlds; wave g runs group g.
-std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups) {
-  const int ng = (int)plan_partition(m, f).groups.size();
+std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups, int* lanes) {
+  const Plan pl = plan_partition(m, f);
+  const int ng = (int)pl.groups.size();
   *ngroups = ng;
+  *lanes = lanes_per_world(m, f, pl);
   const std::string T = f64 ? "double" : "float";
   std::string s = kDeviceSrc;
   s += "\n// ---- model-specialised instantiation ----\n";
@@ -1018,6 +1062,7 @@ struct phz_sim {
   bool f64 = false;
   int device = -1;
   int block = 64;
+  int lanes = 1;  // lanes per world of the step kernel
   int max_steps = 1000;
   hipStream_t stream = nullptr;
   void *q = nullptr, *v = nullptr, *ctrl = nullptr, *qdd = nullptr, *targets = nullptr, *rows = nullptr;
@@ -1116,7 +1161,7 @@ struct phz_sim {
     if (code) return true;
     std::string e;
     int ng = 1;
-    const std::string src = gen_source(model, feat, f64, &ng);
+    const std::string src = gen_source(model, feat, f64, &ng, &lanes);
     block = 64 * ng;
     if (const char* dump = std::getenv("PHZ_DUMP_SOURCE")) {
       std::ofstream out(dump);
@@ -1137,7 +1182,7 @@ struct phz_sim {
                hf_buf,  feat.hf_o[0], feat.hf_o[1], feat.hf_o[2], feat.hf_cell, feat.hf_nx, feat.hf_ny, nworld,
                stride,  nsteps,  feat.contact ? 1 : 0};
     void* params[] = {&a};
-    const unsigned grid = (unsigned)((nworld + 63) / 64);
+    const unsigned grid = (unsigned)(((long)nworld * lanes + 63) / 64);
     return hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
                   "step kernel launch");
   }
@@ -1496,6 +1541,7 @@ int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t 
       cus = 256;
     s->feat.wgs = s->stride / 64;
     s->feat.cus = std::max(cus, 1);
+    s->feat.f64 = s->f64;
   }
   *out = s.release();
   return 0;
@@ -1945,6 +1991,12 @@ int phz_time_step_many(phz_sim* s, uint32_t n, uint32_t reps, double* ms_per_rep
   }
   for (auto& e : ev) hipEventDestroy(e);
   return ok ? 0 : 1;
+}
+
+int phz_lanes_per_world(phz_sim* s) {
+  if (!s) return -1;
+  if (!s->compile()) return -1;
+  return s->lanes;
 }
 
 int phz_kernel_info(phz_sim* s, int64_t* info) {

@@ -282,7 +282,9 @@ class BatchSim:
         info = (C.c_int64 * 6)()
         self._check(self._L.phz_kernel_info(self._h, info))
         keys = ("vgpr", "agpr", "sgpr", "scratch_bytes", "block", "max_steps_per_launch")
-        return dict(zip(keys, [int(x) for x in info]))
+        out = dict(zip(keys, [int(x) for x in info]))
+        out["lanes_per_world"] = int(self._L.phz_lanes_per_world(self._h))
+        return out
 
     def time_step_many(self, n: int, reps: int) -> np.ndarray:
         ms = np.zeros(reps)

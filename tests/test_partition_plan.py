@@ -24,6 +24,8 @@ from phyz_amd.sim import from_workload
     (9, 16384, "f32", 256),   # MJCF hand: 4 waves
     (4, 32768, "f32", 256),   # builder humanoid: 4 waves (trunk+arm 6, arm 4, legs 6 and 6)
     (5, 16384, "f64", 320),   # builder hand (welded palm, no barrier): 5 waves
+    (8, 32768, "f64", 256),   # MJCF humanoid f64: one wave per subtree, never merged
+    (9, 16384, "f64", 320),   # MJCF hand f64: one wave per finger, never merged
 ])
 def test_waves_per_world_group(index, nworld, prec, block):
     s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
@@ -70,3 +72,38 @@ def test_no_three_wave_plan(base, links, nworld, max_groups, monkeypatch):
     s = BatchSim(m, nworld, "f64", device=-1)
     s.compile()
     assert s.kernel_info()["block"] in (64, 128), s.kernel_info()
+
+
+@pytest.mark.parametrize("index,block", [(8, 256), (9, 320)])
+def test_f64_never_merges_subtrees(index, block, monkeypatch):
+    """A cap below the subtree count merges subtrees into one wave in f32 only:
+    in f64 the planner keeps one subtree per wave (the MJCF humanoid's merged
+    f64 kernels gave NaN or launch-varying values from launches of many
+    steps)."""
+    monkeypatch.setenv("PHZ_MAX_GROUPS", "2")
+    s32 = from_workload(W.config(index), "f32", nworld=96, device=-1)
+    s32.compile()
+    assert s32.kernel_info()["block"] == 128
+    s64 = from_workload(W.config(index), "f64", nworld=96, device=-1)
+    s64.compile()
+    assert s64.kernel_info()["block"] == block
+
+
+@pytest.mark.parametrize("index,nworld,lanes", [
+    (1, 4096, 2),     # double pendulum, 64 workgroups: two lanes per world
+    (2, 1024, 4),     # chain7 at 1024 worlds: four lanes
+    (2, 65536, 1),    # chain7 at 65536 worlds fills the SIMDs already
+    (3, 1024, 1),     # contact keeps one lane
+])
+def test_lanes_per_world(index, nworld, lanes, monkeypatch):
+    """Small launches split each world's revolute-joint sincos over 2 or 4
+    lanes when the split waves still fit one per SIMD; PHZ_LANES=1 turns the
+    split off."""
+    monkeypatch.delenv("PHZ_LANES", raising=False)
+    s = from_workload(W.config(index), "f64", nworld=nworld, device=-1)
+    s.compile()
+    assert s.kernel_info()["lanes_per_world"] == lanes
+    monkeypatch.setenv("PHZ_LANES", "1")
+    s = from_workload(W.config(index), "f64", nworld=nworld, device=-1)
+    s.compile()
+    assert s.kernel_info()["lanes_per_world"] == 1
