@@ -15,6 +15,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -1203,7 +1204,10 @@ struct phz_sim {
     if (n == 0) return true;
     if (nworld == 0) return true;
     if (!load_kernel()) return false;
-    if (!graphs) return issue(n);
+    // A span of one launch goes straight to the stream: replaying a one-node
+    // graph costs about 5 us more per span on MI355X (86.5 against 81.8 us
+    // wall for 20 chain steps at 65536 worlds).
+    if (!graphs || n <= (uint32_t)max_steps) return issue(n);
     if (!(gexec && graph_steps == n && graph_epoch == epoch)) {
       drop_graph();
       if (!hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"))
@@ -1884,6 +1888,15 @@ int phz_synchronize(phz_sim* s) {
   if (!s) return 1;
   if (!s->has_device()) return 0;
   if (!set_device(s)) return 1;
+  // Poll the stream for up to 200 us before blocking: a blocking wait wakes
+  // the host about 10 us after a short span ends.
+  const auto t0 = std::chrono::steady_clock::now();
+  for (;;) {
+    const hipError_t e = hipStreamQuery(s->stream);
+    if (e == hipSuccess) return 0;
+    if (e != hipErrorNotReady) return s->hip_ok(e, "synchronize") ? 0 : 1;
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(200)) break;
+  }
   return s->hip_ok(hipStreamSynchronize(s->stream), "synchronize") ? 0 : 1;
 }
 
