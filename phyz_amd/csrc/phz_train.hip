@@ -66,36 +66,66 @@ struct Dims {
   __host__ __device__ uint32_t tW2() const { return n_h * n_in; }
   __host__ __device__ uint32_t tW3() const { return tW2() + n_h * n_h; }
   __host__ __device__ uint32_t t_size() const { return tW3() + n_h * n_out; }
-  // Largest weight matrix, in floats.
-  __host__ __device__ uint32_t max_matrix() const {
-    const uint32_t a = n_in * n_h, b = n_h * n_h, c = n_h * n_out;
-    return a > b ? (a > c ? a : c) : (b > c ? b : c);
-  }
 };
 
 __host__ __device__ inline uint32_t pad4(uint32_t x) { return (x + 3u) & ~3u; }
+// LDS row stride of a row of k values, in floats: k rounded up to whole
+// 16-column blocks (the matrix-core loops read 16 columns per step, so the
+// padding must exist and hold zeros), then the first value = 20 (mod 32)
+// beyond it. An odd number of float4s puts the 16 rows that one ds_read_b128
+// of a 16 x 16 block touches in distinct bank groups, and the offset 20
+// keeps the 4 consecutive rows that one ds_read_b32 of the gradient blocks
+// touches apart (one row stride of 64 floats had put all 16 rows of a block
+// on one bank).
+__host__ __device__ inline uint32_t row_stride(uint32_t k) {
+  const uint32_t s = ((k + 15u) & ~15u) + 4u;
+  return s % 32u == 4u ? s + 16u : s;
+}
 
 // How a tile workgroup reads the weights: all five matrices staged into LDS
 // at the start (one load phase), one layer at a time through a staging buffer,
 // or straight from the mirrors in HBM (networks too wide for the LDS).
 enum { STAGE_ALL = 0, STAGE_LAYER = 1, STAGE_NONE = 2 };
 
-// LDS of one tile workgroup, in floats; rows padded to whole float4s:
+// A network's weights as the tile kernels hold them in LDS: W1 [n_h][lx],
+// W2 [n_h][lh], W3 [n_out][lh] (forward: rows along the summed input), W3t
+// [n_h][lo], W2t [n_h][lh] (backprop), each row padded with zeros to its
+// row_stride, then the biases b1, b2 [n_h] and b3 [n_out], each padded to a
+// float4. The Adam kernel keeps a copy of this image in HBM, so a tile
+// stages it with coalesced 16-byte loads and no index arithmetic.
+struct WImg {
+  uint32_t lx, lh, lo, w_1, w_2, w_3, w_3t, w_2t, b_1, b_2, b_3, size;
+  __host__ __device__ explicit WImg(const Dims& d)
+      : lx(row_stride(d.n_in)), lh(row_stride(d.n_h)), lo(row_stride(d.n_out)) {
+    w_1 = 0;
+    w_2 = w_1 + d.n_h * lx;
+    w_3 = w_2 + d.n_h * lh;
+    w_3t = w_3 + d.n_out * lh;
+    w_2t = w_3t + d.n_h * lo;
+    b_1 = w_2t + d.n_h * lh;
+    b_2 = b_1 + pad4(d.n_h);
+    b_3 = b_2 + pad4(d.n_h);
+    size = b_3 + pad4(d.n_out);
+  }
+};
+
+// LDS of one tile workgroup, in floats; row strides from row_stride:
 // X [R][lx], H1, H2, DA, DB [R][lh], OUT [R][lo] (the output, then dL/dout),
 // ACT [R][lo] (the rows' actions), DLS [R][lo] (per-row dL/dlog_std), RV
 // [R][4] (per-row advantage, old log-prob, return), RS [R][4] (per-row
-// statistics), SD and LSD [lo] (std and log std), then the weights:
-// STAGE_ALL  W1t [n_in][n_h], W2t [n_h][n_h], W3t [n_h][n_out], W3 [n_out][n_h],
-//            W2 [n_h][n_h] at WB + w_*;
-// STAGE_LAYER one [K][N] matrix at a time at WB (max_matrix floats).
+// statistics), SD and LSD [lo] (std and log std), then the weights, each
+// matrix with rows along the summed index and zero padding:
+// STAGE_ALL  W1 [n_h][lx], W2 [n_h][lh], W3 [n_out][lh] (forward),
+//            W3t [n_h][lo], W2t [n_h][lh] (backprop) at WB + w_*;
+// STAGE_LAYER one of them at a time at WB.
 struct Lds {
   uint32_t lx, lh, lo;
   uint32_t X, H1, H2, DA, DB, OUT, ACT, DLS, RV, RS, SD, LSD, WB, total;
-  uint32_t w_1t, w_2t, w_3t, w_3, w_2;
+  uint32_t w_1, w_2, w_3, w_3t, w_2t, b_1, b_2, b_3;
   __host__ __device__ Lds(const Dims& d, uint32_t R, int mode) {
-    lx = pad4(d.n_in);
-    lh = pad4(d.n_h);
-    lo = pad4(d.n_out);
+    lx = row_stride(d.n_in);
+    lh = row_stride(d.n_h);
+    lo = row_stride(d.n_out);
     X = 0;
     H1 = X + R * lx;
     H2 = H1 + R * lh;
@@ -109,13 +139,20 @@ struct Lds {
     SD = RS + R * 4;
     LSD = SD + lo;
     WB = LSD + lo;
-    w_1t = 0;
-    w_2t = pad4(w_1t + d.n_in * d.n_h);
-    w_3t = pad4(w_2t + d.n_h * d.n_h);
-    w_3 = pad4(w_3t + d.n_h * d.n_out);
-    w_2 = pad4(w_3 + d.n_out * d.n_h);
-    const uint32_t all = pad4(w_2 + d.n_h * d.n_h);
-    total = WB + (mode == STAGE_ALL ? all : mode == STAGE_LAYER ? pad4(d.max_matrix()) : 0u);
+    const WImg im(d);
+    w_1 = im.w_1;
+    w_2 = im.w_2;
+    w_3 = im.w_3;
+    w_3t = im.w_3t;
+    w_2t = im.w_2t;
+    b_1 = im.b_1;
+    b_2 = im.b_2;
+    b_3 = im.b_3;
+    const uint32_t all = im.size;
+    uint32_t one = d.n_h * (lx > lh ? lx : lh);  // the largest staged matrix
+    one = one > d.n_out * lh ? one : d.n_out * lh;
+    one = one > d.n_h * lo ? one : d.n_h * lo;
+    total = WB + (mode == STAGE_ALL ? all : mode == STAGE_LAYER ? one : 0u);
   }
 };
 
@@ -123,6 +160,7 @@ struct TileArgs {
   const float* x[2];      // obs_a [n_rows][n_in], obs_c [n_rows][n_in]
   const float* w[2];      // row-major f32 mirrors
   const float* wt[2];     // transposed f32 mirrors of the weight matrices
+  const float* img[2];    // padded weight images (WImg)
   double* part[2];        // [tile][n_param] f64 partial gradients
   Dims dims[2];
   uint32_t n_param[2];
@@ -208,6 +246,65 @@ __device__ void dense(const float* __restrict__ X, uint32_t ldx, uint32_t K, con
   }
 }
 
+// The same layer with both operands in LDS (staged modes), four inputs per
+// lane per load: Wr is [N][ldw], row j holding output j's weights along the
+// summed index (the row-major matrix for a forward layer, the transposed one
+// for a backprop), X is [R][ldx]; both have zeros from K up to the next
+// multiple of 16. For each 16 inputs k0..k0+15, lane l loads the float4s
+// X[r0 + l%16][k0 + 4(l/16) ..] and Wr[j0 + l%16][k0 + 4(l/16) ..] (one
+// ds_read_b128 each) and component s feeds the s-th of four
+// v_mfma_f32_16x16x4: that product sums k0 + 4q + s over q = 0..3, so the four
+// cover the 16 inputs once. Blocks are dealt to the waves in row-major order
+// without a division.
+template <int EPI>
+__device__ void dense4(const float* __restrict__ X, uint32_t ldx, uint32_t K, const float* __restrict__ Wr,
+                       uint32_t ldw, uint32_t N, const float* __restrict__ bias, const float* __restrict__ H,
+                       uint32_t ldh, float* __restrict__ Y, uint32_t ldy, uint32_t R) {
+  const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
+  const uint32_t lr = lane / 16u, lc = lane % 16u;
+  constexpr uint32_t kWaves = kTileThreads / 64u;
+  uint32_t blk = 0;
+  for (uint32_t r0 = 0; r0 < R; r0 += 16u)
+    for (uint32_t j0 = 0; j0 < N; j0 += 16u, blk++) {
+      if (blk % kWaves != wave) continue;
+      const uint32_t ra = r0 + lc < R ? r0 + lc : R - 1u;
+      const uint32_t jb = j0 + lc < N ? j0 + lc : N - 1u;
+      const float init = EPI == EPI_DTANH ? 0.0f : bias[jb];
+      // Two accumulators (components 0, 2 and 1, 3) halve the chain of
+      // dependent MFMAs; the next 16 inputs load while these multiply (the
+      // last prefetch re-reads the final block, in bounds).
+      float4_t acc = {init, init, init, init}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const float* xa = X + ra * ldx + 4u * lr;
+      const float* wb = Wr + jb * ldw + 4u * lr;
+      float4_t a = *reinterpret_cast<const float4_t*>(xa);
+      float4_t b = *reinterpret_cast<const float4_t*>(wb);
+      for (uint32_t k0 = 0; k0 < K; k0 += 16u) {
+        const uint32_t kn = k0 + 16u < K ? k0 + 16u : k0;
+        const float4_t an = *reinterpret_cast<const float4_t*>(xa + kn);
+        const float4_t bn = *reinterpret_cast<const float4_t*>(wb + kn);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc2, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc2, 0, 0, 0);
+        a = an;
+        b = bn;
+      }
+      acc += acc2;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const uint32_t r = r0 + 4u * lr + v, j = j0 + lc;
+        if (r >= R || j >= N) continue;
+        float y = acc[v];
+        if (EPI == EPI_TANH) y = act_tanh(y);
+        if (EPI == EPI_DTANH) {
+          const float h = H[r * ldh + j];
+          y = y * (1.0f - h * h);
+        }
+        Y[r * ldy + j] = y;
+      }
+    }
+}
+
 typedef double double4_t __attribute__((ext_vector_type(4)));
 
 // Tile partials of a linear layer's gradients, Gw[o][i] = sum_r D[r][o] X[r][i]
@@ -225,23 +322,38 @@ __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O
                            uint32_t ldx, uint32_t I, uint32_t R, double* __restrict__ Gw, double* __restrict__ Gb) {
   const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
   const uint32_t lr = lane / 16u, lc = lane % 16u;
-  const uint32_t OB = (O + 15u) / 16u, IB = (I + 15u) / 16u;
-  for (uint32_t blk = wave; blk < OB * IB; blk += kTileThreads / 64u) {
-    const uint32_t ob = blk / IB, o0 = ob * 16u, i0 = (blk - ob * IB) * 16u;
-    const uint32_t oa = o0 + lc < O ? o0 + lc : O - 1u;
-    const uint32_t ia = i0 + lc < I ? i0 + lc : I - 1u;
-    double4_t acc = {0.0, 0.0, 0.0, 0.0};
-    for (uint32_t r0 = 0; r0 < R; r0 += 4u) {
-      const double av = (double)D[(r0 + lr) * ldd + oa];
-      const double bv = (double)X[(r0 + lr) * ldx + ia];
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
-    }
+  constexpr uint32_t kWaves = kTileThreads / 64u;
+  uint32_t blk = 0;
+  for (uint32_t o0 = 0; o0 < O; o0 += 16u)
+    for (uint32_t i0 = 0; i0 < I; i0 += 16u, blk++) {
+      if (blk % kWaves != wave) continue;
+      const uint32_t oa = o0 + lc < O ? o0 + lc : O - 1u;
+      const uint32_t ia = i0 + lc < I ? i0 + lc : I - 1u;
+      // Sixteen rows per round: the eight LDS reads first, then four MFMAs
+      // alternating between two accumulators (R is a multiple of 8).
+      double4_t acc = {0.0, 0.0, 0.0, 0.0}, acc2 = {0.0, 0.0, 0.0, 0.0};
+      for (uint32_t r0 = 0; r0 < R; r0 += 16u) {
+        double av[4], bv[4];
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const uint32_t o = o0 + lr + 4u * v, i = i0 + lc;
-      if (o < O && i < I) Gw[(size_t)o * I + i] = acc[v];
+        for (uint32_t q = 0; q < 4u; q++) {
+          const uint32_t r = r0 + 4u * q + lr < R ? r0 + 4u * q + lr : lr;
+          av[q] = (double)D[r * ldd + oa];
+          bv[q] = (double)X[r * ldx + ia];
+        }
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[0], bv[0], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[1], bv[1], acc2, 0, 0, 0);
+        if (r0 + 8u < R) {
+          acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[2], bv[2], acc, 0, 0, 0);
+          acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[3], bv[3], acc2, 0, 0, 0);
+        }
+      }
+      acc += acc2;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const uint32_t o = o0 + lr + 4u * v, i = i0 + lc;
+        if (o < O && i < I) Gw[(size_t)o * I + i] = acc[v];
+      }
     }
-  }
   for (uint32_t t = threadIdx.x; t < 4u * ((O + 15u) & ~15u); t += kTileThreads) {
     const uint32_t o = t / 4u, p = t % 4u;
     double acc = 0.0;
@@ -253,28 +365,26 @@ __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O
   }
 }
 
-// count floats from global memory into LDS, eight loads in flight per thread
-// (each from a clamped, in-bounds address) before any of them is stored.
-__device__ void copy_batched(float* __restrict__ dst, const float* __restrict__ src, uint32_t count) {
+// count floats (a multiple of 4, 16-byte aligned at both ends) from global
+// memory into LDS, eight 16-byte loads in flight per thread.
+__device__ void copy4(float* __restrict__ dst, const float* __restrict__ src, uint32_t count) {
   constexpr uint32_t U = 8;
-  for (uint32_t base = threadIdx.x; base < count; base += U * kTileThreads) {
-    float v[U];
+  const uint32_t n4 = count / 4u;
+  const float4_t* s4 = reinterpret_cast<const float4_t*>(src);
+  float4_t* d4 = reinterpret_cast<float4_t*>(dst);
+  for (uint32_t base = threadIdx.x; base < n4; base += U * kTileThreads) {
+    float4_t v[U];
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) {
       const uint32_t e = base + u * kTileThreads;
-      v[u] = src[e < count ? e : count - 1u];
+      v[u] = s4[e < n4 ? e : 0u];
     }
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) {
       const uint32_t e = base + u * kTileThreads;
-      if (e < count) dst[e] = v[u];
+      if (e < n4) d4[e] = v[u];
     }
   }
-}
-
-// One layer's [K][N] weights into the LDS staging buffer.
-__device__ void stage(float* __restrict__ WB, const float* __restrict__ src, uint32_t count) {
-  copy_batched(WB, src, count);
 }
 
 __device__ inline float clampf(float x, float lo, float hi) { return x < lo ? lo : (x > hi ? hi : x); }
@@ -307,94 +417,101 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
   const float* wt = a.wt[net];
   double* part = a.part[net] + (size_t)blockIdx.x * a.n_param[net];
   const float* x = a.x[net];
-  // Each matrix's source: its LDS copy (STAGE_ALL), the staging buffer
-  // (STAGE_LAYER, loaded just before use) or the mirror in HBM.
-  auto src = [&](uint32_t lds_off, const float* global) -> const float* {
-    return MODE == STAGE_ALL ? WB + lds_off : MODE == STAGE_LAYER ? WB : global;
-  };
-  auto stage_layer = [&](const float* global, uint32_t count) {
-    if (MODE == STAGE_LAYER) {
-      __syncthreads();
-      stage(WB, global, count);
-      __syncthreads();
-    }
+  const float* img = a.img[net];
+  // A forward layer's weights for the matrix-core loop: the LDS copy
+  // (STAGE_ALL) or the staging buffer, loaded here from the weight image
+  // (STAGE_LAYER; every wave is past the previous layer's reads at the first
+  // barrier).
+  auto staged = [&](uint32_t off, uint32_t rows_, uint32_t ld) -> const float* {
+    if (MODE == STAGE_ALL) return WB + off;
+    __syncthreads();
+    copy4(WB, img + off, rows_ * ld);
+    __syncthreads();
+    return WB;
   };
 
-  // ── gather the tile's rows (the minibatch is an index list into the batch),
-  //    the rows' actions and scalars, and the weights: the row indices first,
-  //    then each copy with several loads in flight per thread ──
-  uint32_t* IDX = reinterpret_cast<uint32_t*>(RS);  // RS is free until the loss pass
-  for (uint32_t r = threadIdx.x; r < R; r += kTileThreads) IDX[r] = r < rows ? a.idx[row0 + r] : 0u;
-  if (net == 0) {
-    for (uint32_t k = threadIdx.x; k < d.n_out; k += kTileThreads) {
-      const float sd = expf(w[d.mlp_params() + k]);
-      SD[k] = sd;
-      LSD[k] = logf(sd);
-    }
-  }
-  __syncthreads();
-  // Rows: one wave per row, lanes over columns, four rows' loads in flight.
-  const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
+  // A layer's biases: the image's LDS copy (STAGE_ALL) or the f32 mirror.
+  auto bias = [&](uint32_t off, uint32_t q) -> const float* { return MODE == STAGE_ALL ? WB + off : w + q; };
+
+  // ── the tile's inputs: its rows (the minibatch is an index list into the
+  //    batch), their actions and scalars, and the weight image. Every global
+  //    load of the first batch is issued before any LDS store. ──
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64u), lane = threadIdx.x % 64u;
   constexpr uint32_t kWaves = kTileThreads / 64u;
-  for (uint32_t c0 = 0; c0 < L.lx; c0 += 64u) {
-    const uint32_t i = c0 + lane, ic = i < d.n_in ? i : d.n_in - 1u;
-    for (uint32_t r0 = wave; r0 < R; r0 += 4u * kWaves) {
-      float v[4];
+  constexpr uint32_t kImgU = 12;  // float4s of the image per thread in the first batch
+  const float4_t* img4 = reinterpret_cast<const float4_t*>(img);
+  float4_t* WB4 = reinterpret_cast<float4_t*>(WB);
+  const uint32_t n4 = MODE == STAGE_ALL ? WImg(d).size / 4u : 0u;
+  float4_t wv[kImgU];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t r = r0 + q * kWaves;
-        v[q] = r < R ? x[(size_t)IDX[r < R ? r : 0u] * d.n_in + ic] : 0.0f;
-      }
+  for (uint32_t u = 0; u < kImgU; u++) {
+    const uint32_t e = threadIdx.x + u * kTileThreads;
+    wv[u] = img4[e < n4 ? e : 0u];
+  }
+  // Zero H1, H2, DA, DB and OUT, whose padding columns the matrix-core loops
+  // read (against zero weights, but an uninitialised NaN would survive the
+  // product); nothing else writes them before the barrier below.
+  for (uint32_t e = L.H1 + 4u * threadIdx.x; e < L.ACT; e += 4u * kTileThreads)
+    *reinterpret_cast<float4_t*>(lds + e) = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // Rows: wave w takes rows w, w + 8, ...; its lanes run over 64-column chunks.
+  const uint32_t nchunk = (L.lx + 63u) / 64u, nrw = (R + kWaves - 1u) / kWaves;
+  const uint32_t nt = nrw * nchunk;
+  float sdv = 0.0f;
+  if (net == 0 && threadIdx.x < d.n_out) sdv = w[d.mlp_params() + threadIdx.x];
+  for (uint32_t t0 = 0; t0 < nt; t0 += 8u) {
+    float xv[8], av[8], rv[8];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t r = r0 + q * kWaves;
-        if (r < R && i < L.lx) X[r * L.lx + i] = (r < rows && i < d.n_in) ? v[q] : 0.0f;
+    for (uint32_t u = 0; u < 8u; u++) {
+      const uint32_t t = t0 + u, q = t / nchunk, i = (t - q * nchunk) * 64u + lane, r = wave + kWaves * q;
+      const bool live = t < nt && r < rows;
+      const uint32_t sidx = live ? a.idx[row0 + r] : 0u;
+      xv[u] = live && i < d.n_in ? x[(size_t)sidx * d.n_in + i] : 0.0f;
+      const bool first = t < nt && t - q * nchunk == 0u;  // one chunk per row fetches the row's extras
+      av[u] = net == 0 && live && first && lane < d.n_out ? a.act[(size_t)sidx * d.n_out + lane] : 0.0f;
+      const float* sc = net == 0 ? (lane == 0 ? a.adv : a.logp_old) : a.ret;
+      rv[u] = live && first && lane < (net == 0 ? 2u : 1u) ? sc[sidx] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; u++) {
+      const uint32_t t = t0 + u, q = t / nchunk, i = (t - q * nchunk) * 64u + lane, r = wave + kWaves * q;
+      if (t >= nt || r >= R) continue;
+      if (i < L.lx) X[r * L.lx + i] = xv[u];  // zero past n_in
+      if (t - q * nchunk == 0u) {
+        if (net == 0 && lane < d.n_out) ACT[r * L.lo + lane] = av[u];
+        if (lane < (net == 0 ? 2u : 1u)) RV[r * 4 + (net == 0 ? lane : 2u)] = rv[u];
       }
     }
   }
-  if (net == 0) {
-    for (uint32_t r0 = wave; r0 < R; r0 += 4u * kWaves) {
-      const uint32_t kc = lane < d.n_out ? lane : d.n_out - 1u;
-      float v[4];
+  if (net == 0 && threadIdx.x < d.n_out) {
+    const float sd = expf(sdv);
+    SD[threadIdx.x] = sd;
+    LSD[threadIdx.x] = logf(sd);
+  }
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t r = r0 + q * kWaves;
-        v[q] = r < R ? a.act[(size_t)IDX[r < R ? r : 0u] * d.n_out + kc] : 0.0f;
-      }
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t r = r0 + q * kWaves;
-        if (r < R && lane < L.lo) ACT[r * L.lo + lane] = (r < rows && lane < d.n_out) ? v[q] : 0.0f;
-      }
-    }
+  for (uint32_t u = 0; u < kImgU; u++) {
+    const uint32_t e = threadIdx.x + u * kTileThreads;
+    if (e < n4) WB4[e] = wv[u];
   }
-  for (uint32_t r = threadIdx.x; r < rows; r += kTileThreads) {
-    const uint32_t sidx = IDX[r];
-    if (net == 0) {
-      RV[r * 4 + 0] = a.adv[sidx];
-      RV[r * 4 + 1] = a.logp_old[sidx];
-    } else {
-      RV[r * 4 + 2] = a.ret[sidx];
-    }
-  }
-  if (MODE == STAGE_ALL) {
-    copy_batched(WB + L.w_1t, wt, d.n_in * d.n_h);
-    copy_batched(WB + L.w_2t, wt + d.tW2(), d.n_h * d.n_h);
-    copy_batched(WB + L.w_3t, wt + d.tW3(), d.n_h * d.n_out);
-    copy_batched(WB + L.w_3, w + d.oW3(), d.n_out * d.n_h);
-    copy_batched(WB + L.w_2, w + d.oW2(), d.n_h * d.n_h);
-  }
-  if (MODE == STAGE_LAYER) stage(WB, wt, d.n_in * d.n_h);
+  for (uint32_t e = threadIdx.x + kImgU * kTileThreads; e < n4; e += kTileThreads) WB4[e] = img4[e];
   __syncthreads();
 
   // ── forward (phyz_train.cu:101-133) ──
-  dense<EPI_TANH>(X, L.lx, d.n_in, src(L.w_1t, wt), d.n_h, w + d.ob1(), nullptr, 0, H1, L.lh, R);
-  stage_layer(wt + d.tW2(), d.n_h * d.n_h);
-  if (MODE != STAGE_LAYER) __syncthreads();
-  dense<EPI_TANH>(H1, L.lh, d.n_h, src(L.w_2t, wt + d.tW2()), d.n_h, w + d.ob2(), nullptr, 0, H2, L.lh, R);
-  stage_layer(wt + d.tW3(), d.n_h * d.n_out);
-  if (MODE != STAGE_LAYER) __syncthreads();
-  dense<EPI_LINEAR>(H2, L.lh, d.n_h, src(L.w_3t, wt + d.tW3()), d.n_out, w + d.ob3(), nullptr, 0, OUT, L.lo, R);
+  if (MODE == STAGE_NONE) {
+    dense<EPI_TANH>(X, L.lx, d.n_in, wt, d.n_h, w + d.ob1(), nullptr, 0, H1, L.lh, R);
+    __syncthreads();
+    dense<EPI_TANH>(H1, L.lh, d.n_h, wt + d.tW2(), d.n_h, w + d.ob2(), nullptr, 0, H2, L.lh, R);
+    __syncthreads();
+    dense<EPI_LINEAR>(H2, L.lh, d.n_h, wt + d.tW3(), d.n_out, w + d.ob3(), nullptr, 0, OUT, L.lo, R);
+  } else {
+    dense4<EPI_TANH>(X, L.lx, d.n_in, staged(L.w_1, d.n_h, L.lx), L.lx, d.n_h, bias(L.b_1, d.ob1()),
+                     nullptr, 0, H1, L.lh, R);
+    if (MODE == STAGE_ALL) __syncthreads();
+    dense4<EPI_TANH>(H1, L.lh, d.n_h, staged(L.w_2, d.n_h, L.lh), L.lh, d.n_h, bias(L.b_2, d.ob2()),
+                     nullptr, 0, H2, L.lh, R);
+    if (MODE == STAGE_ALL) __syncthreads();
+    dense4<EPI_LINEAR>(H2, L.lh, d.n_h, staged(L.w_3, d.n_out, L.lh), L.lh, d.n_out,
+                       bias(L.b_3, d.ob3()), nullptr, 0, OUT, L.lo, R);
+  }
   __syncthreads();
 
   // ── loss gradient; OUT becomes dL/dout ──
@@ -463,7 +580,7 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
       OUT[r * L.lo] = 2.0f * clampf(err, -a.vdelta, a.vdelta) / fb;
     }
   }
-  if (MODE == STAGE_LAYER) stage(WB, w + d.oW3(), d.n_out * d.n_h);
+  if (MODE == STAGE_LAYER) copy4(WB, img + L.w_3t, d.n_h * L.lo);  // W3 transposed, for dL/dh2
   __syncthreads();
 
   // ── layer 3 gradients, tile statistics, dL/dh2 ──
@@ -484,13 +601,24 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
     for (uint32_t r = 0; r < rows; r++) acc += (double)RS[r * 4 + c];
     a.stats_part[(size_t)blockIdx.x * 4 + c] = acc;
   }
-  dense<EPI_DTANH>(OUT, L.lo, d.n_out, src(L.w_3, w + d.oW3()), d.n_h, nullptr, H2, L.lh, DA, L.lh, R);
-  stage_layer(w + d.oW2(), d.n_h * d.n_h);
-  if (MODE != STAGE_LAYER) __syncthreads();
+  if (MODE == STAGE_NONE)
+    dense<EPI_DTANH>(OUT, L.lo, d.n_out, w + d.oW3(), d.n_h, nullptr, H2, L.lh, DA, L.lh, R);
+  else
+    dense4<EPI_DTANH>(OUT, L.lo, d.n_out, MODE == STAGE_ALL ? WB + L.w_3t : WB, L.lo, d.n_h, nullptr, H2, L.lh, DA,
+                      L.lh, R);
+  if (MODE == STAGE_LAYER) {  // W2 transposed, for dL/dh1
+    __syncthreads();
+    copy4(WB, img + L.w_2t, d.n_h * L.lh);
+  }
+  __syncthreads();
 
   // ── layer 2 gradients, dL/dh1 ──
   dense_grad(DA, L.lh, d.n_h, H1, L.lh, d.n_h, R, part + d.oW2(), part + d.ob2());
-  dense<EPI_DTANH>(DA, L.lh, d.n_h, src(L.w_2, w + d.oW2()), d.n_h, nullptr, H1, L.lh, DB, L.lh, R);
+  if (MODE == STAGE_NONE)
+    dense<EPI_DTANH>(DA, L.lh, d.n_h, w + d.oW2(), d.n_h, nullptr, H1, L.lh, DB, L.lh, R);
+  else
+    dense4<EPI_DTANH>(DA, L.lh, d.n_h, MODE == STAGE_ALL ? WB + L.w_2t : WB, L.lh, d.n_h, nullptr, H1, L.lh, DB, L.lh,
+                      R);
   __syncthreads();
 
   // ── layer 1 gradients (input: the gathered rows) ──
@@ -512,6 +640,7 @@ struct AdamArgs {
   double* v[2];
   float* w[2];
   float* wt[2];
+  float* img[2];
   Dims dims[2];
   uint32_t n_param[2];
   uint32_t tiles;
@@ -600,15 +729,28 @@ __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
   const float xf = (float)x;
   a.w[net][q] = xf;
   const Dims d = a.dims[net];
+  const WImg im(d);
+  float* img = a.img[net];
   if (q < d.ob1()) {
     const uint32_t j = q / d.n_in, i = q % d.n_in;
     a.wt[net][i * d.n_h + j] = xf;
+    img[im.w_1 + j * im.lx + i] = xf;
   } else if (q >= d.oW2() && q < d.ob2()) {
     const uint32_t e = q - d.oW2(), j = e / d.n_h, i = e % d.n_h;
     a.wt[net][d.tW2() + i * d.n_h + j] = xf;
+    img[im.w_2 + j * im.lh + i] = xf;
+    img[im.w_2t + i * im.lh + j] = xf;
   } else if (q >= d.oW3() && q < d.ob3()) {
     const uint32_t e = q - d.oW3(), k2 = e / d.n_h, i = e % d.n_h;
     a.wt[net][d.tW3() + i * d.n_out + k2] = xf;
+    img[im.w_3 + k2 * im.lh + i] = xf;
+    img[im.w_3t + i * im.lo + k2] = xf;
+  } else if (q >= d.ob1() && q < d.oW2()) {
+    img[im.b_1 + q - d.ob1()] = xf;
+  } else if (q >= d.ob2() && q < d.oW3()) {
+    img[im.b_2 + q - d.ob2()] = xf;
+  } else if (q >= d.ob3() && q < d.mlp_params()) {
+    img[im.b_3 + q - d.ob3()] = xf;
   }
 }
 
@@ -655,6 +797,7 @@ struct phz_train {
   // device buffers
   float* w[2] = {nullptr, nullptr};
   float* wt[2] = {nullptr, nullptr};
+  float* img[2] = {nullptr, nullptr};  // padded weight images (WImg)
   double* p[2] = {nullptr, nullptr};
   double* m[2] = {nullptr, nullptr};
   double* v[2] = {nullptr, nullptr};
@@ -748,7 +891,28 @@ bool upload_params(phz_train* t, int net, const double* flat) {
     for (uint32_t i = 0; i < d.n_h; i++) tr[d.tW2() + i * d.n_h + j] = mirror[d.oW2() + j * d.n_h + i];
   for (uint32_t k = 0; k < d.n_out; k++)
     for (uint32_t i = 0; i < d.n_h; i++) tr[d.tW3() + i * d.n_out + k] = mirror[d.oW3() + k * d.n_h + i];
-  return t->hip_ok(hipMemcpyAsync(t->p[net], flat, np * sizeof(double), hipMemcpyHostToDevice, t->stream), "upload params") &&
+  const WImg im(d);
+  std::vector<float> img(im.size, 0.0f);
+  for (uint32_t j = 0; j < d.n_h; j++)
+    for (uint32_t i = 0; i < d.n_in; i++) img[im.w_1 + j * im.lx + i] = mirror[d.oW1() + j * d.n_in + i];
+  for (uint32_t j = 0; j < d.n_h; j++)
+    for (uint32_t i = 0; i < d.n_h; i++) {
+      img[im.w_2 + j * im.lh + i] = mirror[d.oW2() + j * d.n_h + i];
+      img[im.w_2t + i * im.lh + j] = mirror[d.oW2() + j * d.n_h + i];
+    }
+  for (uint32_t k = 0; k < d.n_out; k++)
+    for (uint32_t i = 0; i < d.n_h; i++) {
+      img[im.w_3 + k * im.lh + i] = mirror[d.oW3() + k * d.n_h + i];
+      img[im.w_3t + i * im.lo + k] = mirror[d.oW3() + k * d.n_h + i];
+    }
+  for (uint32_t j = 0; j < d.n_h; j++) {
+    img[im.b_1 + j] = mirror[d.ob1() + j];
+    img[im.b_2 + j] = mirror[d.ob2() + j];
+  }
+  for (uint32_t k = 0; k < d.n_out; k++) img[im.b_3 + k] = mirror[d.ob3() + k];
+  return t->hip_ok(hipMemcpyAsync(t->img[net], img.data(), img.size() * sizeof(float), hipMemcpyHostToDevice, t->stream),
+                   "upload params") &&
+         t->hip_ok(hipMemcpyAsync(t->p[net], flat, np * sizeof(double), hipMemcpyHostToDevice, t->stream), "upload params") &&
          t->hip_ok(hipMemcpyAsync(t->w[net], mirror.data(), np * sizeof(float), hipMemcpyHostToDevice, t->stream), "upload params") &&
          t->hip_ok(hipMemcpyAsync(t->wt[net], tr.data(), tr.size() * sizeof(float), hipMemcpyHostToDevice, t->stream), "upload params") &&
          t->hip_ok(hipStreamSynchronize(t->stream), "upload params");
@@ -851,6 +1015,7 @@ int phz_train_create(phz_net_dims actor, phz_net_dims critic, uint64_t capacity,
   for (int n = 0; n < 2 && ok; n++) {
     const uint32_t np = t->n_param[n];
     ok = t->alloc(&t->w[n], np, "alloc weights") && t->alloc(&t->wt[n], t->dims[n].t_size(), "alloc weights") &&
+         t->alloc(&t->img[n], WImg(t->dims[n]).size, "alloc weights") &&
          t->alloc(&t->p[n], np, "alloc master weights") && t->alloc(&t->m[n], np, "alloc Adam moments") &&
          t->alloc(&t->v[n], np, "alloc Adam moments") &&
          t->alloc(&t->part[n], (size_t)t->max_tiles * np, "alloc gradient partials") &&
@@ -1012,6 +1177,7 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
     ta.x[k] = t->obs[k];
     ta.w[k] = t->w[k];
     ta.wt[k] = t->wt[k];
+    ta.img[k] = t->img[k];
     ta.part[k] = t->part[k];
     ta.dims[k] = t->dims[k];
     ta.n_param[k] = t->n_param[k];
@@ -1021,6 +1187,7 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
     aa.v[k] = t->v[k];
     aa.w[k] = t->w[k];
     aa.wt[k] = t->wt[k];
+    aa.img[k] = t->img[k];
     aa.dims[k] = t->dims[k];
     aa.n_param[k] = t->n_param[k];
     aa.lr[k] = t->adam[k].lr;
