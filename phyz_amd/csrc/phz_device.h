@@ -96,7 +96,8 @@ __device__ __forceinline__ void quadrant_sincos(float r, float k, float* s, floa
   *s = (q & 2) ? -a : a;
   *c = ((q + 1) & 2) ? -b : b;
 }
-__device__ __forceinline__ void dsincos(float x, float* s, float* c) { sincosf(x, s, c); }
+__device__ __forceinline__ void angle_sincos(float x, float* s, float* c);
+__device__ __forceinline__ void dsincos(float x, float* s, float* c) { angle_sincos(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
 // sin and cos of x (f64): x = k*pi/2 + r with k the integer nearest 2x/pi,
 // taken as t - M for t = 2x/pi + M, M = 1.5 * 2^52 (the addition rounds to
@@ -141,6 +142,41 @@ __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
   *s = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? cr : sr) ^ ss);
   *c = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? sr : cr) ^ cs);
 }
+// sin and cos of an f32 angle x: the reduction of the f64 angle_sincos (x is
+// exact in f64), then in f32 the Taylor series of sin r through r^9 and of
+// cos r through r^10 (truncation below 3e-9 on |r| <= pi/4) in Horner's form
+// (each step one fma with a literal), and the quadrant from the low word of t.
+// No large-argument branch: the reduction is exact for |x| < 1.6e6.
+__device__ __forceinline__ void angle_sincos(float xf, float* s, float* c) {
+  constexpr double M = 6755399441055744.0;  // 1.5 * 2^52
+  const double x = xf;
+  const double t = fma(x, 0x1.45f306dc9c883p-1, M);
+  const double k = t - M;
+  const float r = (float)fma(-k, 0x1.0b4611a626331p-34, fma(-k, 0x1.921fb54400000p+0, x));
+  const float u = -(r * r);
+  float p = fmaf(u, 1.0f / 362880.0f, 1.0f / 5040.0f);
+  p = fmaf(u, p, 1.0f / 120.0f);
+  p = fmaf(u, p, 1.0f / 6.0f);
+  const float sr = fmaf(r * u, p, r);
+  float q = fmaf(u, 1.0f / 3628800.0f, 1.0f / 40320.0f);
+  q = fmaf(u, q, 1.0f / 720.0f);
+  q = fmaf(u, q, 1.0f / 24.0f);
+  q = fmaf(u, q, 0.5f);
+  const float cr = fmaf(u, q, 1.0f);
+  const unsigned n = (unsigned)__builtin_bit_cast(unsigned long long, t);
+  const bool odd = n & 1u;
+  const unsigned ss = (n & 2u) << 30, cs = ((n + 1u) & 2u) << 30;
+  *s = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? cr : sr) ^ ss);
+  *c = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? sr : cr) ^ cs);
+}
+// The Box-Muller radius sqrt(-2 ln(1 - u)) of a uniform u in [0, 1). f32: the
+// hardware log2 and square root (1 - u >= 2^-24, never denormal), a few ulp
+// from the correctly rounded value, for the synthetic control stream; f64:
+// the library functions, as the oracle replays that stream to 1e-13.
+__device__ __forceinline__ float bm_radius(float u) {
+  return __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(1.0f - u));
+}
+__device__ __forceinline__ double bm_radius(double u) { return sqrt(-2.0 * log(1.0 - u)); }
 // sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1), in
 // turns: 4u and its nearest integer k are exact for the 24-bit uniforms, so
 // the only rounding before quadrant_sincos is r = (4u - k) pi/2.
@@ -1361,7 +1397,7 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
         T u1 = uniform01(rng, T(0));
         T u2 = uniform01(rng, T(0));
         if constexpr (mine0 || mine1) {
-          T r = dsqrt(T(-2) * dlog(T(1) - u1));
+          T r = bm_radius(u1);
           T sn, cs;
           turn_sincos(u2, &sn, &cs);
           if constexpr (mine0) ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
