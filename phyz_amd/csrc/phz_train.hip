@@ -686,8 +686,9 @@ __device__ void brake(const AdamArgs& a) {
 
 // tang's ModuleAdam step, elementwise (phyz_train.cu:268-288), on the sum of
 // the tile partials. Four lanes share a parameter: lane s sums tiles s, s + 4,
-// ... (two interleaved chains each), a fixed xor butterfly gives all four the
-// same total, and the first applies the step.
+// ... in eight interleaved chains (eight loads in flight per lane), added as
+// a fixed tree; a fixed xor butterfly gives all four the same total, and the
+// first applies the step.
 __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
   if (*a.skip) {
     if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
@@ -701,16 +702,21 @@ __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
   const uint32_t q = valid ? (net == 0 ? t : t - a.n_param[0]) : 0u;
   const uint32_t np = a.n_param[net];
   const double* part = a.part[net] + q;
-  double g0 = 0.0, g1 = 0.0;
+  constexpr uint32_t kChains = 8;
+  double gc[kChains];
+#pragma unroll
+  for (uint32_t j = 0; j < kChains; j++) gc[j] = 0.0;
   if (valid) {
     uint32_t k = sub;
-    for (; k + kAdamLanes < a.tiles; k += 2 * kAdamLanes) {
-      g0 += part[(size_t)k * np];
-      g1 += part[(size_t)(k + kAdamLanes) * np];
+    for (; k + (kChains - 1) * kAdamLanes < a.tiles; k += kChains * kAdamLanes) {
+#pragma unroll
+      for (uint32_t j = 0; j < kChains; j++) gc[j] += part[(size_t)(k + j * kAdamLanes) * np];
     }
-    if (k < a.tiles) g0 += part[(size_t)k * np];
+#pragma unroll
+    for (uint32_t j = 0; j < kChains; j++)
+      if (k + j * kAdamLanes < a.tiles) gc[j] += part[(size_t)(k + j * kAdamLanes) * np];
   }
-  double g = g0 + g1;
+  double g = ((gc[0] + gc[1]) + (gc[2] + gc[3])) + ((gc[4] + gc[5]) + (gc[6] + gc[7]));
   for (int off = 1; off < kAdamLanes; off <<= 1) g += __shfl_xor(g, off, 64);
   if (!valid || sub != 0) return;
   const double gr = (double)(float)g;
