@@ -458,29 +458,40 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
   const uint32_t nt = nrw * nchunk;
   float sdv = 0.0f;
   if (net == 0 && threadIdx.x < d.n_out) sdv = w[d.mlp_params() + threadIdx.x];
+  // t = q * nchunk + ch runs over this wave's (row, chunk) pairs; q and ch
+  // are stepped, not divided out.
+  uint32_t q0 = 0, ch0 = 0;
   for (uint32_t t0 = 0; t0 < nt; t0 += 8u) {
     float xv[8], av[8], rv[8];
+    uint32_t q = q0, ch = ch0;
 #pragma unroll
     for (uint32_t u = 0; u < 8u; u++) {
-      const uint32_t t = t0 + u, q = t / nchunk, i = (t - q * nchunk) * 64u + lane, r = wave + kWaves * q;
+      const uint32_t t = t0 + u, i = ch * 64u + lane, r = wave + kWaves * q;
       const bool live = t < nt && r < rows;
       const uint32_t sidx = live ? a.idx[row0 + r] : 0u;
       xv[u] = live && i < d.n_in ? x[(size_t)sidx * d.n_in + i] : 0.0f;
-      const bool first = t < nt && t - q * nchunk == 0u;  // one chunk per row fetches the row's extras
+      const bool first = ch == 0u;  // one chunk per row fetches the row's extras
       av[u] = net == 0 && live && first && lane < d.n_out ? a.act[(size_t)sidx * d.n_out + lane] : 0.0f;
       const float* sc = net == 0 ? (lane == 0 ? a.adv : a.logp_old) : a.ret;
       rv[u] = live && first && lane < (net == 0 ? 2u : 1u) ? sc[sidx] : 0.0f;
+      if (++ch == nchunk) { ch = 0u; ++q; }
     }
+    q = q0;
+    ch = ch0;
 #pragma unroll
     for (uint32_t u = 0; u < 8u; u++) {
-      const uint32_t t = t0 + u, q = t / nchunk, i = (t - q * nchunk) * 64u + lane, r = wave + kWaves * q;
-      if (t >= nt || r >= R) continue;
-      if (i < L.lx) X[r * L.lx + i] = xv[u];  // zero past n_in
-      if (t - q * nchunk == 0u) {
-        if (net == 0 && lane < d.n_out) ACT[r * L.lo + lane] = av[u];
-        if (lane < (net == 0 ? 2u : 1u)) RV[r * 4 + (net == 0 ? lane : 2u)] = rv[u];
+      const uint32_t t = t0 + u, i = ch * 64u + lane, r = wave + kWaves * q;
+      if (t < nt && r < R) {
+        if (i < L.lx) X[r * L.lx + i] = xv[u];  // zero past n_in
+        if (ch == 0u) {
+          if (net == 0 && lane < d.n_out) ACT[r * L.lo + lane] = av[u];
+          if (lane < (net == 0 ? 2u : 1u)) RV[r * 4 + (net == 0 ? lane : 2u)] = rv[u];
+        }
       }
+      if (++ch == nchunk) { ch = 0u; ++q; }
     }
+    q0 = q;
+    ch0 = ch;
   }
   if (net == 0 && threadIdx.x < d.n_out) {
     const float sd = expf(sdv);
