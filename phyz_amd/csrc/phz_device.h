@@ -225,6 +225,21 @@ __device__ __forceinline__ float dpow(float x, float y) { return powf(x, y); }
 __device__ __forceinline__ double dtanh(double x) { return tanh(x); }
 __device__ __forceinline__ float dtanh(float x) { return tanhf(x); }
 __device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x); }
+// Reciprocal on the ABA and penalty-contact paths. f32: the hardware
+// v_rcp_f32 (within 1 ulp) in place of the correctly rounded division's
+// eleven-instruction expansion; the f32 kernels' per-step bound is 1e-4 and
+// one ulp is 6e-8. f64: the correctly rounded division. The impulse solve and
+// the heightfield cell lookup keep their correctly rounded f32 divisions.
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
+// Square root on the penalty-contact path: f32 the hardware v_sqrt_f32 (within
+// 1 ulp, no correction sequence), f64 the correctly rounded one.
+__device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ double fsqrt(double x) { return sqrt(x); }
+// The friction-loss argument qd / 1e-3: f32 multiplies by 1e3 (within an ulp
+// of the quotient), f64 divides as the oracle does.
+__device__ __forceinline__ float per_milli(float x) { return x * 1e3f; }
+__device__ __forceinline__ double per_milli(double x) { return x / 1e-3; }
 template <class T> __device__ __forceinline__ T dmax(T a, T b) { return a > b ? a : b; }
 template <class T> __device__ __forceinline__ T dmin(T a, T b) { return a < b ? a : b; }
 template <class T> __device__ __forceinline__ T dabs(T a) { return a < T(0) ? -a : a; }
@@ -497,8 +512,9 @@ template <class M, class T, int i> __device__ __forceinline__ SV<T> subspace(int
 }
 
 // Effective mass of body i at body-frame offset r along unit direction u
-// (crates/phyz-gpu/cuda/phyz_kernels.cu:545-571).
-template <class M, class T, int i> __device__ __forceinline__ T eff_mass(V3<T> r, V3<T> u) {
+// (crates/phyz-gpu/cuda/phyz_kernels.cu:545-571): 1 / (1/m + a . I_c^-1 a),
+// a = (r - com) x u. FAST takes the reciprocal with frcp (penalty contact).
+template <class M, class T, int i, bool FAST = false> __device__ __forceinline__ T eff_mass(V3<T> r, V3<T> u) {
   if constexpr (!(M::mass[i] > 0.0)) {
     return T(1e30);
   } else {
@@ -509,7 +525,9 @@ template <class M, class T, int i> __device__ __forceinline__ T eff_mass(V3<T> r
                   T(M::iinv[i][1]) * a.x + T(M::iinv[i][3]) * a.y + T(M::iinv[i][4]) * a.z,
                   T(M::iinv[i][2]) * a.x + T(M::iinv[i][4]) * a.y + T(M::iinv[i][5]) * a.z);
     T ang = dmax(dot(a, ia), T(0));
-    return T(1) / (T(1.0 / M::mass[i]) + ang);
+    const T den = T(1.0 / M::mass[i]) + ang;
+    if constexpr (FAST) return frcp(den);
+    else return T(1) / den;
   }
 }
 
@@ -699,17 +717,17 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
     const bool in = pen > T(0);
     V3<T> vpt = vel.l + cross(vel.a, sup);
     T vn = dot(vpt, nb);
-    T mn = eff_mass<M, T, i>(sup, nb);
+    T mn = eff_mass<M, T, i, true>(sup, nb);
     T kb = dmin(T(sc * M::gk[i]), T(4.0 / (dtc * dtc)) * mn);
     T db = dmin(T(sc * M::gd[i]), T(1.0 / dtc) * mn);
     T fn = dmax(kb * pen - db * vn, T(0));
     V3<T> vt3 = vpt - nb * vn;
-    T vt = dsqrt(dot(vt3, vt3));
+    T vt = fsqrt(dot(vt3, vt3));
     const bool slip = vt > T(1e-6);
-    T ivt = slip ? T(1) / dmax(vt, T(5e-7)) : T(0);
+    T ivt = slip ? frcp(dmax(vt, T(5e-7))) : T(0);
     V3<T> td = vt3 * ivt;
     T coul = T(M::mu) * fn * dmin(T(1), vt * T(1e3));
-    T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i>(sup, td) * vt);
+    T ft = dmin(coul, T(1.0 / dtc) * eff_mass<M, T, i, true>(sup, td) * vt);
     ft = slip ? ft : T(0);
     V3<T> fb = nb * fn - td * ft;
     fb = in ? fb : v3(T(0), T(0), T(0));
@@ -1174,7 +1192,7 @@ __device__ __forceinline__ T dof_force(const T* q, const T* v, const T* ctrl) {
       const T lf = sign * (T(M::lim_k[i]) * depth + T(M::lim_d[i]) * dmax(-(sign * xd), T(0)));
       f = f + ((below || above) ? lf : T(0));
     }
-    if constexpr (M::floss[i] > 0.0) f = f - T(M::floss[i]) * dtanh(v[vo] / T(1e-3));
+    if constexpr (M::floss[i] > 0.0) f = f - T(M::floss[i]) * dtanh(per_milli(v[vo]));
   }
   return tau + f;
 }
@@ -1219,7 +1237,7 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
 #pragma unroll
       for (int k = 0; k < j; k++) dj = dj - ws.Lm[i][j][k] * E[j][k];
       ws.ok[i] = ws.ok[i] && !(dabs(dj) < T(1e-20));
-      ws.Dinv[i][j] = T(1) / (dabs(dj) < T(1e-20) ? T(1) : dj);
+      ws.Dinv[i][j] = frcp(dabs(dj) < T(1e-20) ? T(1) : dj);
 #pragma unroll
       for (int r = j + 1; r < nd; r++) {
         T e = D[r][j];

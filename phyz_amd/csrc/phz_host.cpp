@@ -285,79 +285,136 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   const bool forced = want == "1" || want == "2";
   if (parts.size() < 2) return lane_per_world();
   if (mode == 2 && !forced && nb < 14) return lane_per_world();
-  // Waves per world group. pack(cap) puts the parts into at most cap groups
-  // by body count: with more parts than cap, largest first into the lightest
-  // group, group 0 starting from the floating trunk's bodies (it runs the
-  // trunk's passes 2 and 3); otherwise one part per group, the smallest in
-  // group 0. The plan is the one of caps 8, 4, 2 whose busiest SIMD carries
-  // the fewest bodies per step, for the launch's workgroups per CU with waves
-  // dealt to the 4 SIMDs in turn; ties keep more waves. Every plan measured on
-  // MI355X ranks as this predicts (humanoid, 32768 worlds: 2 waves 2.43e9
-  // world-steps/s, 4 waves 2.00e9; hand, 16384 worlds: 4 waves 2.02e9 f32 /
-  // 1.35e9 f64, 5 waves 1.93e9 / 1.05e9; ModelBuilder humanoid with balanced
-  // limbs: 4 waves 3.05e9, 2 waves 2.83e9; welded-palm hand without a
-  // barrier: 5 waves 5.12e9 f64, 4 waves 4.35e9). PHZ_MAX_GROUPS forces a cap
-  // (rounded down to 1, 2, 4 or 8).
-  int ntrunk = 0;
-  for (int i = 0; i < nb; i++) ntrunk += trunk[i];
-  const long t0 = mode == 2 ? ntrunk : 0;
-  auto by_size = [](const std::vector<int>& a, const std::vector<int>& b) { return a.size() < b.size(); };
+  // Waves per world group, from a model of a step's length in body weights
+  // (a hinge, slide or ball body 4, a free body 8, a body without DOFs 2):
+  //  - A wave's own bodies run passes 1-3 in its own instruction stream; wave 0
+  //    also runs the trunk's ground contacts.
+  //  - Every wave recomputes the floating trunk's pass 1, half a trunk body's
+  //    weight per wave.
+  //  - Between the two barriers wave 0 runs the trunk's passes 2 and 3 while
+  //    the others wait: three quarters of the trunk's weight, on every wave's
+  //    clock. A fixed trunk costs nothing (its values are constants).
+  //  - The step kernels hold more than 256 registers, one wave per SIMD: with
+  //    g <= 4 waves floor(4 / g) workgroups share a CU at a time; 5-8 waves run
+  //    one workgroup per CU with waves k and k + 4 on one SIMD. The launch's
+  //    workgroups per CU beyond that run in further rounds.
+  // A round lasts as long as its busiest SIMD plus the serial trunk section.
+  // Measured on MI355X against this model (f32, 1000-step launches): builder
+  // humanoid, 32768 worlds, 2 waves 9.74 ms / 4 waves 13.91 ms (model 55 / 78);
+  // MJCF humanoid 2 waves 13.01 ms / 4 waves 15.53 ms (65 / 82); MJCF hand,
+  // 16384 worlds, 4 waves 7.54 ms / 5 waves 8.12 / 2 waves 11.32 (47 / 53 /
+  // 63). Each cap of 8, 4 and 2 is packed to its cheapest assignment
+  // (exhaustive over parts -> groups when small, else largest first into the
+  // lightest group); the cheapest plan over the caps is kept, ties keeping
+  // more waves. PHZ_MAX_GROUPS forces a cap (rounded down to 1, 2, 4 or 8).
+  // Ground contact adds 2 per contact point (a box 8 points, other shapes 1);
+  // the trunk's contacts run on wave 0 only.
+  auto contact_weight = [&](int i) {
+    if (!f.contact) return 0.0;
+    const int gt = (int)f.geom[(size_t)i * kGeomStride];
+    return gt == 0 ? 0.0 : gt == 2 ? 16.0 : 2.0;
+  };
+  auto weight = [&](int i) {
+    const int jt = m.b[i].jtype;
+    return (jt == 4 ? 8.0 : jt == 2 ? 2.0 : 4.0) + contact_weight(i);
+  };
+  double twt = 0, tcontact = 0;
+  for (int i = 0; i < nb; i++)
+    if (trunk[i]) { twt += weight(i) - contact_weight(i); tcontact += contact_weight(i); }
+  if (mode != 2) tcontact = 0;
+  const double pass1 = mode == 2 ? 0.5 * twt : 0.0, serial = mode == 2 ? 0.75 * twt : 0.0;
+  std::vector<double> pw(parts.size(), 0.0);
+  for (size_t k = 0; k < parts.size(); k++) for (int i : parts[k]) pw[k] += weight(i);
+  auto cost = [&](const std::vector<double>& load) {
+    const int ng = (int)load.size(), cus = std::max(f.cus, 1);
+    const long per_cu = std::max(1, (f.wgs + cus - 1) / cus);
+    const long conc = ng <= 4 ? 4 / ng : 1;
+    const long rounds = (per_cu + conc - 1) / conc;
+    double simd[4] = {0, 0, 0, 0};
+    for (int k = 0; k < ng; k++) simd[k % 4] += load[k] + pass1 + (k == 0 ? tcontact : 0.0);
+    return (double)rounds * (*std::max_element(simd, simd + 4) + serial);
+  };
+  // Cheapest assignment of the parts to at most cap groups (empty groups
+  // dropped, no plan of exactly three groups), as group -> part indices.
   auto pack = [&](int cap) {
-    std::vector<std::vector<int>> g = parts;
-    if ((int)g.size() <= cap) {
-      std::stable_sort(g.begin(), g.end(), by_size);
-      return g;
+    const int n = (int)parts.size();
+    std::vector<std::vector<int>> best;
+    double best_cost = -1;
+    auto consider = [&](const std::vector<int>& owner) {
+      std::vector<std::vector<int>> g(cap);
+      for (int k = 0; k < n; k++) g[owner[k]].push_back(k);
+      std::vector<std::vector<int>> h;
+      for (auto& x : g) if (!x.empty()) h.push_back(x);
+      if (h.size() == 3) return;
+      std::vector<double> load;
+      for (auto& x : h) { double l = 0; for (int k : x) l += pw[k]; load.push_back(l); }
+      const double c = cost(load);
+      if (best_cost < 0 || c < best_cost - 1e-9) { best_cost = c; best = h; }
+    };
+    double combos = 1;
+    for (int k = 0; k < n; k++) combos *= cap;
+    if (combos <= 2e5) {
+      std::vector<int> owner(n, 0);
+      for (;;) {
+        consider(owner);
+        int k = 0;
+        while (k < n && ++owner[k] == cap) owner[k++] = 0;
+        if (k == n) break;
+      }
+    } else {
+      std::vector<int> order(n);
+      for (int k = 0; k < n; k++) order[k] = k;
+      std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pw[a] > pw[b]; });
+      std::vector<int> owner(n, 0);
+      std::vector<double> load(cap, 0.0);
+      for (int k : order) {
+        const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+        owner[k] = j;
+        load[j] += pw[k];
+      }
+      consider(owner);
+      if (best.empty()) {  // three groups: the two-group split of the same greedy order
+        std::fill(load.begin(), load.end(), 0.0);
+        for (int k : order) {
+          const int j = load[0] <= load[1] ? 0 : 1;
+          owner[k] = j;
+          load[j] += pw[k];
+        }
+        consider(owner);
+      }
     }
-    std::stable_sort(g.begin(), g.end(), [&](const std::vector<int>& a, const std::vector<int>& b) { return by_size(b, a); });
-    std::vector<std::vector<int>> bins(cap);
-    std::vector<long> load(cap, 0);
-    load[0] = t0;
-    for (auto& p : g) {
-      const int k = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-      bins[k].insert(bins[k].end(), p.begin(), p.end());
-      load[k] += (long)p.size();
+    return std::make_pair(best, best_cost);
+  };
+  auto as_bodies = [&](const std::vector<std::vector<int>>& g) {
+    std::vector<std::vector<int>> out;
+    for (auto& x : g) {
+      std::vector<int> bodies;
+      for (int k : x) bodies.insert(bodies.end(), parts[k].begin(), parts[k].end());
+      out.push_back(bodies);
     }
-    if (bins[0].empty()) {  // group 0 still takes a part: the lightest group's
-      int k = 0;
-      for (int j = 1; j < cap; j++)
-        if (!bins[j].empty() && (k == 0 || load[j] < load[k])) k = j;
-      bins[0].swap(bins[k]);
-    }
-    g.clear();
-    for (auto& b : bins) if (!b.empty()) g.push_back(b);
-    return g;
+    return out;
   };
-  auto busiest = [&](const std::vector<std::vector<int>>& g) {
-    const int ng = (int)g.size(), cus = std::max(f.cus, 1);
-    const int rounds = std::max(1, (f.wgs + cus - 1) / cus);
-    long load[4] = {0, 0, 0, 0};
-    for (int r = 0; r < rounds; r++)
-      for (int k = 0; k < ng; k++) load[(r * ng + k) % 4] += (long)g[k].size() + (k == 0 ? t0 : 0);
-    return *std::max_element(load, load + 4);
-  };
-  // No plan has three groups. A 3-wave f64 MJCF humanoid kernel (192 threads)
-  // gave values that changed from launch to launch, with no cause found, so a
-  // packing that ends with exactly three groups is re-packed into two. pack(cap)
-  // keeps the parts as they are when there are at most cap of them, and its
-  // bin-0 swap can empty a bin, so any cap of 4 or more can yield three.
-  auto packed = [&](int cap) {
-    std::vector<std::vector<int>> g = pack(cap);
-    return g.size() == 3 ? pack(2) : g;
-  };
-  const std::vector<std::vector<int>> unmerged = pack((int)parts.size());
+  // One part per wave, the lightest first (waves 0 and 4 share a SIMD).
+  std::vector<int> by_weight(parts.size());
+  for (size_t k = 0; k < parts.size(); k++) by_weight[k] = (int)k;
+  std::stable_sort(by_weight.begin(), by_weight.end(), [&](int a, int b) { return pw[a] < pw[b]; });
+  std::vector<std::vector<int>> unmerged;
+  for (int k : by_weight) unmerged.push_back(parts[k]);
   if (const char* e = std::getenv("PHZ_MAX_GROUPS")) {
     // Rounded down to 1, 2, 4 or 8, the caps the planner itself tries.
     const int want = std::atoi(e);
-    parts = packed(want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1);
+    parts = as_bodies(pack(want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1).first);
   } else {
     std::vector<std::vector<int>> best;
-    long best_load = -1;
+    double best_cost = -1;
     for (int cap : {8, 4, 2}) {
-      std::vector<std::vector<int>> g = packed(cap);
-      const long l = busiest(g);
-      if (best_load < 0 || l < best_load) { best_load = l; best = g; }
+      auto pc = pack(cap);
+      if (!pc.first.empty() && (best_cost < 0 || pc.second < best_cost - 1e-9)) {
+        best_cost = pc.second;
+        best = pc.first;
+      }
     }
-    parts = best;
+    parts = as_bodies(best);
   }
   if (parts.size() == 3) return lane_per_world();  // unreachable: pack(2) holds at most two
   if (parts.size() < 2) return lane_per_world();
