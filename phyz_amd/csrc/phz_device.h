@@ -1287,6 +1287,20 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
           for (int k = 1; k < nd; k++) s0 = s0 + W[k][r] * Uv<M, T, i>(ws, k, 3 + c);
           Ia.b[r * 3 + c] = Ia.b[r * 3 + c] - s0;
         }
+      if constexpr (M::zero_axis[i] >= 0) {
+        // I_a S = U - U D^-1 S^T U = 0 when D = S^T U (no armature or
+        // damping): for S a coordinate axis z, row and column z of I_a are
+        // zero in exact arithmetic, and set so here (the computed values are
+        // rounding residue). The zeros then fold through X^T I_a X and I_a c.
+        constexpr int z = M::zero_axis[i];
+#pragma unroll
+        for (int j = 0; j < 6; j++) {
+          if (z < 3 && j < 3) Ia.a[sx(z, j)] = T(0);
+          if (z < 3 && j >= 3) Ia.b[z * 3 + (j - 3)] = T(0);
+          if (z >= 3 && j >= 3) Ia.c[sx(z - 3, j - 3)] = T(0);
+          if (z >= 3 && j < 3) Ia.b[j * 3 + (z - 3)] = T(0);
+        }
+      }
       SV<T> wu;
 #pragma unroll
       for (int r = 0; r < 6; r++) {

@@ -628,6 +628,19 @@ std::string gen_model(const ModelD& m, const Features& f) {
   db("stiffness", [&](int i) { return m.b[i].stiffness; });
   db("spring_ref", [&](int i) { return m.b[i].spring_ref; });
   db("armature", [&](int i) { return m.b[i].armature; });
+  // The component of a one-DOF joint's axis along which I_a S = 0 makes a
+  // row and column of I_a vanish (see body_solve in phz_device.h): a
+  // coordinate axis (one entry +-1), no armature and no damping, so that
+  // D = S^T I_A S exactly. -1 otherwise.
+  ib("zero_axis", [&](int i) {
+    const BodyD& b = m.b[i];
+    if ((b.jtype != 0 && b.jtype != 1) || b.armature != 0.0 || b.damping != 0.0) return -1;
+    int k = -1, nz = 0;
+    for (int c = 0; c < 3; c++)
+      if (b.axis[c] != 0.0) { nz++; k = c; }
+    if (nz != 1 || std::fabs(b.axis[k]) != 1.0) return -1;
+    return b.jtype == 0 ? k : 3 + k;
+  });
   db("mass", [&](int i) { return m.b[i].mass; });
   d2("com", 3, [&](int i, int k) { return m.b[i].com[k]; });
   d2("inA", 6, [&](int i, int k) { return A[i * 6 + k]; });
