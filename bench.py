@@ -7,8 +7,10 @@ every world of the workload. The headline `value` is the 7-link chain, 65536
 worlds, f32: W warmup steps run untimed, then spans of exactly K steps are
 timed by the host clock with the device synchronized on both sides (the median
 of --reps spans, each from the workload's seeded initial state, reloaded
-untimed); the kernel's own time comes from hipEvents recorded on the sim's
-stream around the same spans. Before the warmup the device runs the same span
+untimed); the kernel's own time comes from hipEvents on the sim's stream that
+the span's first and last launch stamp with their own start and end
+(hipExtModuleLaunchKernel), so it is the kernels' execution time, without the
+dispatch around them. Before the warmup the device runs the same span
 untimed for --settle-ms, so a short span is not timed at the idle clock. State
 stays resident in HBM for the whole measurement.
 
@@ -19,7 +21,7 @@ device's parity at the rollout's late state.
 
 roofline: algorithmic FLOPs per launch (tests/golden/flops_per_world_step.json,
 counted on the oracle's structure-exploiting formulation x worlds x steps per
-launch) over the event-timed launch duration, against MI355X's vector peak
+launch) over the kernel-stamped launch duration, against MI355X's vector peak
 (FP64 78.6 TFLOP/s; FP32 157.3 TFLOP/s published). `traffic` is the kernel's
 measured HBM bytes per launch (profiles/hbm_traffic.json, rocprofv3 --pmc
 FETCH_SIZE and WRITE_SIZE scaled by a plain copy's readings): one state round
@@ -36,15 +38,15 @@ terrain_impulse (unless --no-impulse): the same measurement of workload 6, the
 ant on a rolling heightfield with impulse-mode contact (16 sweeps per step),
 131072 worlds x 1000 steps, f32, with its own roofline, CPU baseline and parity.
 mjcf (unless --no-mjcf): workloads 7-9, the reference's MJCF ant, humanoid and
-hand driven by their own actuators, f32. The reference's explicit joint-limit
-law diverges on the lightest links (the oracle identically; without limits
-every world stays finite), so `value` counts only the worlds still finite at
-the end of the timed span, and `all_worlds_value` every world.
+hand driven by their own actuators, f32, at a 1 ms step (the reference's
+explicit joint-limit law runs light links away at the files' own steps).
+`value` counts the worlds still finite at the end of the timed span (every
+world, at 1 ms), and `all_worlds_value` every world.
 control_loop (unless --no-control): the ant driven by the on-device policy.
 ppo_update (unless --no-ppo; --ppo-only runs just this): the PPO update pass at
 the reference's timing shape (a million samples, actor 55-64-64-22, critic
 67-64-64-1, minibatch 4096, one epoch) with the batch resident: samples/s of
-whole updates, the tile kernel's roofline from hipEvents, and, with the CPU
+whole updates, the tile kernel's roofline from kernel-stamped hipEvents, and, with the CPU
 leg, the f64 CPU update on 128 minibatches plus the device's update of that
 sample against it.
 """
@@ -101,8 +103,9 @@ def run_gpu(w, prec, steps, warmup, reps, settle_ms=0.0):
     """W = warmup untimed steps (whole spans of the timed length), then `reps`
     wall-clock spans of exactly `steps` steps, each from the workload's seeded
     initial state (reloaded untimed) and bracketed by a device synchronization
-    on both sides, plus the same number of spans timed by hipEvents on the
-    sim's stream. settle_ms: untimed spans run first until the device has been
+    on both sides, plus the same number of spans run back to back from the
+    initial state, each timed by hipEvents its own launches stamp with their
+    start and end on the sim's stream. settle_ms: untimed spans run first until the device has been
     busy that long, so that a short timed span does not run at the idle clock."""
     from phyz_amd.sim import from_workload
     sim = from_workload(w, prec, nworld=w.nworld, device=0)
@@ -136,10 +139,10 @@ def run_gpu(w, prec, steps, warmup, reps, settle_ms=0.0):
         sim.step_many(steps)
         sim.synchronize()
         walls.append(time.perf_counter() - t0)
-    ev = []
-    for _ in range(reps):
-        reload()
-        ev.extend(sim.time_step_many(steps, 1))
+    # Kernel time: `reps` spans back to back (the clock stays up between them),
+    # each timed by the events its own launches stamp.
+    reload()
+    ev = list(sim.time_step_many(steps, reps))
     reload()
     sim.step_many(steps)
     info = sim.kernel_info()

@@ -173,8 +173,11 @@ int phz_collidable_bodies(const phz_sim* sim);
  * the policy are enabled) for the current configuration now; otherwise each is
  * compiled at its first launch. Works on host-only sims. */
 int phz_compile(phz_sim* sim);
-/* Measurement: `reps` spans of n steps, each bracketed by hipEvents on the
- * sim's stream; ms_per_rep[reps] receives the event times. */
+/* Measurement: `reps` spans of n steps (n >= 1) on the sim's stream, each
+ * timed by hipEvents that its first and last launch stamp with their own start
+ * and end (hipExtModuleLaunchKernel): ms_per_rep[reps] receives the kernels'
+ * execution time from the first start to the last end, without the dispatch
+ * around them. */
 int phz_time_step_many(phz_sim* sim, uint32_t n, uint32_t reps, double* ms_per_rep);
 /* Kernel resource use of the compiled step kernel: [0] VGPRs per lane (arch),
  * [1] AGPRs, [2] SGPRs, [3] private (scratch) bytes per lane, [4] block size,

@@ -30,6 +30,7 @@
 //              as the reference's host loop does, without the reference's
 //              per-minibatch readback.
 // Every sum has a fixed order, so an update is bit-reproducible run to run.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
@@ -1160,7 +1161,7 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
   if (!set_device(t)) return 1;
   if (tm) {
     const uint64_t total = epochs * ((n + cfg->minibatch - 1) / cfg->minibatch);
-    tm->ev.assign(3 * total, nullptr);
+    tm->ev.assign(4 * total, nullptr);
     for (auto& e : tm->ev)
       if (!t->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
   }
@@ -1246,12 +1247,14 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
         aa.bc1[k] = 1.0 - powi(t->adam[k].beta1, t->t[k] + j + 1);
         aa.bc2[k] = 1.0 - powi(t->adam[k].beta2, t->t[k] + j + 1);
       }
-      if (tm) hipEventRecord(tm->ev[3 * j], t->stream);
-      hipLaunchKernelGGL(tiles_kernel, dim3(tiles, 2), dim3(kTileThreads), t->lds_bytes, t->stream, ta);
-      if (tm) hipEventRecord(tm->ev[3 * j + 1], t->stream);
-      hipLaunchKernelGGL(ppo_adam, dim3((n_all * kAdamLanes + kAdamThreads - 1) / kAdamThreads), dim3(kAdamThreads), 0,
-                         t->stream, aa);
-      if (tm) hipEventRecord(tm->ev[3 * j + 2], t->stream);
+      // Timed updates pass events to the launch itself: HIP stamps them with
+      // the kernel's own start and end, so they measure its execution and not
+      // the dispatch around it.
+      hipEvent_t* ev = tm ? &tm->ev[4 * j] : nullptr;
+      hipExtLaunchKernelGGL(tiles_kernel, dim3(tiles, 2), dim3(kTileThreads), (uint32_t)t->lds_bytes, t->stream,
+                            ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, 0u, ta);
+      hipExtLaunchKernelGGL(ppo_adam, dim3((n_all * kAdamLanes + kAdamThreads - 1) / kAdamThreads), dim3(kAdamThreads),
+                            0u, t->stream, ev ? ev[2] : nullptr, ev ? ev[3] : nullptr, 0u, aa);
     }
   }
   if (!t->hip_ok(hipGetLastError(), "launch update")) return 1;
@@ -1263,7 +1266,7 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
     for (uint64_t i = 0; i < j; i++)
       for (int k = 0; k < 2; k++) {
         float ms = 0.0f;
-        if (!t->hip_ok(hipEventElapsedTime(&ms, tm->ev[3 * i + k], tm->ev[3 * i + k + 1]), "time update")) return 1;
+        if (!t->hip_ok(hipEventElapsedTime(&ms, tm->ev[4 * i + 2 * k], tm->ev[4 * i + 2 * k + 1]), "time update")) return 1;
         tm->ms[k] += ms;
       }
     tm->launches = j;
