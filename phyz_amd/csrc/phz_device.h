@@ -1411,9 +1411,15 @@ template <class T> __device__ __forceinline__ void add_sym(const T* lds, int s, 
 // Control noise and PD servos of group G's DOFs, before the dynamics.
 template <class M, class T, int G>
 __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)[M::NV], T (&ctrl)[M::NCTRL], const T* tgt,
-                                               u64& rng) {
+                                               u64& rng, const T* lds, int lane) {
   // ── control noise: every group advances the whole stream; values only for its DOFs ──
-  if constexpr (M::NNOISE > 0) {
+  if constexpr (M::NNOISE > 0 && M::NOISE_G >= 0) {
+    // Drawn by wave NOISE_G during the previous step (draw_shared_noise).
+    sfor<0, M::NNOISE>([&](auto K) {
+      constexpr int k = decltype(K)::value;
+      if constexpr (M::ctrl_owner[M::noise_dof[k]] == G) ctrl[M::noise_dof[k]] = lds_get(lds, M::slot_noise + k, lane);
+    });
+  } else if constexpr (M::NNOISE > 0) {
     if constexpr (M::noise_dist == 1) {
       sfor<0, M::NNOISE>([&](auto K) {
         constexpr int k = decltype(K)::value;
@@ -1447,6 +1453,32 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
     }
   });
 
+}
+
+// Floating-trunk plans (NOISE_G >= 0): wave NOISE_G draws one step's noise
+// for every DOF into the LDS slots, the draws and transforms of
+// apply_controls in the same order, so every value is the one-lane kernel's.
+// It runs between the two barriers, while wave 0 runs the trunk and the other
+// waves wait, instead of every wave advancing the whole stream each step.
+template <class M, class T> __device__ __forceinline__ void draw_shared_noise(u64& rng, T* lds, int lane) {
+  if constexpr (M::noise_dist == 1) {
+    sfor<0, M::NNOISE>([&](auto K) {
+      constexpr int k = decltype(K)::value;
+      T u = uniform01(rng, T(0));
+      lds_put(lds, M::slot_noise + k, lane, T(M::noise_a) + T(M::noise_b - M::noise_a) * u);
+    });
+  } else {
+    sfor<0, (M::NNOISE + 1) / 2>([&](auto K) {
+      constexpr int k = 2 * decltype(K)::value;
+      T u1 = uniform01(rng, T(0));
+      T u2 = uniform01(rng, T(0));
+      T r = bm_radius(u1);
+      T sn, cs;
+      turn_sincos(u2, &sn, &cs);
+      lds_put(lds, M::slot_noise + k, lane, T(M::noise_a) + T(M::noise_b) * (r * cs));
+      if constexpr (k + 1 < M::NNOISE) lds_put(lds, M::slot_noise + k + 1, lane, T(M::noise_a) + T(M::noise_b) * (r * sn));
+    });
+  }
 }
 
 // Value x of lane o of each aligned group of L lanes (L = 2 or 4), for every
@@ -1501,12 +1533,12 @@ template <class M, class T> __device__ __forceinline__ void trig_prepass(WS<M, T
 template <class M, class T, int G>
 __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctrl)[M::NCTRL], T (&qdd)[M::NV],
                                            const T* tgt, u64& rng, T* rows, int S, bool write_rows, T* lds, int lane,
-                                           const Terrain<T>& tr) {
+                                           const Terrain<T>& tr, bool draw_next) {
   constexpr int NB = M::NB;
   constexpr int NL = M::glen[G];
   constexpr int NT = M::NTRUNK;
   constexpr bool FLOAT = M::PMODE == 2;
-  apply_controls<M, T, G>(q, v, ctrl, tgt, rng);
+  apply_controls<M, T, G>(q, v, ctrl, tgt, rng, lds, lane);
 
   WS<M, T> ws;
   if constexpr (M::LANES > 1) trig_prepass<M, T>(ws, q, lane);
@@ -1556,6 +1588,11 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
   });
   if constexpr (FLOAT) {
     __syncthreads();
+    if constexpr (M::NOISE_G == G) {
+      // Every wave has read this step's noise before the barrier above; the
+      // next step's is read after the one below.
+      if (draw_next) draw_shared_noise<M, T>(rng, lds, lane);
+    }
     if constexpr (G == 0) {
       // Contributions of the other groups' subtrees, in body order.
       sfor<0, NB>([&](auto I) {
@@ -1721,7 +1758,7 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
                                              T (&impp)[M::NB][24], const Terrain<T>& tr, T* rows, int S,
                                              bool write_rows) {
   constexpr int NB = M::NB;
-  apply_controls<M, T, 0>(q, v, ctrl, tgt, rng);
+  apply_controls<M, T, 0>(q, v, ctrl, tgt, rng, nullptr, 0);
   WS<M, T> ws;
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
@@ -1936,9 +1973,13 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
       });
     }
   } else {
+    if constexpr (M::NOISE_G >= 0) {
+      if constexpr (G == M::NOISE_G) draw_shared_noise<M, T>(rng, lds, lane);
+      __syncthreads();
+    }
     for (int s = 0; s < n; s++) {
       const bool last = (s == n - 1) && a.write_contacts && live;
-      step_group<M, T, G>(q, v, ctrl, qdd, tgt, rng, rows, S, last, lds, lane, tr);
+      step_group<M, T, G>(q, v, ctrl, qdd, tgt, rng, rows, S, last, lds, lane, tr, s + 1 < n);
     }
   }
   if (!live) return;
@@ -1960,7 +2001,7 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
     constexpr int j = decltype(J)::value;
     if constexpr (M::ctrl_group[j] == G || (G == 0 && M::ctrl_group[j] == -1)) gc[j * S + w] = ctrl[j];
   });
-  if constexpr (M::NNOISE > 0 && G == 0) a.rng[w] = rng;
+  if constexpr (M::NNOISE > 0 && G == (M::NOISE_G >= 0 ? M::NOISE_G : 0)) a.rng[w] = rng;
 }
 
 }  // namespace phz

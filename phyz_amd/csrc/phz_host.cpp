@@ -545,14 +545,28 @@ std::string gen_model(const ModelD& m, const Features& f) {
   }
   const int slot_state = nslot;
   if (pl.mode == 2) nslot += 2 * ntd;
+  // Control noise of a floating-trunk plan: one wave other than wave 0 (the
+  // one with the fewest bodies) draws the next step's values for every DOF
+  // between the two barriers, while wave 0 runs the trunk, and hands them to
+  // the other waves through LDS (NOISE_G; -1: each wave draws for itself).
+  const int nn = f.noise ? (int)f.noise_dofs.size() : 0;
+  int noise_g = -1;
+  if (pl.mode == 2 && nn > 0 && ng > 1) {
+    noise_g = 1;
+    for (int g = 2; g < ng; g++)
+      if (pl.groups[g].size() < pl.groups[noise_g].size()) noise_g = g;
+  }
+  const int slot_noise = nslot;
+  if (noise_g >= 0) nslot += nn;
 
   std::ostringstream o;
-  const int npd = f.npd, nn = f.noise ? (int)f.noise_dofs.size() : 0;
+  const int npd = f.npd;
   o << "struct Model {\n";
   o << "  static constexpr int NB = " << nb << ", NQ = " << m.nq << ", NV = " << m.nv
     << ", MAXD = " << std::max(maxnd, 1) << ";\n";
   o << "  static constexpr int PMODE = " << pl.mode << ", NG = " << ng << ", NTRUNK = " << pl.trunk.size()
     << ", MAXG = " << maxg << ", NSLOT = " << nslot << ", slot_state = " << slot_state << ";\n";
+  o << "  static constexpr int NOISE_G = " << noise_g << ", slot_noise = " << slot_noise << ";\n";
   {
     std::vector<int> rev;
     for (int i = 0; i < nb; i++) if (m.b[i].jtype == 0) rev.push_back(i);
