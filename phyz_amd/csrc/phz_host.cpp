@@ -1271,10 +1271,19 @@ struct phz_sim {
                stride,  nsteps,  feat.contact ? 1 : 0};
     void* params[] = {&a};
     const unsigned grid = (unsigned)(((long)nworld * lanes + 63) / 64);
-    if (start || stop)
-      return hip_ok(hipExtModuleLaunchKernel(fn, grid * (unsigned)block, 1, 1, (unsigned)block, 1, 1, 0, stream, params,
-                                             nullptr, start, stop, 0),
-                    "step kernel launch");
+    if (start || stop) {
+      // hipExtModuleLaunchKernel takes the grid in work-items (32 bits);
+      // beyond that the events bracket the launch on the stream instead.
+      if ((uint64_t)grid * (uint64_t)block <= 0xffffffffull)
+        return hip_ok(hipExtModuleLaunchKernel(fn, grid * (unsigned)block, 1, 1, (unsigned)block, 1, 1, 0, stream,
+                                               params, nullptr, start, stop, 0),
+                      "step kernel launch");
+      if (start && !hip_ok(hipEventRecord(start, stream), "hipEventRecord")) return false;
+      if (!hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
+                  "step kernel launch"))
+        return false;
+      return !stop || hip_ok(hipEventRecord(stop, stream), "hipEventRecord");
+    }
     return hip_ok(hipModuleLaunchKernel(fn, grid, 1, 1, (unsigned)block, 1, 1, 0, stream, params, nullptr),
                   "step kernel launch");
   }

@@ -122,6 +122,32 @@ def test_graph_replay_bit_identical(prec):
         assert np.array_equal(o[0], outs[0][0]) and np.array_equal(o[1], outs[0][1])
 
 
+def test_time_step_many_is_kernel_time():
+    """phz_time_step_many reports each span's kernel time from events its
+    launches stamp: positive, no longer than the same span's wall clock, and
+    for a span of two launches (1500 steps, 1000 per launch) about the sum of
+    its launches; a span of no steps is refused."""
+    import time
+    from phyz_amd.sim import PhzError
+    w = W.config(2)
+    q, v, c, _ = w.initial_state(4096)
+    sim = from_workload(w, "f32", nworld=4096)
+    sim.load_states(q, v, c)
+    one = sim.time_step_many(500, 3)
+    two = sim.time_step_many(1500, 2)
+    sim.synchronize()
+    t0 = time.perf_counter()
+    sim.step_many(500)
+    sim.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    print(f"500 steps: events {one} ms, wall {wall_ms:.3f} ms; 1500 steps: {two} ms", flush=True)
+    assert np.all(one > 0) and np.all(two > 0)
+    assert np.median(one) <= wall_ms * 1.05
+    assert 2.0 * np.median(one) < np.median(two) < 4.0 * np.median(one)
+    with pytest.raises(PhzError):
+        sim.time_step_many(0, 1)
+
+
 @pytest.mark.parametrize("cfg,prec", CASES + [(6, "f32"), (6, "f64")])
 def test_repeat_launch_bit_identical(cfg, prec):
     """The same inputs stepped again give the same bits, every world: a kernel
