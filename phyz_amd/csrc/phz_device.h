@@ -169,14 +169,45 @@ __device__ __forceinline__ void angle_sincos(float xf, float* s, float* c) {
   *s = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? cr : sr) ^ ss);
   *c = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? sr : cr) ^ cs);
 }
+// ln x for x in [2^-53, 1] (1 - u of the f64 Box-Muller radius), within
+// about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from the hardware
+// frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) / (m + 1),
+// |s| <= 0.1716, z = s^2, and P(z) = sum_j z^j / (2j + 3) through z^8 (the
+// first omitted term is below 3e-17 of ln m), in Estrin's form; 1 / (m + 1)
+// is the hardware reciprocal refined by two Newton steps; ln 2 is split so
+// that e * ln2_hi is exact. About a third of the library log's instructions.
+__device__ __forceinline__ double bm_log(double x) {
+  double m = __builtin_amdgcn_frexp_mant(x);  // [0.5, 1)
+  int e = __builtin_amdgcn_frexp_exp(x);
+  const bool low = m < 0x1.6a09e667f3bcdp-1;
+  m = low ? 2.0 * m : m;
+  e = low ? e - 1 : e;
+  const double d = m + 1.0;
+  double r = __builtin_amdgcn_rcp(d);
+  r = fma(fma(-d, r, 1.0), r, r);
+  r = fma(fma(-d, r, 1.0), r, r);
+  const double s = (m - 1.0) * r;
+  const double z = s * s;
+  const double z2 = z * z;
+  const double z4 = z2 * z2;
+  const double p01 = fma(z, 1.0 / 5.0, 1.0 / 3.0);
+  const double p23 = fma(z, 1.0 / 9.0, 1.0 / 7.0);
+  const double p45 = fma(z, 1.0 / 13.0, 1.0 / 11.0);
+  const double p67 = fma(z, 1.0 / 17.0, 1.0 / 15.0);
+  const double p = fma(z4, fma(z4, 1.0 / 19.0, fma(z2, p67, p45)), fma(z2, p23, p01));
+  const double lnm = 2.0 * fma(s * z, p, s);
+  const double fe = (double)e;
+  return fma(fe, 0x1.62e42fefa3800p-1, fma(fe, 0x1.ef35793c76730p-45, lnm));
+}
 // The Box-Muller radius sqrt(-2 ln(1 - u)) of a uniform u in [0, 1). f32: the
 // hardware log2 and square root (1 - u >= 2^-24, never denormal), a few ulp
 // from the correctly rounded value, for the synthetic control stream; f64:
-// the library functions, as the oracle replays that stream to 1e-13.
+// bm_log (about 2 ulp) and the correctly rounded square root, as the oracle
+// replays that stream to 1e-13.
 __device__ __forceinline__ float bm_radius(float u) {
   return __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(1.0f - u));
 }
-__device__ __forceinline__ double bm_radius(double u) { return sqrt(-2.0 * log(1.0 - u)); }
+__device__ __forceinline__ double bm_radius(double u) { return sqrt(-2.0 * bm_log(1.0 - u)); }
 // sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1), in
 // turns: 4u and its nearest integer k are exact for the 24-bit uniforms, so
 // the only rounding before quadrant_sincos is r = (4u - k) pi/2.
