@@ -212,13 +212,19 @@ struct PolicyArgs {
 };
 
 // KernelRng::uniform / normal (policy_pipeline.rs:441-456): 53-bit uniform,
-// Box–Muller on two uniforms, cosine branch, in double.
+// Box–Muller on two uniforms, cosine branch, in double. ln u1 is bm_log (u1 >=
+// 1e-300, a normal number; within about 2 ulp of the library log) and the
+// cosine the step kernels' closed-form angle_sincos: about a third of the
+// library routines' instructions, and these 37 normals per world and control
+// step are the part of the policy kernel that does not overlap its MFMAs.
 __device__ __forceinline__ double policy_uniform(u64& s) { return (double)(xorshift64(s) >> 11) * 0x1.0p-53; }
 __device__ __forceinline__ double policy_normal(u64& s) {
   double u1 = policy_uniform(s);
   const double u2 = policy_uniform(s);
   if (u1 < 1e-300) u1 = 1e-300;
-  return sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925286766559 * u2);
+  double sn, cs;
+  angle_sincos(6.283185307179586476925286766559 * u2, &sn, &cs);
+  return sqrt(-2.0 * bm_log(u1)) * cs;
 }
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
