@@ -282,6 +282,16 @@ template <class T> struct Eps;
 template <> struct Eps<double> { static constexpr double v = 2.220446049250313e-16; };
 template <> struct Eps<float> { static constexpr float v = 1e-6f; };
 
+// From here to the end of the file (vector and spatial algebra, contact laws,
+// the articulated-body passes, integration) a kernel built with PHZ_REASSOC
+// lets the compiler reassociate floating-point sums and products: a change at
+// the rounding level, since nothing below relies on the order of its
+// operations (no compensated sums, no magic-number rounding, no argument
+// reduction). The closed-form sines, cosines and logarithms above keep their
+// written order in every build.
+#if PHZ_REASSOC
+#pragma clang fp reassociate(on)
+#endif
 template <class T> struct V3 { T x, y, z; };
 template <class T> __device__ __forceinline__ V3<T> v3(T x, T y, T z) { return V3<T>{x, y, z}; }
 template <class T> __device__ __forceinline__ V3<T> operator+(V3<T> a, V3<T> b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
@@ -609,7 +619,14 @@ template <class M, class T> __device__ __forceinline__ T terrain_at(const Terrai
 
 // Contact point cp of body i's shape, body frame: a box corner, or the
 // support point against body-frame direction d (phyz_kernels.cu:667-730).
-template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_point(int cp, V3<T> d) {
+// The shape's sign and threshold tests (which end of a capsule or cylinder,
+// which corner of a mesh box, whether a cylinder's rim is defined) read dd, the
+// same direction in precision D: f32 kernels with the f64 height chain pass
+// the chain's f64 direction, so that the point is the one whose depth the chain
+// computed. A capsule lying within f32 rounding of level would otherwise touch
+// at one end and take its force at the other.
+template <class M, class T, int i, class D = T>
+__device__ __forceinline__ V3<T> contact_point(int cp, V3<T> d, V3<D> dd) {
   constexpr int gt = M::gtype[i];
   const R3<T> oR = R3<T>{{T(M::gorot[i][0]), T(M::gorot[i][1]), T(M::gorot[i][2]), T(M::gorot[i][3]), T(M::gorot[i][4]),
                           T(M::gorot[i][5]), T(M::gorot[i][6]), T(M::gorot[i][7]), T(M::gorot[i][8])}};
@@ -619,23 +636,30 @@ template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_poin
                       T(M::gp[i][2] * ((cp & 4) ? 1.0 : -1.0)));
     return oP + tmul(oR, corner);
   } else {
-    V3<T> n = mul(oR, d);
+    const R3<D> oRd = R3<D>{{D(M::gorot[i][0]), D(M::gorot[i][1]), D(M::gorot[i][2]), D(M::gorot[i][3]),
+                             D(M::gorot[i][4]), D(M::gorot[i][5]), D(M::gorot[i][6]), D(M::gorot[i][7]),
+                             D(M::gorot[i][8])}};
+    const V3<T> n = mul(oR, d);
+    const V3<D> nd = mul(oRd, dd);
     V3<T> sp;
     if constexpr (gt == G_SPHERE) {
       sp = n * T(-M::gp[i][0]);
     } else if constexpr (gt == G_CAPSULE) {
-      sp = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * dsign(n.z)) - n * T(M::gp[i][0]);
+      sp = v3(T(0), T(0), T(-0.5 * M::gp[i][1]) * T(dsign(nd.z))) - n * T(M::gp[i][0]);
     } else if constexpr (gt == G_CYLINDER) {
-      T rl = dsqrt(n.x * n.x + n.y * n.y);
-      T f = rl > T(1e-6) ? T(M::gp[i][0]) / dmax(rl, T(5e-7)) : T(0);
-      sp = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * dsign(n.z));
+      const D rl = dsqrt(nd.x * nd.x + nd.y * nd.y);
+      const T f = rl > D(1e-6) ? T(D(M::gp[i][0]) / dmax(rl, D(5e-7))) : T(0);
+      sp = v3(-n.x * f, -n.y * f, T(-0.5 * M::gp[i][1]) * T(dsign(nd.z)));
     } else {  // mesh AABB
-      sp = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * dsign(n.x),
-              T(0.5 * (M::gp[i][1] + M::gp[i][4])) - T(0.5 * (M::gp[i][4] - M::gp[i][1])) * dsign(n.y),
-              T(0.5 * (M::gp[i][2] + M::gp[i][5])) - T(0.5 * (M::gp[i][5] - M::gp[i][2])) * dsign(n.z));
+      sp = v3(T(0.5 * (M::gp[i][0] + M::gp[i][3])) - T(0.5 * (M::gp[i][3] - M::gp[i][0])) * T(dsign(nd.x)),
+              T(0.5 * (M::gp[i][1] + M::gp[i][4])) - T(0.5 * (M::gp[i][4] - M::gp[i][1])) * T(dsign(nd.y)),
+              T(0.5 * (M::gp[i][2] + M::gp[i][5])) - T(0.5 * (M::gp[i][5] - M::gp[i][2])) * T(dsign(nd.z)));
     }
     return oP + tmul(oR, sp);
   }
+}
+template <class M, class T, int i> __device__ __forceinline__ V3<T> contact_point(int cp, V3<T> d) {
+  return contact_point<M, T, i, T>(cp, d, d);
 }
 
 // SolImp impedance with the margin taper, smoothstep restitution, and the
@@ -721,7 +745,8 @@ __device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_n
 // point (x, y, h), summed world force) at out[k * S], k = 8 i .. 8 i + 7.
 template <class M, class T, int i>
 __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const double* cz64,
-                                              const Terrain<T>& tr, T* out, int S, bool write) {
+                                              const V3<double>& zb64, const Terrain<T>& tr, T* out, int S,
+                                              bool write) {
   constexpr int gt = M::gtype[i];
   constexpr int npts = gt == G_BOX ? 8 : 1;
   constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
@@ -734,7 +759,9 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
   bool any = false;
 #pragma unroll
   for (int cp = 0; cp < npts; cp++) {
-    const V3<T> sup = contact_point<M, T, i>(cp, zb);
+    V3<T> sup;
+    if constexpr (pen64<M, T>()) sup = contact_point<M, T, i, double>(cp, zb, zb64);
+    else sup = contact_point<M, T, i>(cp, zb);
     V3<T> supw = pw + mul(Rw, sup);
     V3<T> nw;
     const T th = terrain_at<M, T>(tr, supw.x, supw.y, nw);
@@ -815,7 +842,7 @@ template <class M, class T> struct GroundPrep {
 // Body i's contact geometry; writes the position part of its readback row
 // (touching, deepest penetration, deepest point) when `write`.
 template <class M, class T, int i>
-__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const double* cz64,
+__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const double* cz64, const V3<double>& zb64,
                                                const Terrain<T>& tr, GroundPrep<M, T>& gp, T* out, int S, bool write) {
   constexpr int n = ground_pts<M>(i), o = ground_off<M>(i);
   const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
@@ -825,7 +852,8 @@ __device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const 
   int nact = 0;
 #pragma unroll
   for (int cp = 0; cp < n; cp++) {
-    gp.sup[o + cp] = contact_point<M, T, i>(cp, zb);
+    if constexpr (pen64<M, T>()) gp.sup[o + cp] = contact_point<M, T, i, double>(cp, zb, zb64);
+    else gp.sup[o + cp] = contact_point<M, T, i>(cp, zb);
     supw[cp] = pw + mul(Rw, gp.sup[o + cp]);
     V3<T> nw;
     const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw);
@@ -1182,7 +1210,8 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
   }
   if constexpr (M::gtype[i] != G_NONE) {
     if (do_contact) {
-      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], ws.cz64 + ground_off<M>(i), tr, rows, S, write_rows);
+      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], ws.cz64 + ground_off<M>(i), ws.zb64[i], tr, rows, S,
+                                             write_rows);
       ws.pA[i] = ws.pA[i] - f;
     }
   }
@@ -1821,7 +1850,8 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
     if constexpr (M::gtype[i] != G_NONE)
-      ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws.cz64 + ground_off<M>(i), tr, gp, rows, S, write_rows);
+      ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws.cz64 + ground_off<M>(i), ws.zb64[i], tr, gp, rows, S,
+                              write_rows);
   });
   // Each sweep moves qdd by the ABA's response to that sweep's change of the
   // contact forces (the solve is affine in them): qdd and ext carry from one
@@ -2035,4 +2065,7 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
   if constexpr (M::NNOISE > 0 && G == (M::NOISE_G >= 0 ? M::NOISE_G : 0)) a.rng[w] = rng;
 }
 
+#if PHZ_REASSOC
+#pragma clang fp reassociate(off)
+#endif
 }  // namespace phz

@@ -40,3 +40,24 @@ def test_f32_late_state_parity(cfg, steps):
     print(f"  qdd rel err max {e.max():.3e} p99 {np.percentile(e, 99):.3e} median {np.median(e):.3e}; "
           f"within 1e-4 {np.mean(e <= TOL_F32):.4f} {extra}", flush=True)
     assert e.max() <= tol, f"world {idx[e.argmax()]}: {e.max():.3e}"
+
+
+def test_level_capsule_touches_where_its_depth_was_taken():
+    """A late MJCF-ant state whose front ankle capsule lies within f32 rounding
+    of level (its axis' world-z component is 3.8e-9 in f64): both ends are
+    equally deep, and which end touches is decided by the sign of that
+    component. The f32 kernel takes the decision from its f64 height chain, so
+    the force acts at the end whose depth was computed, as in the f64 oracle;
+    an f32 decision picked the other end here (qdd error 1.94)."""
+    import os
+    w = W.config(7)
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "mjcf_ant_level_capsule_state.npz"))
+    n = 64
+    q, v, c, _ = w.initial_state(n)
+    q[:] = fx["q"].astype(np.float64)
+    v[:] = fx["v"].astype(np.float64)
+    sim = from_workload(w, "f32", nworld=n)
+    sim.load_states(q, v, c)
+    e, _ = late_step_errors(w, sim, "f32", np.arange(n))
+    print(f"qdd rel err max {e.max():.3e}", flush=True)
+    assert e.max() <= TOL_F32
