@@ -407,23 +407,77 @@ template <class T> __device__ __forceinline__ void sym_rot(const T* m, const R3<
 #pragma unroll
     for (int j = i; j < 3; j++) out[sx(i, j)] = E.m[i] * t[j] + E.m[3 + i] * t[3 + j] + E.m[6 + i] * t[6 + j];
 }
+// E^T M E for E a rotation about coordinate axis k: E_kk = 1, no other
+// entries in row or column k, and on the plane (u, w) = (k + 1, k + 2) mod 3
+// the block [[c, s], [-s, c]]. The plane block of E^T M E turns by twice the
+// angle: with h = (m_uu + m_ww) / 2, d = (m_uu - m_ww) / 2,
+//   m'_uu = h + d cos2 - m_uw sin2,  m'_ww = h - d cos2 + m_uw sin2,
+//   m'_uw = d sin2 + m_uw cos2,
+// and the plane entries of column k turn by the angle itself. c2h, s2h are
+// cos2 / 2 = 1/2 - s^2 and sin2 / 2 = c s.
+template <class T, int k>
+__device__ __forceinline__ void sym_rot_axis(const T* m, T c, T s, T c2h, T s2h, T* out) {
+  constexpr int u = (k + 1) % 3, w = (k + 2) % 3;
+  const T muu = m[sx(u, u)], mww = m[sx(w, w)], muw = m[sx(u, w)];
+  const T h2 = muu + mww, d2 = muu - mww;
+  const T t = d2 * c2h - muw * (s2h + s2h);
+  out[sx(u, u)] = T(0.5) * h2 + t;
+  out[sx(w, w)] = T(0.5) * h2 - t;
+  out[sx(u, w)] = d2 * s2h + muw * (c2h + c2h);
+  const T muk = m[sx(u, k)], mwk = m[sx(w, k)];
+  out[sx(u, k)] = c * muk - s * mwk;
+  out[sx(w, k)] = s * muk + c * mwk;
+  out[sx(k, k)] = m[sx(k, k)];
+}
+// The same for a general 3x3 M (row-major): with p, r, t, q the halved sums
+// m_uu + m_ww, m_uu - m_ww, m_uw + m_wu, m_uw - m_wu, the plane block is
+//   m'_uu = p + (r cos2 - t sin2),  m'_ww = p - (r cos2 - t sin2),
+//   m'_uw = q + (r sin2 + t cos2),  m'_wu = -q + (r sin2 + t cos2);
+// row k and column k turn by the angle.
+template <class T, int k>
+__device__ __forceinline__ void gen_rot_axis(const T* m, T c, T s, T c2h, T s2h, T* out) {
+  constexpr int u = (k + 1) % 3, w = (k + 2) % 3;
+  const T muu = m[u * 3 + u], mww = m[w * 3 + w], muw = m[u * 3 + w], mwu = m[w * 3 + u];
+  const T p2 = muu + mww, r2 = muu - mww, t2 = muw + mwu, q2 = muw - mwu;
+  const T rr = r2 * c2h - t2 * s2h, tt = r2 * s2h + t2 * c2h;
+  out[u * 3 + u] = T(0.5) * p2 + rr;
+  out[w * 3 + w] = T(0.5) * p2 - rr;
+  out[u * 3 + w] = T(0.5) * q2 + tt;
+  out[w * 3 + u] = tt - T(0.5) * q2;
+  out[u * 3 + k] = c * m[u * 3 + k] - s * m[w * 3 + k];
+  out[w * 3 + k] = s * m[u * 3 + k] + c * m[w * 3 + k];
+  out[k * 3 + u] = c * m[k * 3 + u] - s * m[k * 3 + w];
+  out[k * 3 + w] = s * m[k * 3 + u] + c * m[k * 3 + w];
+  out[k * 3 + k] = m[k * 3 + k];
+}
 // X^T I X = T^T (Rot^T I Rot) T with T = [1 0; -r x 1]:
 //   A1 = E^T A E, B1 = E^T B E, C1 = E^T C E
 //   B2 = B1 + r x C1,  A2 = A1 - B1 r x + r x B2^T,  C2 = C1
-template <class T> __device__ __forceinline__ Sym<T> sym_xtix(const Sym<T>& I, const Xf<T>& X) {
+// KAX >= 0: X.E is a rotation about coordinate axis KAX (see sym_rot_axis).
+template <class T, int KAX = -1> __device__ __forceinline__ Sym<T> sym_xtix(const Sym<T>& I, const Xf<T>& X) {
   const R3<T>& E = X.E;
   Sym<T> o;
-  sym_rot(I.a, E, o.a);
-  sym_rot(I.c, E, o.c);
-  T t[9], b1[9];
+  T b1[9];
+  if constexpr (KAX >= 0) {
+    constexpr int u = (KAX + 1) % 3, w = (KAX + 2) % 3;
+    const T c = E.m[u * 3 + u], s = E.m[u * 3 + w];
+    const T c2h = T(0.5) - s * s, s2h = c * s;
+    sym_rot_axis<T, KAX>(I.a, c, s, c2h, s2h, o.a);
+    sym_rot_axis<T, KAX>(I.c, c, s, c2h, s2h, o.c);
+    gen_rot_axis<T, KAX>(I.b, c, s, c2h, s2h, b1);
+  } else {
+    sym_rot(I.a, E, o.a);
+    sym_rot(I.c, E, o.c);
+    T t[9];
 #pragma unroll
-  for (int i = 0; i < 3; i++)
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-    for (int j = 0; j < 3; j++) t[i * 3 + j] = I.b[i * 3] * E.m[j] + I.b[i * 3 + 1] * E.m[3 + j] + I.b[i * 3 + 2] * E.m[6 + j];
+      for (int j = 0; j < 3; j++) t[i * 3 + j] = I.b[i * 3] * E.m[j] + I.b[i * 3 + 1] * E.m[3 + j] + I.b[i * 3 + 2] * E.m[6 + j];
 #pragma unroll
-  for (int i = 0; i < 3; i++)
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-    for (int j = 0; j < 3; j++) b1[i * 3 + j] = E.m[i] * t[j] + E.m[3 + i] * t[3 + j] + E.m[6 + i] * t[6 + j];
+      for (int j = 0; j < 3; j++) b1[i * 3 + j] = E.m[i] * t[j] + E.m[3 + i] * t[3 + j] + E.m[6 + i] * t[6 + j];
+  }
   const V3<T> r = X.r;
 #pragma unroll
   for (int j = 0; j < 3; j++) {
@@ -1444,7 +1498,7 @@ template <class M, class T, int i> __device__ __forceinline__ void body_integrat
 // I_A[p] += X^T I_a X, p_A[p] += X^T p_a.
 template <class M, class T, int i>
 __device__ __forceinline__ void propagate(WS<M, T>& ws, const Sym<T>& Ia, const SV<T>& pa, Sym<T>& dI, SV<T>& dp) {
-  dI = sym_xtix(Ia, ws.X[i]);
+  dI = sym_xtix<T, M::rot_axis[i]>(Ia, ws.X[i]);
   dp = inv_apply_force(ws.X[i], pa);
 }
 

@@ -656,6 +656,16 @@ std::string gen_model(const ModelD& m, const Features& f) {
     if (nz != 1 || std::fabs(b.axis[k]) != 1.0) return -1;
     return b.jtype == 0 ? k : 3 + k;
   });
+  // A revolute joint about a coordinate axis with no rotation from the
+  // parent (X.E a rotation about that axis, see sym_xtix): the axis, else -1.
+  ib("rot_axis", [&](int i) {
+    const BodyD& b = m.b[i];
+    if (b.jtype != 0 || !ptj_id[i]) return -1;
+    int k = -1, nz = 0;
+    for (int c = 0; c < 3; c++)
+      if (b.axis[c] != 0.0) { nz++; k = c; }
+    return nz == 1 && std::fabs(b.axis[k]) == 1.0 ? k : -1;
+  });
   db("mass", [&](int i) { return m.b[i].mass; });
   d2("com", 3, [&](int i, int k) { return m.b[i].com[k]; });
   d2("inA", 6, [&](int i, int k) { return A[i * 6 + k]; });
