@@ -20,7 +20,8 @@ TOL_F32 = 1e-4
 TOL_F32_IMPULSE = 2e-4
 
 
-@pytest.mark.parametrize("cfg,steps", [(3, 1000), (3, 300), (4, 1000), (6, 1000), (7, 1000), (8, 300)])
+@pytest.mark.parametrize("cfg,steps", [(3, 1000), (3, 300), (4, 1000), (6, 1000), (7, 1000), (7, 2000), (8, 300),
+                                       (8, 1000), (9, 1000)])
 def test_f32_late_state_parity(cfg, steps):
     w = W.config(cfg)
     n = 2048
