@@ -1095,6 +1095,8 @@ template <class M, class T> struct WS {
   double pz64[M::NB];
   double cz64[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];  // contact points' world heights
   T ts[M::NB], tc[M::NB];  // revolute joints' sin and cos of -q (split-lane kernels)
+  Sym<T> cI[M::NB];        // a group's summed subtree contributions to trunk body p (groups other than 0)
+  SV<T> cP[M::NB];
 };
 
 // Column k, entry r of U = I_A S of body i. A free joint's S is the identity,
@@ -1688,7 +1690,14 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
         SV<T> dp;
         propagate<M, T, i>(ws, Ia, pa, dI, dp);
         if (!ws.ok[i]) { dI = Sym<T>{}; dp = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))}; }
-        put_sym(lds, M::slot_contrib[i], lane, dI, dp);
+        if constexpr (M::contrib_first[i]) {
+          ws.cI[p] = dI;
+          ws.cP[p] = dp;
+        } else {
+          sym_add(ws.cI[p], dI);
+          ws.cP[p] = ws.cP[p] + dp;
+        }
+        if constexpr (M::contrib_put[i]) put_sym(lds, M::slot_contrib[i], lane, ws.cI[p], ws.cP[p]);
       } else {
         if (ws.ok[i]) {
           Sym<T> dI;
@@ -1708,10 +1717,11 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
       if (draw_next) draw_shared_noise<M, T>(rng, lds, lane);
     }
     if constexpr (G == 0) {
-      // Contributions of the other groups' subtrees, in body order.
+      // The other groups' summed subtree contributions, in body order.
       sfor<0, NB>([&](auto I) {
         constexpr int i = decltype(I)::value;
-        if constexpr (M::slot_contrib[i] >= 0) add_sym(lds, M::slot_contrib[i], lane, ws.IA[M::parent[i]], ws.pA[M::parent[i]]);
+        if constexpr (M::slot_contrib[i] >= 0 && M::contrib_put[i])
+          add_sym(lds, M::slot_contrib[i], lane, ws.IA[M::parent[i]], ws.pA[M::parent[i]]);
       });
       rfor<NT>([&](auto K) {
         constexpr int i = M::tlist[decltype(K)::value];

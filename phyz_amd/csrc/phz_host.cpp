@@ -24,6 +24,7 @@
 #include <cstring>
 #include <fstream>
 #include <memory>
+#include <map>
 #include <mutex>
 #include <sstream>
 #include <string>
@@ -530,17 +531,26 @@ std::string gen_model(const ModelD& m, const Features& f) {
       dof_owner[j] = is_trunk[i] ? 0 : owner[i];
       if (is_trunk[i]) tdof[j] = ntd++;
     }
-  // LDS slots (floating trunk): 27 per subtree root handed to group 0, 6 per
-  // trunk body whose acceleration other groups read, 2 per trunk DOF.
-  std::vector<int> slot_contrib(nb, -1), slot_acc(nb, -1);
+  // LDS slots (floating trunk): 27 per (group, trunk body) pair through which
+  // a group other than 0 hands its subtrees' summed contributions to group 0,
+  // 6 per trunk body whose acceleration other groups read, 2 per trunk DOF.
+  // A group's subtree roots under one trunk body share the slot: pass 2 runs
+  // them in decreasing body order, so the highest-numbered root starts the sum
+  // (contrib_first) and the lowest stores it (contrib_put).
+  std::vector<int> slot_contrib(nb, -1), slot_acc(nb, -1), contrib_first(nb, 0), contrib_put(nb, 0);
   int nslot = 0;
   if (pl.mode == 2) {
+    std::map<std::pair<int, int>, std::vector<int>> roots;  // (group, trunk parent) -> roots, ascending
     for (int i = 0; i < nb; i++)
-      if (!is_trunk[i] && m.b[i].parent >= 0 && is_trunk[m.b[i].parent] && owner[i] != 0) {
-        slot_contrib[i] = nslot;
-        nslot += 27;
-        if (slot_acc[m.b[i].parent] < 0) { slot_acc[m.b[i].parent] = -2; }
-      }
+      if (!is_trunk[i] && m.b[i].parent >= 0 && is_trunk[m.b[i].parent] && owner[i] != 0)
+        roots[{owner[i], m.b[i].parent}].push_back(i);
+    for (auto& kv : roots) {
+      for (int i : kv.second) slot_contrib[i] = nslot;
+      nslot += 27;
+      contrib_first[kv.second.back()] = 1;
+      contrib_put[kv.second.front()] = 1;
+      if (slot_acc[kv.first.second] < 0) slot_acc[kv.first.second] = -2;
+    }
     for (int i = 0; i < nb; i++) if (slot_acc[i] == -2) { slot_acc[i] = nslot; nslot += 6; }
   }
   const int slot_state = nslot;
@@ -629,6 +639,8 @@ std::string gen_model(const ModelD& m, const Features& f) {
   bb("is_trunk", [&](int i) { return is_trunk[i]; });
   ib("slot_contrib", [&](int i) { return slot_contrib[i]; });
   ib("slot_acc", [&](int i) { return slot_acc[i]; });
+  bb("contrib_first", [&](int i) { return contrib_first[i]; });
+  bb("contrib_put", [&](int i) { return contrib_put[i]; });
   ib("jtype", [&](int i) { return m.b[i].jtype; });
   ib("qoff", [&](int i) { return m.b[i].qoff; });
   ib("voff", [&](int i) { return m.b[i].voff; });
