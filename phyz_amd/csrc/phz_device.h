@@ -75,27 +75,6 @@ __device__ __forceinline__ void angle_sincos(double x, double* s, double* c);
 // f64 joint angles take the closed form below (reduction exact for |x| < 1.6e6)
 // rather than the library routine and its large-argument branch.
 __device__ __forceinline__ void dsincos(double x, double* s, double* c) { angle_sincos(x, s, c); }
-// sin and cos of r in [-pi/4, pi/4] (f32), then of k pi/2 + r: Taylor series
-// through r^9 and r^10 (truncation below 3e-9 on the interval) and the
-// quadrant's sign and swap. Used for the Box-Muller angle below; joint angles
-// take the library routine, whose small-argument path is as short.
-__device__ __forceinline__ void quadrant_sincos(float r, float k, float* s, float* c) {
-  const float r2 = r * r;
-  float ps = fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
-  ps = fmaf(r2, ps, 1.0f / 120.0f);
-  ps = fmaf(r2, ps, -1.0f / 6.0f);
-  const float sr = fmaf(r * r2, ps, r);
-  float pc = fmaf(r2, -1.0f / 3628800.0f, 1.0f / 40320.0f);
-  pc = fmaf(r2, pc, -1.0f / 720.0f);
-  pc = fmaf(r2, pc, 1.0f / 24.0f);
-  pc = fmaf(r2, pc, -0.5f);
-  const float cr = fmaf(r2, pc, 1.0f);
-  const int q = (int)k & 3;
-  const float a = (q & 1) ? cr : sr;
-  const float b = (q & 1) ? sr : cr;
-  *s = (q & 2) ? -a : a;
-  *c = ((q + 1) & 2) ? -b : b;
-}
 __device__ __forceinline__ void angle_sincos(float x, float* s, float* c);
 __device__ __forceinline__ void dsincos(float x, float* s, float* c) { angle_sincos(x, s, c); }
 __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
@@ -169,6 +148,22 @@ __device__ __forceinline__ void angle_sincos(float xf, float* s, float* c) {
   *s = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? cr : sr) ^ ss);
   *c = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, odd ? sr : cr) ^ cs);
 }
+// sin and cos of a revolute joint's f32 angle, for its rotation matrix, where
+// the absolute error is what counts: x in turns, t = x / 2pi in f64 (its
+// rounding 1e-16 relative), reduced to its fractional part in [-1/2, 1/2] in
+// f64 and rounded to f32 (3e-8 turns), then the hardware v_sin_f32 /
+// v_cos_f32, which take turns: their largest error measured on gfx950 was
+// 1.25e-7 absolute, over [0, 1) turns and over joint angles in [-60, 60] rad.
+// About 3e-7 absolute in all, against 6e-8 for angle_sincos, in seven
+// instructions instead of about twenty. angle_sincos stays where a small
+// angle's relative error matters (a free joint's quaternion exponential).
+__device__ __forceinline__ void rev_sincos(float xf, float* s, float* c) {
+  const double t = (double)xf * 0.15915494309189535;
+  const float x = (float)(t - rint(t));
+  *s = __builtin_amdgcn_sinf(x);
+  *c = __builtin_amdgcn_cosf(x);
+}
+__device__ __forceinline__ void rev_sincos(double x, double* s, double* c) { angle_sincos(x, s, c); }
 // ln x for x in [2^-53, 1] (1 - u of the f64 Box-Muller radius), within
 // about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from the hardware
 // frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) / (m + 1),
@@ -208,13 +203,12 @@ __device__ __forceinline__ float bm_radius(float u) {
   return __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(1.0f - u));
 }
 __device__ __forceinline__ double bm_radius(double u) { return sqrt(-2.0 * bm_log(1.0 - u)); }
-// sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1), in
-// turns: 4u and its nearest integer k are exact for the 24-bit uniforms, so
-// the only rounding before quadrant_sincos is r = (4u - k) pi/2.
+// sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1): u is
+// the angle in turns, which the hardware v_sin_f32 / v_cos_f32 take as they
+// are (1.25e-7 absolute at most, see angle_sincos(float)); f64 as angle_sincos.
 __device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
-  const float t = 4.0f * u;
-  const float k = rintf(t);
-  quadrant_sincos((t - k) * 0x1.921fb6p+0f, k, s, c);
+  *s = __builtin_amdgcn_sinf(u);
+  *c = __builtin_amdgcn_cosf(u);
 }
 __device__ __forceinline__ void turn_sincos(double u, double* s, double* c) {
   angle_sincos(6.283185307179586 * u, s, c);
@@ -1136,7 +1130,7 @@ __device__ __forceinline__ void joint_xf(const T* q, const T* v, Xf<T>& X, SV<T>
   vj = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
   if constexpr (jt == J_REV) {
     T s, c;
-    dsincos(-q[qo], &s, &c);
+    rev_sincos(-q[qo], &s, &c);
     rev_xf<M, T, i>(s, c, v, X, vj);
   } else if constexpr (jt == J_PRIS) {
     X.E = Rp;
@@ -1632,7 +1626,7 @@ template <class M, class T> __device__ __forceinline__ void trig_prepass(WS<M, T
       }
     });
     T sn, cs;
-    dsincos(ang, &sn, &cs);
+    rev_sincos(ang, &sn, &cs);
     sfor<0, L>([&](auto O) {
       constexpr int o = decltype(O)::value;
       if constexpr (u * L + o < M::NREV) {
