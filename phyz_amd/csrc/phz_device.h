@@ -257,6 +257,9 @@ __device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x);
 // the heightfield cell lookup keep their correctly rounded f32 divisions.
 __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
+// a / b: f32 through the hardware reciprocal (about 2 ulp), f64 correctly rounded.
+__device__ __forceinline__ float fdiv(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
+__device__ __forceinline__ double fdiv(double a, double b) { return a / b; }
 // Square root on the penalty-contact path: f32 the hardware v_sqrt_f32 (within
 // 1 ulp, no correction sequence), f64 the correctly rounded one.
 __device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
@@ -505,14 +508,17 @@ template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
   T s, c;
   dsincos(ang * T(0.5), &s, &c);
   const bool small = ang < T(Eps<T>::v);
-  T f = small ? T(0.5) : s / dmax(ang, T(0.5) * T(Eps<T>::v));
+  T f = small ? T(0.5) : fdiv(s, dmax(ang, T(0.5) * T(Eps<T>::v)));
   return {small ? T(1) : c, w.x * f, w.y * f, w.z * f};
 }
+// Rotation vector of q. Outside the small-angle branch any positive scale of
+// a unit quaternion gives the same result; the products of unit quaternions
+// that the integration passes are unit to rounding.
 template <class T> __device__ __forceinline__ V3<T> quat_log(const Q<T>& q) {
   V3<T> v = v3(q.x, q.y, q.z);
   T n = dsqrt(dot(v, v));
   const bool small = n < T(Eps<T>::v);
-  T f = small ? T(2) : T(2) * datan2(n, q.w) / dmax(n, T(0.5) * T(Eps<T>::v));
+  T f = small ? T(2) : fdiv(T(2) * datan2(n, q.w), dmax(n, T(0.5) * T(Eps<T>::v)));
   return v * f;
 }
 // Rotation matrix of unit q (active), row-major.
@@ -1074,6 +1080,12 @@ __device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw,
 //      through LDS, group 0 finishes the trunk and hands back the branch-point
 //      accelerations and the new trunk state. Two workgroup barriers per step.
 // A workgroup is NG waves over the same 64 worlds; wave g runs group g's code.
+// f32 kernels with the f64 height chain compute a ball or free joint's
+// quaternion in f64 in pass 1; the integration takes its rounding instead of
+// a second, f32 exponential of the same rotation vector.
+template <class M, class T, int i> constexpr bool quat_from_pass1() {
+  return pen64<M, T>() && M::need_world[i] && (M::jtype[i] == J_BALL || M::jtype[i] == J_FREE);
+}
 template <class M, class T> struct WS {
   Xf<T> X[M::NB];
   SV<T> vel[M::NB], cb[M::NB], pA[M::NB], acc[M::NB];
@@ -1091,6 +1103,7 @@ template <class M, class T> struct WS {
   T ts[M::NB], tc[M::NB];  // revolute joints' sin and cos of -q (split-lane kernels)
   Sym<T> cI[M::NB];        // a group's summed subtree contributions to trunk body p (groups other than 0)
   SV<T> cP[M::NB];
+  Q<T> qj[M::NB];          // a ball or free joint's quaternion from pass 1's f64 transform (quat_from_pass1)
 };
 
 // Column k, entry r of U = I_A S of body i. A free joint's S is the identity,
@@ -1164,7 +1177,8 @@ template <class T> __device__ __forceinline__ Q<double> quat_exp64(V3<T> wf) {
 }
 
 // Body i's joint rotation and offset (joint_xf's X.E and X.r) in f64.
-template <class M, class T, int i> __device__ __forceinline__ void joint_xf64(const T* q, R3<double>& E, V3<double>& r) {
+template <class M, class T, int i>
+__device__ __forceinline__ void joint_xf64(const T* q, R3<double>& E, V3<double>& r, Q<double>* qj = nullptr) {
   constexpr int jt = M::jtype[i];
   constexpr int qo = M::qoff[i];
   const R3<double> Rp = R3<double>{{M::ptj_rot[i][0], M::ptj_rot[i][1], M::ptj_rot[i][2], M::ptj_rot[i][3],
@@ -1184,7 +1198,9 @@ template <class M, class T, int i> __device__ __forceinline__ void joint_xf64(co
     E = Rp;
     r = pp + tmul(Rp, v3(M::axis[i][0], M::axis[i][1], M::axis[i][2]) * double(q[qo]));
   } else if constexpr (jt == J_BALL || jt == J_FREE) {
-    R3<double> EJ = transpose(quat_mat(quat_exp64(v3(q[qo], q[qo + 1], q[qo + 2]))));
+    const Q<double> qq = quat_exp64(v3(q[qo], q[qo + 1], q[qo + 2]));
+    if (qj) *qj = qq;
+    R3<double> EJ = transpose(quat_mat(qq));
     E = M::ptj_identity[i] ? EJ : mul(EJ, Rp);
     if constexpr (jt == J_FREE) r = pp + tmul(Rp, v3(double(q[qo + 3]), double(q[qo + 4]), double(q[qo + 5])));
     else r = pp;
@@ -1220,7 +1236,9 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
     // Rw_i = Rw_p X.E^T: third row zb_i = X.E zb_p; Pw_i = Pw_p + Rw_p X.r.
     R3<double> E64;
     V3<double> r64;
-    joint_xf64<M, T, i>(q, E64, r64);
+    Q<double> q64;
+    joint_xf64<M, T, i>(q, E64, r64, &q64);
+    if constexpr (quat_from_pass1<M, T, i>()) ws.qj[i] = Q<T>{T(q64.w), T(q64.x), T(q64.y), T(q64.z)};
 #pragma unroll
     for (int k = 0; k < 9; k++) X.E.m[k] = T(E64.m[k]);
     X.r = v3(T(r64.x), T(r64.y), T(r64.z));
@@ -1463,7 +1481,8 @@ template <class M, class T, int i> __device__ __forceinline__ void body_pass3(WS
 }
 
 // Semi-implicit Euler for body i's joint (integrate.rs:41-92); v += dt qdd first.
-template <class M, class T, int i> __device__ __forceinline__ void body_integrate(T* q, T* v, const T* qdd) {
+template <class M, class T, int i, bool QJ = false>
+__device__ __forceinline__ void body_integrate(T* q, T* v, const T* qdd, const Q<T>& qj = Q<T>{}) {
   constexpr int jt = M::jtype[i];
   constexpr int nd = ndof_of(jt);
   constexpr int qo = M::qoff[i], vo = M::voff[i];
@@ -1473,16 +1492,19 @@ template <class M, class T, int i> __device__ __forceinline__ void body_integrat
   if constexpr (jt == J_REV || jt == J_PRIS) {
     q[qo] = q[qo] + dt * v[vo];
   } else if constexpr (jt == J_BALL || jt == J_FREE) {
-    Q<T> cur = quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]));
+    Q<T> cur;
+    if constexpr (QJ) cur = qj;
+    else cur = quat_exp(v3(q[qo], q[qo + 1], q[qo + 2]));
     if constexpr (jt == J_FREE) {
       V3<T> wl = qrotate(cur, v3(v[vo + 3], v[vo + 4], v[vo + 5]));
       q[qo + 3] = q[qo + 3] + dt * wl.x;
       q[qo + 4] = q[qo + 4] + dt * wl.y;
       q[qo + 5] = q[qo + 5] + dt * wl.z;
     }
+    // The product is not normalised: it is unit to rounding, and quat_log is
+    // scale-free (atan2(s n, s w) = atan2(n, w), v / |v|), so the reference's
+    // normalisation would move the result by rounding only.
     Q<T> nx = qmul(cur, quat_exp(v3(v[vo], v[vo + 1], v[vo + 2]) * dt));
-    T n = dsqrt(nx.w * nx.w + nx.x * nx.x + nx.y * nx.y + nx.z * nx.z);
-    nx = Q<T>{nx.w / n, nx.x / n, nx.y / n, nx.z / n};
     V3<T> lg = quat_log(nx);
     q[qo] = lg.x;
     q[qo + 1] = lg.y;
@@ -1742,7 +1764,7 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
           lds_put(lds, s, lane, ws.acc[i].a.x); lds_put(lds, s + 1, lane, ws.acc[i].a.y); lds_put(lds, s + 2, lane, ws.acc[i].a.z);
           lds_put(lds, s + 3, lane, ws.acc[i].l.x); lds_put(lds, s + 4, lane, ws.acc[i].l.y); lds_put(lds, s + 5, lane, ws.acc[i].l.z);
         }
-        body_integrate<M, T, i>(q, v, qdd);
+        body_integrate<M, T, i, quat_from_pass1<M, T, i>()>(q, v, qdd, ws.qj[i]);
       });
       sfor<0, M::NQ>([&](auto J) {
         constexpr int j = decltype(J)::value;
@@ -1781,7 +1803,7 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
   sfor<0, NL>([&](auto K) {
     constexpr int i = M::glist[G][decltype(K)::value];
     body_pass3<M, T, i>(ws, qdd);
-    body_integrate<M, T, i>(q, v, qdd);
+    body_integrate<M, T, i, quat_from_pass1<M, T, i>()>(q, v, qdd, ws.qj[i]);
   });
 }
 
