@@ -182,3 +182,28 @@ def test_worlds_independent_and_nan_isolated():
     bad = ~np.isfinite(qg).all(axis=1) | ~np.isfinite(vg).all(axis=1)
     assert bad[7]
     assert not bad[np.arange(130) != 7].any()
+
+
+@pytest.mark.parametrize("cfg,prec", [(4, "f64"), (5, "f64"), (7, "f64"), (8, "f64"), (9, "f64"), (8, "f32"), (9, "f32")])
+def test_repeat_span_bit_identical(cfg, prec):
+    """Spans of many steps per launch, repeated from the same state, give the
+    same bits in every world: the partitioned kernels (and the MJCF f64 ones,
+    which spill registers to scratch) hold no state across steps or launches
+    beyond what the span carries."""
+    w = W.config(cfg)
+    n = 2048
+    q, v, c, tg = w.initial_state(n)
+    sim = from_workload(w, prec, nworld=n)
+    print(f"cfg {cfg} {prec}: kernel {sim.kernel_info()}", flush=True)
+    outs = []
+    for _ in range(4):
+        sim.load_states(q, v, c)
+        if tg is not None:
+            sim.set_position_targets(tg)
+        sim.step_many(200)
+        qg, vg = sim.readback_states()
+        bits = np.uint64 if qg.dtype == np.float64 else np.uint32
+        outs.append((qg.view(bits).copy(), vg.view(bits).copy()))
+    for k, (qg, vg) in enumerate(outs[1:], start=1):
+        bad = ~(np.all(qg == outs[0][0], axis=1) & np.all(vg == outs[0][1], axis=1))
+        assert not bad.any(), f"cfg {cfg} {prec}: repeat {k} differs in {bad.sum()} worlds"
