@@ -968,8 +968,18 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
     const T tu = slot[3 * cp + 1] - dot(vpt, gp.tu[k]) * gp.cu[k];
     const T tw = slot[3 * cp + 2] - dot(vpt, gtw) * gp.cw[k];
     const T limit = T(M::mu) * fn;
-    const T tn = dsqrt(tu * tu + tw * tw);
-    const T sc = tn > limit ? (tn > T(0) ? limit / dmax(tn, T(1e-30)) : T(0)) : T(1);
+    T sc;
+    if constexpr (sizeof(T) == 4) {
+      // Slip when |t| > limit, compared as squares; the scale limit / |t|
+      // from the hardware reciprocal square root (about 1 ulp): no rooted
+      // or divided expansion in the sweep loop, which runs every contact
+      // point NS times a step. limit >= 0, so slipping implies |t| > 0.
+      const T t2 = tu * tu + tw * tw;
+      sc = t2 > limit * limit ? limit * __builtin_amdgcn_rsqf(dmax(t2, T(1e-36))) : T(1);
+    } else {
+      const T tn = dsqrt(tu * tu + tw * tw);
+      sc = tn > limit ? (tn > T(0) ? limit / dmax(tn, T(1e-30)) : T(0)) : T(1);
+    }
     const bool in = gp.in[k];
     slot[3 * cp] = in ? fn : T(0);
     slot[3 * cp + 1] = in ? tu * sc : T(0);
