@@ -264,6 +264,9 @@ __device__ __forceinline__ double fdiv(double a, double b) { return a / b; }
 // 1 ulp, no correction sequence), f64 the correctly rounded one.
 __device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
 __device__ __forceinline__ double fsqrt(double x) { return sqrt(x); }
+// 1 / sqrt(x): f32 the hardware v_rsq_f32 (about 1 ulp), f64 correctly rounded steps.
+__device__ __forceinline__ float frsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ double frsqrt(double x) { return 1.0 / sqrt(x); }
 // The friction-loss argument qd / 1e-3: f32 multiplies by 1e3 (within an ulp
 // of the quotient), f64 divides as the oracle does.
 __device__ __forceinline__ float per_milli(float x) { return x * 1e3f; }
@@ -504,7 +507,7 @@ template <class T> __device__ __forceinline__ Q<T> qmul(const Q<T>& a, const Q<T
           a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x, a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
 }
 template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
-  T ang = dsqrt(dot(w, w));
+  T ang = fsqrt(dot(w, w));
   T s, c;
   dsincos(ang * T(0.5), &s, &c);
   const bool small = ang < T(Eps<T>::v);
@@ -516,7 +519,7 @@ template <class T> __device__ __forceinline__ Q<T> quat_exp(V3<T> w) {
 // that the integration passes are unit to rounding.
 template <class T> __device__ __forceinline__ V3<T> quat_log(const Q<T>& q) {
   V3<T> v = v3(q.x, q.y, q.z);
-  T n = dsqrt(dot(v, v));
+  T n = fsqrt(dot(v, v));
   const bool small = n < T(Eps<T>::v);
   T f = small ? T(2) : fdiv(T(2) * datan2(n, q.w), dmax(n, T(0.5) * T(Eps<T>::v)));
   return v * f;
@@ -666,7 +669,7 @@ template <class M, class T> __device__ __forceinline__ T terrain_at(const Terrai
     if (tr.ny >= 2 && py >= tr.oy && py <= tr.oy + T(tr.ny - 1) * tr.cell)
       dhdy = ((h01 - h00) * (T(1) - tx) + (h11 - h10) * tx) / tr.cell;
     const V3<T> g = v3(-dhdx, -dhdy, T(1));
-    n = g * (T(1) / dsqrt(dot(g, g)));
+    n = g * frsqrt(dot(g, g));  // |g| >= 1
     return h;
   }
 }
@@ -765,8 +768,8 @@ template <class T> __device__ __forceinline__ void tangent_frame(V3<T> n, V3<T>&
   const bool ax = dabs(n.x) > T(0.9);
   const V3<T> a = v3(ax ? T(0) : T(1), ax ? T(1) : T(0), T(0));
   const V3<T> c = cross(n, a);
-  const T l = dsqrt(dot(c, c));
-  u = sel(l > T(0), c * (T(1) / dmax(l, T(1e-30))), c);
+  const T l2 = dot(c, c);
+  u = sel(l2 > T(0), c * frsqrt(dmax(l2, T(1e-36))), c);
   w = cross(n, u);
 }
 
