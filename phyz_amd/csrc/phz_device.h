@@ -975,8 +975,8 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
     if constexpr (sizeof(T) == 4) {
       // Slip when |t| > limit, compared as squares; the scale limit / |t|
       // from the hardware reciprocal square root (about 1 ulp): no rooted
-      // or divided expansion in the sweep loop, which runs every contact
-      // point NS times a step. limit >= 0, so slipping implies |t| > 0.
+      // or divided expansion in the sweep loop, which runs for every contact
+      // point SWEEPS times a step. limit >= 0, so slipping implies |t| > 0.
       const T t2 = tu * tu + tw * tw;
       sc = t2 > limit * limit ? limit * __builtin_amdgcn_rsqf(dmax(t2, T(1e-36))) : T(1);
     } else {
