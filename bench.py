@@ -42,6 +42,12 @@ hand driven by their own actuators, f32, at a 1 ms step (the reference's
 explicit joint-limit law runs light links away at the files' own steps).
 `value` counts the worlds still finite at the end of the timed span (every
 world, at 1 ms), and `all_worlds_value` every world.
+world_sweep (unless --no-sweep; --sweep-only runs just this): chain7 in f32
+and f64 at 1024 to 262144 worlds, 100-step spans: kernel and wall
+world-steps/s, and with each span's load and readback.
+io (every configuration): load_states, readback_states and its
+allocation-free variant timed apart from the resident spans, and the
+reference's repetition (load, span, readback) with the readback's share.
 control_loop (unless --no-control): the ant driven by the on-device policy.
 ppo_update (unless --no-ppo; --ppo-only runs just this): the PPO update pass at
 the reference's timing shape (a million samples, actor 55-64-64-22, critic
@@ -143,10 +149,46 @@ def run_gpu(w, prec, steps, warmup, reps, settle_ms=0.0):
     # each timed by the events its own launches stamp.
     reload()
     ev = list(sim.time_step_many(steps, reps))
+    io = time_io(sim, reload, steps)
     reload()
     sim.step_many(steps)
     info = sim.kernel_info()
-    return sim, np.array(walls), np.array(ev), info, done, settle
+    return sim, np.array(walls), np.array(ev), info, done, settle, io
+
+
+def _median_ms(fn, reps):
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+    return round(float(np.median(t)) * 1e3, 4)
+
+
+def time_io(sim, reload, steps, reps=5):
+    """Upload and readback, timed apart from the resident spans (the
+    reference's batch bench, crates/phyz-bench/src/suites/gpu_batch.rs:231-246):
+    load_states (world-major f64 rows to the device's SoA layout, with the PD
+    targets where the workload has them), readback_states and its
+    allocation-free variant, and the reference's own repetition, load + span +
+    readback, with the readback's share of it."""
+    out = {"load_states_ms": _median_ms(reload, reps)}
+    sim.step_many(steps)
+    sim.synchronize()
+    out["readback_states_ms"] = _median_ms(sim.readback_states, reps)
+    width = max(sim.model.nq, sim.model.nv)
+    if sim.nworld * width * 8 <= 32 << 20:
+        out["readback_states_noalloc_ms"] = _median_ms(sim.readback_states_noalloc, reps)
+
+    def rep():
+        reload()
+        sim.step_many(steps)
+        sim.readback_states()
+
+    out["load_span_readback_ms"] = _median_ms(rep, reps)
+    out["readback_share"] = round(out["readback_states_ms"] / out["load_span_readback_ms"], 4)
+    out["steps"] = steps
+    return out
 
 
 def launches_per_span(steps, info):
@@ -269,7 +311,7 @@ def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=8.0, settle_ms
     results = {}
     for prec in precs:
         log(f"[bench] {w.name} {prec}: {w.nworld} worlds, warmup {warmup}, timed {steps} steps x {reps}")
-        sim, walls, ev, info, warm_done, settle = run_gpu(w, prec, steps, warmup, reps, settle_ms)
+        sim, walls, ev, info, warm_done, settle, io = run_gpu(w, prec, steps, warmup, reps, settle_ms)
         wall = float(np.median(walls))
         med = float(np.median(ev))
         spread = (max(ev) - min(ev)) / med if med > 0 else 0.0
@@ -288,6 +330,7 @@ def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=8.0, settle_ms
             "roofline": roofline(w, prec, steps, ev, info, flops_tab, traffic_tab),
             "kernel": info,
             "warmup_steps_run": warm_done,
+            "io": io,
         }
         if settle["spans"]:
             r["clock_settle"] = settle
@@ -304,6 +347,71 @@ def measure(w, precs, steps, warmup, reps, with_cpu, cpu_budget_s=8.0, settle_ms
         log(f"[bench] {w.name}: cpu_baseline")
         cpu = cpu_baseline(w, cpu_budget_s)
     return {"results": results, "cpu": cpu}
+
+
+SWEEP_WORLDS = (1024, 2048, 4096, 8192, 16384, 32768, 65536, 131072, 262144)
+
+
+def run_world_sweep(idx=2, sizes=SWEEP_WORLDS, precs=("f32", "f64"), steps=100, reps=5):
+    """Throughput against the number of worlds (the reference sweeps batch
+    sizes the same way, BENCHMARKS.md:318-338): the workload's kernel at each
+    size, spans of `steps` steps from its seeded states; kernel time from the
+    launches' own hipEvents, wall time with the device synchronized on both
+    sides, and the reference's repetition (load, span, readback). 8192 worlds
+    is one GPU's share of the 65536-world chain over eight GPUs."""
+    from phyz_amd import workloads as W
+    from phyz_amd.sim import from_workload
+    w = W.config(idx)
+    flops = json.load(open(FLOPS_JSON))[w.name]["flops_per_world_step"]
+    out = []
+    for prec in precs:
+        for n in sizes:
+            sim = from_workload(w, prec, nworld=n, device=0)
+            q, v, c, tg = w.initial_state(n)
+
+            def reload():
+                sim.load_states(q, v, c)
+                if tg is not None:
+                    sim.set_position_targets(tg)
+
+            reload()
+            sim.compile()
+            for _ in range(3):
+                sim.step_many(steps)
+            sim.synchronize()
+            ev = float(np.median(sim.time_step_many(steps, reps)))
+            reload()
+            wall = []
+            for _ in range(reps):
+                sim.synchronize()
+                t0 = time.perf_counter()
+                sim.step_many(steps)
+                sim.synchronize()
+                wall.append(time.perf_counter() - t0)
+            wall_ms = float(np.median(wall)) * 1e3
+
+            def rep():
+                reload()
+                sim.step_many(steps)
+                sim.readback_states()
+
+            rep_ms = _median_ms(rep, 3)
+            info = sim.kernel_info()
+            out.append({"workload": w.name, "dtype": prec, "nworld": n, "steps": steps,
+                        "lanes_per_world": info["lanes_per_world"], "block": info["block"],
+                        "event_ms_per_span": round(ev, 4), "wall_ms_per_span": round(wall_ms, 4),
+                        "world_steps_per_s_event": round(n * steps / (ev / 1e3), 1),
+                        "world_steps_per_s_wall": round(n * steps / (wall_ms / 1e3), 1),
+                        "tflops_event": round(flops * n * steps / (ev / 1e3) / 1e12, 3),
+                        "frac_of_peak_event": round(flops * n * steps / (ev / 1e3) / 1e12 / PEAK_TFLOPS[prec], 4),
+                        "load_span_readback_ms": rep_ms,
+                        "world_steps_per_s_with_io": round(n * steps / (rep_ms / 1e3), 1)})
+            sim.close()
+            r = out[-1]
+            log(f"[bench] sweep {w.name} {prec} {n:>6} worlds: {r['world_steps_per_s_event']:.3g} world-steps/s "
+                f"(kernel), {r['world_steps_per_s_wall']:.3g} (wall), {100 * r['frac_of_peak_event']:.1f}% of peak; "
+                f"with load + readback {r['world_steps_per_s_with_io']:.3g}")
+    return out
 
 
 def run_control_loop(prec: str, reps: int, with_cpu: bool):
@@ -537,6 +645,7 @@ def ppo_cpu_baseline(batch, a0, c0, ad, cd, cfg, n_mb: int = 128):
 
 
 def config_of(w, r):
+    from phyz_amd import workloads as W
     c = {"workload": w.name, "config_index": w.index, "nworld": w.nworld, "bodies": w.model.nbodies,
          "nv": w.model.nv, "dt": w.model.dt, "steps_per_launch": r["roofline"]["steps_per_launch"]}
     if w.heightfield is not None:
@@ -546,6 +655,18 @@ def config_of(w, r):
         c["contact"] = {"mode": "impulse", "sweeps": w.impulse_sweeps}
     if w.model.actuators:
         c["actuators"] = w.model.nu()
+    # Joint regularisation the configuration's text does not name (the
+    # builder humanoid's hinges carry rotor armature and viscous damping).
+    terms = {}
+    for key in ("armature", "damping", "stiffness"):
+        vals = sorted({round(float(getattr(b.joint, key)), 12) for b in w.model.bodies if b.joint.ndof() == 1})
+        if any(x != 0.0 for x in vals):
+            terms[f"hinge_{key}"] = vals[0] if len(vals) == 1 else {"min": vals[0], "max": vals[-1]}
+    if terms:
+        c["joint_terms"] = terms
+    if w.index in W.MJCF_WORKLOADS:
+        c["file_dt"] = float(W.mjcf_model(W.MJCF_WORKLOADS[w.index][0]).dt)
+        c["dt_note"] = "every MJCF workload steps at 1 ms; file_dt is the model file's own timestep"
     return c
 
 
@@ -572,6 +693,8 @@ def main():
     ap.add_argument("--only", action="store_true", help="measure the headline workload only (profiling runs)")
     ap.add_argument("--control-only", action="store_true", help="measure only the control loop")
     ap.add_argument("--no-ppo", action="store_true", help="skip the PPO update pass measurement")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the chain7 world-count sweep")
+    ap.add_argument("--sweep-only", action="store_true", help="measure only the chain7 world-count sweep")
     ap.add_argument("--ppo-only", action="store_true", help="measure only the PPO update pass")
     ap.add_argument("--precision", choices=["f32", "f64"], default=None,
                     help="headline precision (default: f32 where the workload runs it)")
@@ -598,6 +721,9 @@ def main():
         return
     if args.ppo_only:
         print(json.dumps(run_ppo_update(args.reps, not args.no_cpu)), flush=True)
+        return
+    if args.sweep_only:
+        print(json.dumps({"world_sweep": run_world_sweep()}), flush=True)
         return
 
     from phyz_amd import workloads as W
@@ -654,7 +780,7 @@ def main():
             entry = {"config": config_of(wc, next(iter(rc["results"].values()))), "cpu_baseline": rc["cpu"]}
             for pr, res in rc["results"].items():
                 entry[pr] = {k: res[k] for k in ("value", "unit", "ms_per_step", "world_steps_per_s_event_median",
-                                                 "event_ms_per_span", "finite_worlds", "roofline", "kernel")}
+                                                 "event_ms_per_span", "finite_worlds", "roofline", "kernel", "io")}
                 if with_cpu:
                     entry[pr]["parity"] = res["parity"]
                     entry[pr]["gpu_over_cpu"] = round(res["value"] / rc["cpu"]["value"], 1)
@@ -684,6 +810,8 @@ def main():
                                      "roofline": pm["roofline"], "cpu_baseline": rm["cpu"],
                                      "event_ms_per_span": pm["event_ms_per_span"], "kernel": pm["kernel"],
                                      "parity": pm.get("parity")}
+    if not args.no_sweep:
+        line["world_sweep"] = run_world_sweep()
     if not args.no_control:
         line["control_loop"] = run_control_loop("f32", min(args.reps, 5), with_cpu)
     if not args.no_ppo:

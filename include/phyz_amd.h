@@ -149,12 +149,13 @@ int phz_synchronize(phz_sim* sim);
 /* BatchSim::readback_states (mod.rs:978-983): q [nworld][nq], v [nworld][nv]. */
 int phz_readback_states(phz_sim* sim, double* q, double* v);
 /* No counterpart in the reference. For callers that cannot allocate device
- * memory (code under graph capture, tight serving loops, harnesses that forbid
- * hipMalloc): phz_readback_states staged through the library's static 32 MiB
- * per-GPU scratch array instead of the sim's lazily allocated staging buffer,
- * so no call allocates. Rejects nworld * max(nq, nv) * 8 bytes above 32 MiB.
- * Synchronizes the sim's stream. All calls on one GPU share its array: calls
- * that overlap on one GPU (two threads, two sims) race. */
+ * memory (tight serving loops, harnesses that forbid hipMalloc):
+ * phz_readback_states staged through the library's static 32 MiB per-GPU
+ * scratch array instead of the sim's lazily allocated staging buffer, so no
+ * call allocates. Rejects nworld * max(nq, nv) * 8 bytes above 32 MiB.
+ * Synchronizes the sim's stream, so it returns an error while that stream is
+ * capturing a graph. All calls on one GPU share its array and take turns on a
+ * per-device host mutex (two threads or two sims on one GPU are serialized). */
 int phz_readback_states_noalloc(phz_sim* sim, double* q, double* v);
 /* BatchSim::readback_contacts (mod.rs:988-997): [nworld][nb][8] = touching,
  * penetration, point (x, y, z), force (x, y, z); errors before contact is enabled. */

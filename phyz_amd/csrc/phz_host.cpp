@@ -47,8 +47,9 @@ hipError_t phz_io_unpack(const void* src, double* dst, int nworld, int width, in
 hipError_t phz_io_zero(void* dst, size_t bytes, hipStream_t s);
 hipError_t phz_io_seed(uint64_t* rng, uint64_t seed, int nworld, hipStream_t s);
 hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
-hipError_t phz_io_scratch(void** ptr, size_t* bytes);
+hipError_t phz_io_scratch(void** ptr, size_t* bytes, int* device);
 }
+std::mutex& phz_io_scratch_mutex(int device);
 
 namespace {
 
@@ -1336,15 +1337,26 @@ struct phz_sim {
     }
     return true;
   }
-  bool step_many(uint32_t n) {
-    if (!has_device()) { err = "host-only sim (device_ordinal -1) cannot step"; return false; }
+  // What every step span needs before a launch: a device, a sweep count in
+  // impulse mode and the loaded kernel. `launch` is false (and the call a
+  // successful no-op) for zero steps or zero worlds.
+  bool span_ready(uint32_t n, bool& launch) {
+    launch = false;
     if (feat.contact && feat.cmode == 1 && feat.sweeps < 1) {
       err = "impulse contact needs at least one contact sweep per step";
       return false;
     }
-    if (n == 0) return true;
-    if (nworld == 0) return true;
+    if (n == 0 || nworld == 0) return true;
+    if (!has_device()) { err = "host-only sim (device_ordinal -1) cannot step"; return false; }
     if (!load_kernel()) return false;
+    launch = true;
+    return true;
+  }
+
+  bool step_many(uint32_t n) {
+    bool launch = false;
+    if (!span_ready(n, launch)) return false;
+    if (!launch) return true;
     // A span of one launch goes straight to the stream: replaying a one-node
     // graph costs about 5 us more per span on MI355X (86.5 against 81.8 us
     // wall for 20 chain steps at 65536 worlds).
@@ -2055,9 +2067,19 @@ int phz_readback_states_noalloc(phz_sim* s, double* q, double* v) {
   if (!s) return 1;
   if (!s->has_device()) return s->fail("host-only sim has no device buffers");
   if (!set_device(s)) return 1;
+  // Every step here (a kernel launch, a pageable device-to-host copy, a
+  // stream synchronize) is illegal inside stream capture: refuse it plainly.
+  hipStreamCaptureStatus cap_state = hipStreamCaptureStatusNone;
+  if (!s->hip_ok(hipStreamIsCapturing(s->stream, &cap_state), "readback_states_noalloc: capture query")) return 1;
+  if (cap_state != hipStreamCaptureStatusNone)
+    return s->fail("readback_states_noalloc: the sim's stream is capturing a graph; a readback synchronizes and "
+                   "cannot be captured");
   void* scr = nullptr;
   size_t cap = 0;
-  if (!s->hip_ok(phz_io_scratch(&scr, &cap), "readback_states_noalloc: scratch lookup")) return 1;
+  int dev = -1;
+  if (!s->hip_ok(phz_io_scratch(&scr, &cap, &dev), "readback_states_noalloc: scratch lookup")) return 1;
+  // One caller at a time per GPU, from staging to the end of the copy out.
+  std::lock_guard<std::mutex> use(phz_io_scratch_mutex(dev));
   const int width = std::max(s->model.nq, s->model.nv);
   const size_t need = (size_t)s->nworld * (size_t)width * sizeof(double);
   if (need > cap)
@@ -2126,17 +2148,18 @@ int phz_compile(phz_sim* s) {
 
 int phz_time_step_many(phz_sim* s, uint32_t n, uint32_t reps, double* ms_per_rep) {
   if (!s || !ms_per_rep) return 1;
-  if (!s->has_device()) return s->fail("host-only sim cannot step");
+  if (n == 0) return s->fail("time_step_many needs at least one step");
+  if (s->nworld == 0) return s->fail("time_step_many needs at least one world");
   if (!set_device(s)) return 1;
-  if (!s->load_kernel()) return 1;
+  bool launch = false;
+  if (!s->span_ready(n, launch)) return 1;  // sweeps, device, kernel
   std::vector<hipEvent_t> ev(2 * (size_t)reps);
   for (auto& e : ev)
     if (!s->hip_ok(hipEventCreate(&e), "hipEventCreate")) return 1;
   // Each span's launches go straight to the stream, the first stamping the
   // start event with its own start and the last the stop event with its own
   // end: the time from the first kernel's start to the last one's end.
-  bool ok = n > 0;
-  if (!ok) s->err = "time_step_many needs at least one step";
+  bool ok = true;
   for (uint32_t r = 0; r < reps && ok; r++) ok = s->issue(n, ev[2 * r], ev[2 * r + 1]);
   ok = ok && s->hip_ok(hipStreamSynchronize(s->stream), "timing sync");
   for (uint32_t r = 0; r < reps && ok; r++) {

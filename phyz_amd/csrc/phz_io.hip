@@ -58,13 +58,19 @@ constexpr size_t kScratchBytes = size_t(32) << 20;
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_use[kMaxDevices];
 
 }  // namespace
 
+// Held by a caller across its whole use of device `dev`'s scratch array
+// (stage, copy out, synchronize), so calls from several threads or sims on
+// one GPU take turns instead of overwriting each other's rows.
+std::mutex& phz_io_scratch_mutex(int dev) { return g_scratch_use[dev]; }
+
 // Staging rows for callers that cannot allocate device memory
 // (phz_readback_states_noalloc): 32 MiB per GPU, held until the process ends.
-// Every call on a GPU shares that GPU's copy, so calls that overlap on one GPU
-// race. In host code `scratch` names a host-side stand-in, never the device
+// Every call on a GPU shares that GPU's copy; callers serialize their use of
+// it with phz_io_scratch_mutex. In host code `scratch` names a host-side stand-in, never the device
 // memory: use the address phz_io_scratch returns.
 static __device__ __align__(256) double scratch[kScratchBytes / sizeof(double)];
 
@@ -99,9 +105,10 @@ hipError_t phz_io_copy(void* dst, const void* src, size_t bytes, hipStream_t s) 
   return hipGetLastError();
 }
 
-// The device address of the current device's scratch array and its size,
-// looked up once per device (with that device current) and kept.
-hipError_t phz_io_scratch(void** ptr, size_t* bytes) {
+// The device address of the current device's scratch array, its size and the
+// device's ordinal, looked up once per device (with that device current) and
+// kept.
+hipError_t phz_io_scratch(void** ptr, size_t* bytes, int* device) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -116,6 +123,7 @@ hipError_t phz_io_scratch(void** ptr, size_t* bytes) {
   }
   *ptr = g_scratch_ptr[dev];
   *bytes = kScratchBytes;
+  *device = dev;
   return hipSuccess;
 }
 

@@ -1,12 +1,13 @@
-"""Write tests/golden/mjcf_models.npz: the reference's benchmark MJCF models
+"""Write phyz_amd/data/mjcf_models.npz: the reference's benchmark MJCF models
 (models/ant.xml, humanoid.xml, shadow_hand.xml, half_cheetah.xml,
 simple_arm.xml under the reference tree) as loaded by phyz_amd.mjcf, in the
 packed tables the C ABI takes. The model files themselves stay in the
-reference; this is the data they describe, so workloads and GPU tests can use
-the models where the reference tree is absent. tests/test_mjcf.py checks that
-the loader still produces exactly these tables.
+reference; this is the data they describe, package data that the benchmark
+workloads (phyz_amd.workloads.mjcf_model) and the GPU tests load where the
+reference tree is absent. tests/test_mjcf.py checks that the loader still
+produces exactly these tables.
 
-    python tests/golden/make_mjcf_models.py [reference root]
+    python phyz_amd/data/make_mjcf_models.py [reference root]
 """
 from __future__ import annotations
 

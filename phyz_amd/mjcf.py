@@ -25,15 +25,24 @@ euler / xyaxes / zaxis orientations (that precedence); ``fromto``; geom-
 derived inertia (density or mass) or an explicit inertial; hinge, slide, ball
 and free joints with limits, damping, armature, stiffness, springref and
 frictionloss; motor, position, velocity and general actuators on joints;
-sensors (recorded, not simulated). Reported by unsupported() and skipped:
-``<include>``, mesh assets and mesh geoms, heightfield assets, tendons,
-equality constraints, unknown joint types and actuators without a joint.
+sensors (recorded, not simulated); ``<include file>`` (spliced into the tree
+before anything is read, paths relative to the including file, nesting capped
+at 16 levels, which also stops cycles: include.rs); ``<asset><mesh>`` from
+binary or ASCII STL and OBJ files, resolved through ``<compiler meshdir>`` (or
+``assetdir``) against the model's directory, scaled per axis (assets.rs;
+meshes()). A mesh geom whose asset loaded collides through its body-frame
+bounding box, as the device's geometry table carries meshes (layout.rs:241-
+257), and adds no mass, as in the reference. Reported by unsupported() and
+skipped: meshes that do not load (and geoms that use them), heightfield
+assets, tendons, equality constraints, unknown joint types and actuators
+without a joint.
 """
 from __future__ import annotations
 
 import dataclasses
 import math
 import os
+import struct
 import xml.etree.ElementTree as ET
 from typing import Dict, Iterator, List, Optional, Tuple
 
@@ -43,6 +52,7 @@ from .model import (BALL, FIXED, FREE, PRISMATIC, REVOLUTE, Actuator, Geometry, 
                     SpatialInertia, SpatialTransform, G_NONE)
 
 PLACEHOLDER_MASS = 1e-9  # mass and inertia of the leading links of a multi-joint body
+MAX_INCLUDE_DEPTH = 16
 
 
 class MjcfError(ValueError):
@@ -87,6 +97,7 @@ _SCHEMA: Dict[str, Dict[str, str]] = {
              "mass": "num", "contype": "num", "conaffinity": "num", "mesh": "str", **_ORIENT},
     "actuator": {"name": "str", "joint": "str", "gear": "nums", "ctrlrange": "pair", "forcerange": "pair",
                  "kp": "num", "kv": "num", "gainprm": "nums", "biasprm": "nums"},
+    "mesh": {"name": "str", "file": "str", "scale": "v3"},
 }
 _SCHEMA["freejoint"] = _SCHEMA["joint"]
 _CONVERT = {
@@ -307,6 +318,129 @@ class _MassSum:
         return SpatialInertia.new(m, com, inertia)
 
 
+# ── includes (include.rs) ───────────────────────────────────────────────────
+def _splice_includes(root: ET.Element, base_dir: Optional[str], depth: int = 0) -> ET.Element:
+    """Replace every ``<include file>`` under `root` by the children of the
+    named document's root element, in place and in order; the included
+    document's own includes resolve against its directory."""
+    for parent in list(root.iter()):
+        kids = list(parent)
+        if not any(isinstance(k.tag, str) and k.tag == "include" for k in kids):
+            continue
+        spliced: List[ET.Element] = []
+        for k in kids:
+            if not (isinstance(k.tag, str) and k.tag == "include"):
+                spliced.append(k)
+                continue
+            name = k.get("file")
+            if name is None:
+                raise MjcfError("Invalid MJCF: <include> is missing required attribute 'file'")
+            if depth + 1 >= MAX_INCLUDE_DEPTH:
+                raise MjcfError(f"Invalid MJCF: <include> nesting exceeded {MAX_INCLUDE_DEPTH} levels at "
+                                f"'{name}'; the includes are probably cyclic")
+            path = name if base_dir is None else os.path.join(base_dir, name)
+            try:
+                with open(path) as f:
+                    text = f.read()
+            except OSError as e:
+                raise MjcfError(f'Invalid MJCF: <include file="{name}"> could not be read: {e}') from None
+            try:
+                sub = ET.fromstring(text)
+            except ET.ParseError as e:
+                raise MjcfError(f'Invalid MJCF: <include file="{name}">: XML parse error: {e}') from None
+            _splice_includes(sub, os.path.dirname(os.path.abspath(path)), depth + 1)
+            spliced.extend(sub)
+        parent[:] = spliced
+    return root
+
+
+# ── mesh assets (assets.rs) ─────────────────────────────────────────────────
+@dataclasses.dataclass
+class MeshAsset:
+    """A ``<mesh>`` asset: `vertices` [n][3] (scaled) and `faces` [m][3], or
+    None with the reason in `load_error`."""
+    name: str
+    file: Optional[str]
+    resolved_path: Optional[str]
+    scale: np.ndarray
+    vertices: Optional[np.ndarray] = None
+    faces: Optional[np.ndarray] = None
+    load_error: Optional[str] = None
+
+
+def _stl(data: bytes) -> Tuple[np.ndarray, np.ndarray]:
+    """Binary STL when the size matches the header's facet count (80-byte
+    header, u32 count, 50 bytes a facet), else ASCII when it starts 'solid'."""
+    if len(data) >= 84:
+        n = struct.unpack_from("<I", data, 80)[0]
+        if 84 + 50 * n == len(data):
+            rec = np.frombuffer(data, dtype=np.dtype([("normal", "<f4", 3), ("v", "<f4", (3, 3)), ("attr", "<u2")]),
+                                count=n, offset=84)
+            verts = rec["v"].reshape(-1, 3).astype(np.float64)
+            return verts, np.arange(3 * n).reshape(n, 3)
+    if not data.startswith(b"solid"):
+        raise ValueError("file is neither a valid binary nor ASCII STL")
+    verts, faces, facet = [], [], []
+    for lineno, line in enumerate(data.decode("utf-8").splitlines(), start=1):
+        words = line.split()
+        if words[:1] == ["vertex"]:
+            if len(words) != 4:
+                raise ValueError(f"line {lineno}: vertex needs 3 numbers")
+            facet.append(len(verts))
+            verts.append([float(x) for x in words[1:]])
+        elif words[:1] == ["endfacet"]:
+            if len(facet) == 3:
+                faces.append(facet)
+            facet = []
+    if not faces:
+        raise ValueError("no facets found")
+    return np.array(verts), np.array(faces)
+
+
+def _obj(text: str) -> Tuple[np.ndarray, np.ndarray]:
+    """OBJ 'v' and 'f' records; polygons fan into triangles; face indices
+    1-based, negative ones counted back from the last vertex."""
+    verts, faces = [], []
+    for lineno, line in enumerate(text.splitlines(), start=1):
+        words = line.split()
+        if not words:
+            continue
+        if words[0] == "v":
+            xyz = [float(x) for x in words[1:4]]
+            if len(xyz) != 3:
+                raise ValueError(f"line {lineno}: vertex needs 3 numbers")
+            verts.append(xyz)
+        elif words[0] == "f":
+            idx = []
+            for tok in words[1:]:
+                k = int(tok.split("/")[0])
+                if k == 0:
+                    raise ValueError(f"line {lineno}: face index 0 is invalid")
+                j = k - 1 if k > 0 else len(verts) + k
+                if not 0 <= j < len(verts):
+                    raise ValueError(f"line {lineno}: face index {k} out of range of {len(verts)} vertices")
+                idx.append(j)
+            faces.extend([idx[0], idx[t], idx[t + 1]] for t in range(1, len(idx) - 1))
+    if not faces:
+        raise ValueError("no faces found")
+    return np.array(verts, dtype=np.float64), np.array(faces)
+
+
+def load_mesh_file(path: str) -> Tuple[np.ndarray, np.ndarray]:
+    """(vertices, faces) of an STL or OBJ file, by extension."""
+    ext = os.path.splitext(path)[1][1:].lower()
+    try:
+        if ext == "stl":
+            with open(path, "rb") as f:
+                return _stl(f.read())
+        if ext == "obj":
+            with open(path) as f:
+                return _obj(f.read())
+    except (OSError, ValueError, UnicodeDecodeError) as e:
+        raise ValueError(f"{path}: {e}") from None
+    raise ValueError(f"unsupported mesh format '{ext}' for {path} (STL and OBJ are supported)")
+
+
 # ── records ─────────────────────────────────────────────────────────────────
 @dataclasses.dataclass
 class UnsupportedFeature:
@@ -343,6 +477,7 @@ class _GeomRec:
     rot: np.ndarray  # geom frame -> body frame
     mass: float
     collides: bool
+    mesh: Optional["MeshAsset"] = None  # a mesh geom's loaded asset
 
 
 @dataclasses.dataclass
@@ -390,8 +525,11 @@ def _actuator_law(tag: str, a: Dict[str, object]) -> Tuple[float, float, float]:
 
 # ── the document walk ───────────────────────────────────────────────────────
 class _Reader:
-    def __init__(self, doc: ET.Element):
+    def __init__(self, doc: ET.Element, model_dir: Optional[str] = None):
         self.defaults = _DefaultTables(doc)
+        self.model_dir = model_dir
+        self.mesh_dir: Optional[str] = None
+        self.meshes: List[MeshAsset] = []
         self.degrees = False
         self.eulerseq = "xyz"
         self.gravity = np.array([0.0, 0.0, -9.81])
@@ -427,6 +565,10 @@ class _Reader:
     def _compiler(self, el: ET.Element):
         if el.get("angle") is not None:
             self.degrees = el.get("angle") == "degree"
+        # meshdir wins over the general assetdir, whatever their order.
+        for key in ("assetdir", "meshdir"):
+            if el.get(key) is not None and (key == "meshdir" or el.get("meshdir") is None):
+                self.mesh_dir = el.get(key)
         seq = el.get("eulerseq")
         if seq is not None:
             if len(seq) != 3 or any(c not in "xyzXYZ" for c in seq):
@@ -450,18 +592,43 @@ class _Reader:
             elif c.tag == "asset":
                 for a in self._children(c):
                     if a.tag == "mesh":
-                        self.note("mesh", "mesh assets are not loaded; geoms that use them are dropped")
+                        self._mesh(a)
                     elif a.tag == "hfield":
                         self.note("hfield", "heightfield assets are not loaded; the ground is the contact "
                                             "pass's own plane or heightfield")
-            elif c.tag == "include":
-                self.note("include", f"<include file={c.get('file')!r}> is not read; its elements are missing")
             elif c.tag == "tendon":
                 self.note("tendon", "tendons are ignored; coupled joints move independently")
             elif c.tag == "equality":
                 self.note("equality", "equality constraints are ignored; closed loops act as open chains")
             elif c.tag not in ("default", "compiler", "option"):
                 self._top(c)
+
+    def _asset_dir(self) -> Optional[str]:
+        if self.model_dir is not None and self.mesh_dir is not None:
+            return os.path.join(self.model_dir, self.mesh_dir)
+        return self.model_dir if self.model_dir is not None else self.mesh_dir
+
+    def _mesh(self, el: ET.Element):
+        a = self._attrs(el, None)
+        file = a.get("file")
+        name = a.get("name") or (os.path.splitext(os.path.basename(file))[0] if file else None)
+        if name is None:
+            raise MjcfError("Invalid MJCF: <mesh> is missing required attribute 'name'")
+        scale = a.get("scale") if a.get("scale") is not None else np.ones(3)
+        d = self._asset_dir()
+        path = None if file is None else (file if d is None else os.path.join(d, file))
+        m = MeshAsset(name, file, path, np.asarray(scale, dtype=np.float64))
+        if path is None:
+            m.load_error = "mesh has no 'file' attribute"
+        else:
+            try:
+                v, f = load_mesh_file(path)
+                m.vertices, m.faces = v * m.scale, f
+            except ValueError as e:
+                m.load_error = str(e)
+        if m.load_error is not None:
+            self.note("mesh", f"mesh '{name}' not loaded: {m.load_error}")
+        self.meshes.append(m)
 
     def _class_of(self, el: ET.Element, body: Optional[int]) -> Optional[str]:
         """An explicit class, else the nearest enclosing body's childclass."""
@@ -534,9 +701,15 @@ class _Reader:
     def _geom(self, el: ET.Element, body: int) -> Optional[_GeomRec]:
         a = self._attrs(el, body)
         kind = a.get("type") or "sphere"
+        mesh = None
         if kind == "mesh" or a.get("mesh") is not None:
-            self.note("geom", "mesh geoms are dropped: the body loses that collision shape and its mass")
-            return None
+            mesh = next((m for m in self.meshes if m.name == (a.get("mesh") or "") and m.vertices is not None
+                         and len(m.vertices)), None)
+            if mesh is None:
+                self.note("geom", "mesh geoms whose asset could not be loaded are dropped; the body loses that "
+                                  "collision shape")
+                return None
+            kind = "mesh"
         size = a.get("size")
         size = [0.05] if size is None else size
         pos = a["pos"] if a.get("pos") is not None else np.zeros(3)
@@ -558,7 +731,9 @@ class _Reader:
             mass = (a.get("density") if a.get("density") is not None else 1000.0) * shape_volume(kind, size)
         else:
             mass = 0.0
-        return _GeomRec(kind, size, pos, rot, mass, not (off("contype") and off("conaffinity")))
+        if mesh is not None:
+            mass = 0.0  # a mesh's volume is not integrated: it adds no mass (the reference's rule)
+        return _GeomRec(kind, size, pos, rot, mass, not (off("contype") and off("conaffinity")), mesh)
 
     def _actuator(self, el: ET.Element):
         if el.tag not in _ACTUATOR_TAGS:
@@ -600,6 +775,8 @@ def _collision_shape(g: _GeomRec) -> Optional[Geometry]:
         return Geometry.box(s[:3] if len(s) >= 3 else (0.05, 0.05, 0.05), origin)
     if g.kind == "plane":  # may be a body's first collision geom; it never meets the ground
         return Geometry(G_NONE, (), origin)
+    if g.kind == "mesh":  # the body-frame bounding box of the mesh's vertices, as the device table holds it
+        return Geometry.mesh_aabb(g.mesh.vertices.min(axis=0), g.mesh.vertices.max(axis=0), origin)
     return None
 
 
@@ -607,17 +784,18 @@ class MjcfLoader:
     """An MJCF document, read: from_file / from_xml_str, build_model(),
     unsupported(), sensors() (the reference's MjcfLoader surface)."""
 
-    def __init__(self, xml: str):
+    def __init__(self, xml: str, model_dir: Optional[str] = None):
         try:
             doc = ET.fromstring(xml)
         except ET.ParseError as e:
             raise MjcfError(f"XML parse error: {e}") from None
-        self._r = _Reader(doc)
+        self._r = _Reader(_splice_includes(doc, model_dir), model_dir)
 
     @staticmethod
     def from_file(path: str) -> "MjcfLoader":
+        """A model file; its includes and mesh files resolve against its directory."""
         with open(path) as f:
-            return MjcfLoader(f.read())
+            return MjcfLoader(f.read(), os.path.dirname(os.path.abspath(path)))
 
     @staticmethod
     def from_xml_str(xml: str) -> "MjcfLoader":
@@ -628,6 +806,10 @@ class MjcfLoader:
 
     def sensors(self) -> List[SensorElement]:
         return list(self._r.sensors)
+
+    def meshes(self) -> List[MeshAsset]:
+        """The ``<mesh>`` assets in document order, loaded or with their error."""
+        return list(self._r.meshes)
 
     def _links(self) -> Iterator[Tuple[int, str, int, Joint, SpatialInertia]]:
         """(body record, link name, parent link, joint, inertia) per link, in

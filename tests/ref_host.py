@@ -3,8 +3,8 @@ the reference's f32 wire format — TEST INFRASTRUCTURE ONLY.
 
 oracle/Makefile builds crates/phyz-gpu/cuda/phyz_kernels.cu as host C++, the
 reference's `cuda-host` build (crates/phyz-gpu/build.rs:7-19). Its entry points
-phyz_host_{pd,contact,aba,integrate} (phyz_kernels.cu:1779-1802) walk the grid
-serially. This module packs buffers exactly as crates/phyz-gpu/src/layout.rs
+phyz_host_{pd,contact,aba,integrate} (phyz_kernels.cu:1779-1802) and
+phyz_host_{fk,obs,policy} (1809-1835) walk the grid serially. This module packs buffers exactly as crates/phyz-gpu/src/layout.rs
 and crates/phyz-gpu/src/contact_pipeline.rs:60-100 do (f32, integer slots
 bit-cast) and runs the reference step order of
 crates/phyz-gpu/src/cuda/mod.rs:879-945 (PD, contact, ABA, integrate; in
@@ -37,6 +37,10 @@ def lib():
         L.phyz_host_contact.argtypes = [u, fp, fp, fp, fp, fp, fp, fp, fp, fp]
         L.phyz_host_aba.argtypes = [u, u, u, C.c_float, u, C.c_float, C.c_float, C.c_float, fp, fp, fp, fp, fp, fp]
         L.phyz_host_integrate.argtypes = [u, u, u, C.c_float, u, fp, fp, fp, fp]
+        L.phyz_host_fk.argtypes = [u, u, u, u, fp, fp, fp, fp]
+        L.phyz_host_obs.argtypes = [u, u, u, u, u, u, u, fp, fp, fp, fp, fp, fp, fp]
+        L.phyz_host_policy.argtypes = [u, u, u, u, u, u, C.c_float, u, C.c_float, u, u, fp, fp, fp, fp, fp, fp, fp,
+                                       fp, fp, fp, fp]
         _lib = L
     return _lib
 
@@ -157,3 +161,56 @@ class RefStepper:
         L.phyz_host_integrate(n * self.nb, n, self.nv, self.dt, self.nb, P(q), P(v), P(self.qdd), P(self.bodies))
         rows = self.cstate.reshape(n, self.nb, 56)[:, :, :8].copy()
         return self.qdd.reshape(n, self.nv).copy(), self.ext.reshape(n, self.nb, 6).copy(), rows
+
+
+class RefControl:
+    """The reference's FK readout, observation and policy passes on the host
+    (phyz_host_fk / phyz_host_obs / phyz_host_policy) for `nworld` worlds: f32
+    buffers in the reference's layouts (policy_pipeline.rs:285-297 for the op
+    table, [mass, com] per body, the policy weights W1 b1 W2 b2 W3 b3)."""
+
+    def __init__(self, table64, model, spec, weights, std, n_dofs, nworld):
+        from phyz_amd.policy import pack_obs_ops
+        self.L = lib()
+        self.nb, self.nq, self.nv, self.nworld = table64.shape[0], model.nq, model.nv, nworld
+        self.bodies = np.ascontiguousarray(pack_bodies_f32(table64).reshape(-1))
+        ops, aux = pack_obs_ops(spec.obs)
+        self.ops = np.ascontiguousarray(ops.astype(np.float32).reshape(-1))
+        self.aux = np.ascontiguousarray(np.asarray(aux if len(aux) else [0.0], dtype=np.float32))
+        self.com = np.ascontiguousarray(np.array([[b.inertia.mass, *b.inertia.com] for b in model.bodies],
+                                                 dtype=np.float32).reshape(-1))
+        self.spec = spec
+        self.n_in, self.n_h, self.n_out, self.n_dofs = spec.n_in(), spec.hidden, spec.n_out(), n_dofs
+        self.weights = np.ascontiguousarray(np.asarray(weights, dtype=np.float32))
+        self.std = np.ascontiguousarray(np.asarray(std, dtype=np.float32))
+        self.in_noise = np.ascontiguousarray(np.asarray(spec.input_noise, dtype=np.float32))
+        self.slots = np.ascontiguousarray(np.asarray(spec.act_slots, dtype=np.float32))
+        cs = spec.act_clamp_slots
+        self.clamp_slots = np.ascontiguousarray(np.asarray(cs if cs is not None else [0.0], dtype=np.float32))
+
+    P = staticmethod(lambda a: a.ctypes.data_as(fp))
+
+    def fk(self, q32, v32):
+        xf = np.zeros(self.nworld * self.nb * 18, dtype=np.float32)
+        self.L.phyz_host_fk(self.nworld, self.nworld, self.nv, self.nb, self.P(self.bodies), self.P(q32),
+                            self.P(v32), self.P(xf))
+        return xf
+
+    def obs(self, q32, v32, xf):
+        o = np.zeros(self.nworld * self.n_in, dtype=np.float32)
+        self.L.phyz_host_obs(self.nworld, self.nworld, self.nq, self.nv, self.nb, self.n_in, 0, self.P(self.ops),
+                             self.P(self.aux), self.P(self.com), self.P(q32), self.P(v32), self.P(xf), self.P(o))
+        return o
+
+    def policy(self, obs, rng, z, base_targets):
+        """One policy pass in place on obs (input noise), rng words and z.
+        Returns (targets [nworld][n_dofs], out [nworld][n_out + 1])."""
+        tg = np.zeros(self.nworld * self.n_dofs, dtype=np.float32)
+        out = np.zeros(self.nworld * (self.n_out + 1), dtype=np.float32)
+        sp = self.spec
+        self.L.phyz_host_policy(self.nworld, self.nworld, self.n_in, self.n_h, self.n_out, self.n_dofs,
+                                float(sp.act_clamp), 1 if sp.act_clamp_slots is not None else 0, float(sp.noise_rho),
+                                0, 0, self.P(self.weights), self.P(self.std), self.P(self.in_noise), self.P(obs),
+                                self.P(rng), self.P(z), self.P(self.slots), self.P(self.clamp_slots),
+                                self.P(base_targets), self.P(tg), self.P(out))
+        return tg.reshape(self.nworld, self.n_dofs), out.reshape(self.nworld, self.n_out + 1)

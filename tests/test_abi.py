@@ -86,6 +86,30 @@ def test_error_paths_match_reference():
         s.enable_control_noise(1, 0, 0.0, 1.0, [7])
 
 
+def test_step_span_preconditions_shared_by_timing():
+    """step_many and time_step_many check the same preconditions before any
+    launch: impulse mode needs a sweep, zero steps or worlds launch nothing
+    (step_many succeeds, the timer refuses), a host-only sim never launches."""
+    s = host_sim(TM.shapes()["sphere"])
+    s.step_many(0)  # nothing to launch: a no-op even without a device
+    with pytest.raises(PhzError, match="at least one step"):
+        s.time_step_many(0, 1)
+    with pytest.raises(PhzError, match="host-only"):
+        s.time_step_many(5, 1)
+    s.enable_contact_impulse(0.0, 0.5, [(1e4, 100.0)])
+    s.contact_sweeps = 0
+    for call in (lambda: s.step_many(3), lambda: s.time_step_many(3, 2)):
+        with pytest.raises(PhzError, match="at least one contact sweep"):
+            call()
+    s.contact_sweeps = 4
+    with pytest.raises(PhzError, match="host-only"):
+        s.step_many(3)
+    empty = host_sim(TM.shapes()["sphere"], n=0)
+    empty.step_many(3)  # zero worlds: nothing to launch
+    with pytest.raises(PhzError, match="at least one world"):
+        empty.time_step_many(3, 1)
+
+
 def test_set_model_same_shape_and_collidable_count():
     m = TM.shapes()["sphere"]
     s = host_sim(m)

@@ -16,7 +16,7 @@ from oracle.oracle import Oracle
 from phyz_amd import workloads as W
 from phyz_amd.mjcf import MjcfLoader
 from phyz_amd.model import pack_geometries, uniform_frequency_gains
-from phyz_amd.sim import BatchSim
+from phyz_amd.sim import BatchSim, from_workload
 from tests.helpers import as_precision, rel_err_rows
 
 pytestmark = pytest.mark.gpu
@@ -243,3 +243,59 @@ def test_mjcf_merged_groups_match(name, groups):
     assert np.array_equal(fa, fb) and fa.mean() >= 0.5
     assert np.abs(qa[fa] - qb[fa]).max() <= 1e-9
     assert np.abs(va[fa] - vb[fa]).max() <= 1e-8 * max(1.0, np.abs(vb[fa]).max())
+
+
+def _span_bits(sim, q, v, c, tg, steps, reps):
+    out = []
+    for _ in range(reps):
+        sim.load_states(q, v, c)
+        if tg is not None:
+            sim.set_position_targets(tg)
+        sim.step_many(steps)
+        qg, vg = sim.readback_states()
+        out.append((qg.copy(), vg.copy()))
+    return out
+
+
+@pytest.mark.parametrize("cfg,nworld,groups", [(8, 32768, None), (9, 16384, None), (8, 2048, 2), (9, 2048, 2)])
+def test_merged_f32_plans_multistep_repeat(cfg, nworld, groups):
+    """The merged f32 plans the benchmarks run (the MJCF humanoid's 2 waves at
+    32768 worlds, the hand's 4 waves at 16384, five fingers on four waves) and
+    the 2-wave cap at a small size, over 200-step launches: repeated from the
+    same state they give the same bits, every world stays finite, and the
+    states stay within the f32 rollout bound of the one-lane-per-world
+    kernel's (the two differ only in the order the trunk sums its subtrees'
+    contributions)."""
+    w = W.config(cfg)
+    q, v, c, tg = w.initial_state(nworld)
+    if groups is not None:
+        os.environ["PHZ_MAX_GROUPS"] = str(groups)
+    try:
+        sim = from_workload(w, "f32", nworld=nworld)
+        info = sim.kernel_info()
+    finally:
+        os.environ.pop("PHZ_MAX_GROUPS", None)
+    parts = UNMERGED_WAVES[{8: "humanoid", 9: "shadow_hand"}[cfg]]
+    waves = info["block"] // 64
+    print(f"cfg {cfg} f32, {nworld} worlds: {waves} waves for {parts} subtrees, kernel {info}", flush=True)
+    assert 1 < waves < parts  # subtrees share waves
+    outs = _span_bits(sim, q, v, c, tg, 200, 3)
+    for k, (qg, vg) in enumerate(outs[1:], start=1):
+        same = np.all(qg.view(np.uint32) == outs[0][0].view(np.uint32), axis=1) & \
+            np.all(vg.view(np.uint32) == outs[0][1].view(np.uint32), axis=1)
+        assert same.all(), f"repeat {k} differs in {(~same).sum()} worlds"
+    qa, va = outs[0]
+    assert np.isfinite(qa).all() and np.isfinite(va).all()
+    os.environ["PHZ_PARTITION"] = "0"
+    try:
+        one = from_workload(w, "f32", nworld=nworld)
+        assert one.kernel_info()["block"] == 64
+        (qb, vb), = _span_bits(one, q, v, c, tg, 200, 1)
+    finally:
+        os.environ.pop("PHZ_PARTITION", None)
+    dq = np.abs(qa - qb).max(axis=1)
+    dv = np.abs(va - vb).max(axis=1) / np.maximum(1.0, np.abs(vb).max(axis=1))
+    print(f"  merged vs one lane after 200 steps: q max {dq.max():.2e} p99 {np.percentile(dq, 99):.2e} "
+          f"median {np.median(dq):.2e}; v max {dv.max():.2e} p99 {np.percentile(dv, 99):.2e}", flush=True)
+    assert np.median(dq) <= 1e-5 and np.percentile(dq, 99) <= 1e-3
+    assert np.median(dv) <= 1e-4

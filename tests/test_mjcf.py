@@ -3,7 +3,7 @@
 
 Loader: the articulation the reference's own benchmark-model tests assert
 (crates/phyz-mjcf/tests/benchmark_models.rs), the packed fixture
-(tests/golden/mjcf_models.npz), and the element semantics of
+(phyz_amd/data/mjcf_models.npz), and the element semantics of
 crates/phyz-mjcf/src, each checked against a closed form or an independent
 construction (inertia by voxel integration, orientations by explicit
 rotation products).
@@ -15,6 +15,7 @@ the force range, the gated limit damping and the tanh friction.
 """
 import math
 import os
+import struct
 
 import numpy as np
 import pytest
@@ -22,7 +23,7 @@ import pytest
 from oracle.oracle import Oracle
 from phyz_amd import workloads as W
 from phyz_amd.mjcf import MjcfError, MjcfLoader, quat_to_matrix, shape_principal_inertia, shape_volume
-from phyz_amd.model import (FIXED, FREE, G_CAPSULE, G_SPHERE, REVOLUTE, pack_actuators, pack_bodies,
+from phyz_amd.model import (FIXED, FREE, G_CAPSULE, G_MESH, G_SPHERE, REVOLUTE, pack_actuators, pack_bodies,
                             pack_geometries, pack_joint_terms)
 
 REF_MODELS = "/root/reference/models"
@@ -65,7 +66,7 @@ def test_benchmark_models_articulation():
 
 @need_ref
 @pytest.mark.parametrize("name", ["ant", "humanoid", "shadow_hand", "half_cheetah", "simple_arm"])
-def test_fixture_is_what_the_loader_makes_of_the_reference_models(name):
+def test_tables_are_what_the_loader_makes_of_the_reference_models(name):
     z = np.load(W.MJCF_TABLES)
     m = MjcfLoader.from_file(os.path.join(REF_MODELS, f"{name}.xml")).build_model()
     assert np.array_equal(pack_bodies(m), z[f"{name}/body"])
@@ -75,7 +76,7 @@ def test_fixture_is_what_the_loader_makes_of_the_reference_models(name):
 
 
 @pytest.mark.parametrize("name", ["ant", "humanoid", "shadow_hand", "half_cheetah", "simple_arm"])
-def test_fixture_round_trips_through_model_from_tables(name):
+def test_tables_round_trip_through_model_from_tables(name):
     z = np.load(W.MJCF_TABLES)
     m = W.mjcf_model(name)
     assert np.array_equal(pack_bodies(m), z[f"{name}/body"])
@@ -313,19 +314,96 @@ def test_unsupported_features_are_reported():
     assert tags == {"hfield", "joint", "tendon", "equality"}
 
 
-def test_includes_and_meshes_are_reported_and_skipped():
-    """<include>, mesh assets and mesh geoms are outside this loader: each is
-    reported, and the rest of the model still loads (the unloadable mesh geom
-    gives its body no shape and no mass)."""
-    xml = """<mujoco><include file="other.xml"/><asset><mesh name="m" file="m.stl"/></asset>
-        <worldbody><body><joint/><geom type="mesh" mesh="m"/><geom type="sphere" size="0.1"/></body>
-        <body><joint/><geom mesh="m"/></body></worldbody></mujoco>"""
-    L = load(xml)
-    assert {u.tag for u in L.unsupported()} == {"include", "mesh", "geom"}
+def test_includes_splice_defaults_and_bodies(tmp_path):
+    """include.rs: an included file's children land where the <include> stood
+    (its defaults apply to the including file's bodies too); nested includes
+    resolve against their own directory; a cycle stops at the depth cap; a
+    missing file or attribute is an error that names it."""
+    (tmp_path / "parts").mkdir()
+    (tmp_path / "parts" / "leg.xml").write_text("""<mujocoinclude><body name="nested_leg"><joint/>
+        <geom type="sphere" size="0.05"/></body></mujocoinclude>""")
+    (tmp_path / "child.xml").write_text("""<mujoco><default><joint damping="3.25"/></default>
+        <worldbody><body name="included_child"><joint/><include file="parts/leg.xml"/></body></worldbody></mujoco>""")
+    (tmp_path / "main.xml").write_text("""<mujoco><include file="child.xml"/>
+        <worldbody><body name="own"><joint/></body></worldbody></mujoco>""")
+    m = MjcfLoader.from_file(str(tmp_path / "main.xml")).build_model()
+    assert [b.name for b in m.bodies] == ["included_child", "nested_leg", "own"]
+    assert m.bodies[1].parent == 0
+    assert all(b.joint.damping == 3.25 for b in m.bodies)
+    (tmp_path / "a.xml").write_text('<mujoco><include file="b.xml"/></mujoco>')
+    (tmp_path / "b.xml").write_text('<mujoco><include file="a.xml"/></mujoco>')
+    with pytest.raises(MjcfError, match="cyclic"):
+        MjcfLoader.from_file(str(tmp_path / "a.xml"))
+    with pytest.raises(MjcfError, match="does_not_exist.xml"):
+        MjcfLoader.from_xml_str('<mujoco><include file="does_not_exist.xml"/></mujoco>')
+    with pytest.raises(MjcfError, match="missing required attribute 'file'"):
+        MjcfLoader.from_xml_str("<mujoco><include/></mujoco>")
+    assert MjcfLoader.from_xml_str("<mujoco><worldbody/></mujoco>").unsupported() == []
+
+
+TET = np.array([[0, 0, 0], [1, 0, 0], [0, 1, 0], [0, 0, 1]], dtype=float)
+TET_FACES = [(0, 2, 1), (0, 1, 3), (0, 3, 2), (1, 2, 3)]
+
+
+def test_mesh_files_obj_and_stl():
+    """assets.rs loaders: OBJ polygons fan into triangles, index forms v, v/vt,
+    v//vn and negative indices; binary STL by its size, ASCII STL by 'solid';
+    garbage is an error, not a crash."""
+    from phyz_amd.mjcf import _obj, _stl
+    v, f = _obj("v 0 0 0\nv 1 0 0\nv 1 1 0\nv 0 1 0\nf 1 2 3 4\n")
+    assert v.shape == (4, 3) and f.tolist() == [[0, 1, 2], [0, 2, 3]]
+    v, f = _obj("v 0 0 0\nv 1 0 0\nv 0 1 0\nf 1/1/1 2//2 -1\n")
+    assert f.tolist() == [[0, 1, 2]]
+    with pytest.raises(ValueError):
+        _obj("v 0 0 0\nf 1 2 3\n")
+    ascii_stl = b"solid t\n facet normal 0 0 1\n  outer loop\n   vertex 0 0 0\n   vertex 1 0 0\n" \
+                b"   vertex 0 1 0\n  endloop\n endfacet\nendsolid t\n"
+    v, f = _stl(ascii_stl)
+    assert v.shape == (3, 3) and f.tolist() == [[0, 1, 2]]
+    binary = b"solid-looking header".ljust(80, b"\0") + struct.pack("<I", 1) + struct.pack("<3f", 0, 0, 1) + \
+        struct.pack("<9f", 0, 0, 0, 1, 0, 0, 0, 1, 0) + b"\0\0"
+    v, f = _stl(binary)
+    assert v.shape == (3, 3) and v[1, 0] == 1.0
+    with pytest.raises(ValueError):
+        _stl(b"not a mesh at all")
+
+
+def test_mesh_assets_obj_and_binary_stl(tmp_path):
+    """<asset><mesh> through <compiler meshdir> (which wins over assetdir),
+    the name defaulting to the file stem, per-axis scale; a mesh geom
+    collides through its body-frame bounding box and adds no mass; an
+    unloadable mesh is reported and its geom dropped."""
+    (tmp_path / "meshes").mkdir()
+    (tmp_path / "meshes" / "t.obj").write_text("".join(f"v {a} {b} {c}\n" for a, b, c in TET) +
+                                               "".join(f"f {a + 1} {b + 1} {c + 1}\n" for a, b, c in TET_FACES))
+    with open(tmp_path / "meshes" / "t.stl", "wb") as f:
+        f.write(b"\0" * 80 + struct.pack("<I", 4))
+        for tri in TET_FACES:
+            f.write(struct.pack("<3f", 0, 0, 0) + b"".join(struct.pack("<3f", *TET[k] * 2) for k in tri) + b"\0\0")
+    (tmp_path / "m.xml").write_text("""<mujoco><compiler meshdir="meshes" assetdir="elsewhere"/>
+        <asset><mesh file="t.obj"/><mesh name="s" file="t.stl" scale="1 2 3"/>
+        <mesh name="gone" file="missing.stl"/></asset>
+        <worldbody><body><joint/><geom type="mesh" mesh="t"/></body>
+        <body><joint/><geom type="mesh" mesh="s" pos="0 0 0.5"/><geom type="sphere" size="0.1"/></body>
+        <body><joint/><geom type="mesh" mesh="gone"/><geom type="sphere" size="0.1"/></body></worldbody></mujoco>""")
+    L = MjcfLoader.from_file(str(tmp_path / "m.xml"))
+    ms = {m.name: m for m in L.meshes()}
+    assert list(ms) == ["t", "s", "gone"]
+    assert ms["t"].vertices.shape == (4, 3) and ms["t"].faces.shape == (4, 3)
+    assert ms["s"].vertices.shape == (12, 3) and np.allclose(ms["s"].vertices.max(axis=0), [2, 4, 6])
+    assert ms["gone"].vertices is None and "missing.stl" in ms["gone"].load_error
     m = L.build_model()
-    assert m.bodies[0].geometry.kind == G_SPHERE and len(m.bodies[0].collisions) == 1
-    assert m.bodies[0].inertia.mass == pytest.approx(1000 * 4 / 3 * math.pi * 1e-3)
-    assert m.bodies[1].geometry is None and m.bodies[1].inertia.mass == 1.0
+    g0, g1 = m.bodies[0].geometry, m.bodies[1].geometry
+    assert g0.kind == G_MESH and g0.params == (0, 0, 0, 1, 1, 1)
+    assert g1.kind == G_MESH and g1.params == (0, 0, 0, 2, 4, 6) and np.allclose(g1.origin.pos, [0, 0, 0.5])
+    assert len(m.bodies[1].collisions) == 2
+    assert m.bodies[0].inertia.mass == 1.0  # the mesh adds no mass: the body takes the default
+    sphere = 1000 * 4 / 3 * math.pi * 1e-3
+    assert m.bodies[1].inertia.mass == pytest.approx(sphere)
+    assert m.bodies[2].geometry.kind == G_SPHERE and len(m.bodies[2].collisions) == 1
+    assert {u.tag for u in L.unsupported()} == {"mesh", "geom"}
+    geom, collidable = pack_geometries(m)
+    assert collidable == 3 and int(geom[0, 0]) == G_MESH and list(geom[0, 1:7]) == [0, 0, 0, 1, 1, 1]
 
 
 # ── force terms in the oracle ───────────────────────────────────────────────
