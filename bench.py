@@ -238,11 +238,9 @@ def roofline(w, prec, steps, ev_ms, info, flops_tab, traffic_tab):
     }
 
 
-# Per-step qdd bounds, normwise relative to max|qdd| of the f64 oracle; f32
-# impulse-mode contact is held to 2e-4, the deviation of the reference's own f32
-# contact pass from the f64 law in that mode.
+# Per-step qdd bounds, normwise relative to max|qdd| of the f64 oracle, in
+# every contact mode.
 QDD_BOUND = {"f64": 1e-10, "f32": 1e-4}
-QDD_BOUND_F32_IMPULSE = 2e-4
 
 
 def device_step_parity(w, sim, prec):
@@ -257,7 +255,7 @@ def device_step_parity(w, sim, prec):
         return {"worlds_checked": 0, "pass": False, "note": "no finite world left after the timed spans"}
     idx = finite[np.linspace(0, len(finite) - 1, 64).astype(int)]
     e, extra = late_step_errors(w, sim, prec, idx)
-    bound = QDD_BOUND_F32_IMPULSE if prec == "f32" and w.impulse_sweeps > 0 else QDD_BOUND[prec]
+    bound = QDD_BOUND[prec]
     return {"worlds_checked": len(idx), "qdd_rel_err_max": float(e.max()), "qdd_rel_err_median": float(np.median(e)),
             "bound": bound, "pass": bool(e.max() <= bound), "share_within_bound": round(float(np.mean(e <= bound)), 4),
             **extra}

@@ -563,7 +563,7 @@ struct StepArgs {
   void* contact_rows;  // [nb * 8][stride], last step's contact readback
   void* ext;           // [nb * 6][stride], contact forces carried between steps (impulse mode)
   void* imp;           // [nb * 48][stride], warm-start impulses: 24 ground, 24 plane per body (impulse mode)
-  const void* hf;      // heightfield nodes [ny][nx] in T
+  const void* hf;      // heightfield nodes [ny][nx], f64 in every kernel
   double hf_ox, hf_oy, hf_oz, hf_cell;
   int hf_nx, hf_ny;
   int nworld;
@@ -591,6 +591,21 @@ template <class M, int i> struct BodyK {
 // and the world height of its origin in f64, and evaluate the depth from
 // them. Everything else about the contact, and the dynamics, stays f32.
 template <class M, class T> constexpr bool pen64() { return M::HAS_CONTACT && sizeof(T) == 4; }
+// Over a heightfield the depth also needs the contact point's world x and y,
+// and against a body-attached plane the plane's whole frame: such kernels
+// carry the chain's other two rows and origins too.
+template <class M, class T> constexpr bool full64() { return pen64<M, T>() && (M::HAS_HF || M::PLANE >= 0); }
+// Ground contact points of body i (a box's 8 corners, one support point
+// otherwise) and where they start in the per-world list of contact points.
+template <class M> constexpr int ground_pts(int i) {
+  return M::gtype[i] == G_NONE ? 0 : (M::gtype[i] == G_BOX ? 8 : 1);
+}
+template <class M> constexpr int ground_off(int i) {
+  int s = 0;
+  for (int k = 0; k < i; k++) s += ground_pts<M>(k);
+  return s;
+}
+
 
 template <class M, class T, int i> __device__ __forceinline__ Sym<T> rigid_inertia() {
   Sym<T> s;
@@ -629,18 +644,26 @@ template <class M, class T, int i, bool FAST = false> __device__ __forceinline__
   }
 }
 
-// Heightfield terrain: nodes h[iy * nx + ix] and the header, uniform over a launch.
+// Heightfield terrain: nodes h[iy * nx + ix] and the header, uniform over a
+// launch. Always f64, in f32 kernels too: the terrain's height and normal are
+// evaluated in f64 at the contact point's f64 position, so that which side of
+// a contact threshold a point lies on, and which cell it is in, is decided as
+// the f64 oracle decides it.
 template <class T> struct Terrain {
-  const T* h;
-  T ox, oy, oz, cell;
+  const double* h;
+  double ox, oy, oz, cell;
   int nx, ny;
 };
 
 // Cell and fraction along one axis, clamped to the grid. The cell index is in
 // [0, n - 2] whatever w holds (a diverged world's NaN or inf included).
+// Grid coordinate of w along one axis, clamped to the grid.
+template <class T> __device__ __forceinline__ T hf_u(T w, T o, int n, T cell) {
+  return n < 2 ? T(0) : dmin(dmax((w - o) / cell, T(0)), T(n - 1));
+}
 template <class T> __device__ __forceinline__ void hf_locate(T w, T o, int n, T cell, int& i, T& t) {
   if (n < 2) { i = 0; t = T(0); return; }
-  const T u = dmin(dmax((w - o) / cell, T(0)), T(n - 1));
+  const T u = hf_u(w, o, n, cell);
   int ii = cvt_sat_i32(u);
   ii = ii < 0 ? 0 : (ii > n - 2 ? n - 2 : ii);
   i = ii;
@@ -649,29 +672,82 @@ template <class T> __device__ __forceinline__ void hf_locate(T w, T o, int n, T 
 
 // Terrain height and unit normal at world (x, y): the flat ground, or the
 // bilinear heightfield with its cell-wise gradient (phyz_kernels.cu:641-664).
-template <class M, class T> __device__ __forceinline__ T terrain_at(const Terrain<T>& tr, T px, T py, V3<T>& n) {
+// hf_cell finds the cell, the fractions in it and whether x and y lie over the
+// grid (outside it the height is the edge's and the gradient along that axis
+// zero); hf_eval evaluates the patch. terrain_at does both in f64.
+struct HfCell {
+  int ix, iy;
+  bool inx, iny;
+};
+template <class T, class S>
+__device__ __forceinline__ HfCell hf_cell(const Terrain<T>& tr, S px, S py, S& tx, S& ty) {
+  HfCell c;
+  hf_locate(px, S(tr.ox), tr.nx, S(tr.cell), c.ix, tx);
+  hf_locate(py, S(tr.oy), tr.ny, S(tr.cell), c.iy, ty);
+  c.inx = tr.nx >= 2 && px >= S(tr.ox) && px <= S(tr.ox + double(tr.nx - 1) * tr.cell);
+  c.iny = tr.ny >= 2 && py >= S(tr.oy) && py <= S(tr.oy + double(tr.ny - 1) * tr.cell);
+  return c;
+}
+template <class T, class S>
+__device__ __forceinline__ S hf_eval(const Terrain<T>& tr, const HfCell& c, S tx, S ty, S* grad) {
+  const int ix1 = c.ix + 1 < tr.nx - 1 ? c.ix + 1 : tr.nx - 1;
+  const int iy1 = c.iy + 1 < tr.ny - 1 ? c.iy + 1 : tr.ny - 1;
+  const S oz = S(tr.oz);
+  const S h00 = oz + S(tr.h[c.iy * tr.nx + c.ix]), h10 = oz + S(tr.h[c.iy * tr.nx + ix1]);
+  const S h01 = oz + S(tr.h[iy1 * tr.nx + c.ix]), h11 = oz + S(tr.h[iy1 * tr.nx + ix1]);
+  const S h = (h00 * (S(1) - tx) + h10 * tx) * (S(1) - ty) + (h01 * (S(1) - tx) + h11 * tx) * ty;
+  const S cell = S(tr.cell);
+  grad[0] = c.inx ? -(((h10 - h00) * (S(1) - ty) + (h11 - h01) * ty) / cell) : S(0);
+  grad[1] = c.iny ? -(((h01 - h00) * (S(1) - tx) + (h11 - h10) * tx) / cell) : S(0);
+  return h;
+}
+template <class M, class T>
+__device__ __forceinline__ double terrain_at(const Terrain<T>& tr, double px, double py, V3<double>& n,
+                                             HfCell* cell_out = nullptr) {
   if constexpr (!M::HAS_HF) {
-    n = v3(T(0), T(0), T(1));
-    return T(M::ground_h);
+    n = v3(0.0, 0.0, 1.0);
+    return M::ground_h;
   } else {
-    int ix, iy;
-    T tx, ty;
-    hf_locate(px, tr.ox, tr.nx, tr.cell, ix, tx);
-    hf_locate(py, tr.oy, tr.ny, tr.cell, iy, ty);
-    const int ix1 = ix + 1 < tr.nx - 1 ? ix + 1 : tr.nx - 1;
-    const int iy1 = iy + 1 < tr.ny - 1 ? iy + 1 : tr.ny - 1;
-    const T h00 = tr.oz + tr.h[iy * tr.nx + ix], h10 = tr.oz + tr.h[iy * tr.nx + ix1];
-    const T h01 = tr.oz + tr.h[iy1 * tr.nx + ix], h11 = tr.oz + tr.h[iy1 * tr.nx + ix1];
-    const T h = (h00 * (T(1) - tx) + h10 * tx) * (T(1) - ty) + (h01 * (T(1) - tx) + h11 * tx) * ty;
-    T dhdx = T(0), dhdy = T(0);
-    if (tr.nx >= 2 && px >= tr.ox && px <= tr.ox + T(tr.nx - 1) * tr.cell)
-      dhdx = ((h10 - h00) * (T(1) - ty) + (h11 - h01) * ty) / tr.cell;
-    if (tr.ny >= 2 && py >= tr.oy && py <= tr.oy + T(tr.ny - 1) * tr.cell)
-      dhdy = ((h01 - h00) * (T(1) - tx) + (h11 - h10) * tx) / tr.cell;
-    const V3<T> g = v3(-dhdx, -dhdy, T(1));
-    n = g * frsqrt(dot(g, g));  // |g| >= 1
+    double tx, ty, g[2];
+    const HfCell c = hf_cell(tr, px, py, tx, ty);
+    const double h = hf_eval(tr, c, tx, ty, g);
+    const V3<double> gv = v3(g[0], g[1], 1.0);
+    n = gv * (1.0 / sqrt(dot(gv, gv)));  // |g| >= 1
+    if (cell_out) *cell_out = c;
     return h;
   }
+}
+// A cell packed in one word: ix (15 bits), iy (15 bits), the two over-grid
+// flags (the host limits heightfields to 32768 nodes per axis).
+__device__ __forceinline__ int pack_cell(const HfCell& c) {
+  return c.ix | (c.iy << 15) | (c.inx ? 1 << 30 : 0) | (c.iny ? int(1u << 31) : 0);
+}
+__device__ __forceinline__ HfCell unpack_cell(int w) {
+  return HfCell{w & 0x7fff, (w >> 15) & 0x7fff, ((w >> 30) & 1) != 0, w < 0};
+}
+template <class T> __device__ __forceinline__ V3<T> to_t(const V3<double>& a) { return v3(T(a.x), T(a.y), T(a.z)); }
+
+// A depth computed in f64 and kept in f32 for the contact law, on the same
+// side of the law's activation threshold (0 in penalty mode, -margin in
+// impulse mode) as the f64 value: the f32 rounding moves it by at most one
+// ulp of the threshold, where the law's force is continuous in the depth
+// (impulse mode's impedance vanishes at -margin), so only the decision is
+// carried, not a new value.
+__device__ __forceinline__ float next_above(float t) {
+  if (t == 0.0f) return 1.17549435e-38f;
+  const int b = __builtin_bit_cast(int, t);
+  return __builtin_bit_cast(float, t > 0.0f ? b + 1 : b - 1);
+}
+template <class M, class T> __device__ __forceinline__ T pen_decided(double pen) {
+  constexpr double thr = M::CMODE == 1 ? -M::c_margin : 0.0;
+  const T t = T(thr);
+  T p = T(pen);
+  if constexpr (sizeof(T) == 4) {
+    const bool in = pen > thr;
+    p = (in && !(p > t)) ? next_above(t) : p;
+    p = (!in && p > t) ? t : p;
+  }
+  return p;
 }
 
 // Contact point cp of body i's shape, body frame: a box corner, or the
@@ -795,15 +871,51 @@ __device__ __forceinline__ void impulse_update(T pen, T b_n, T b_u, T b_w, T a_n
   slot[2] = tw * sc;
 }
 
+template <class M, class T> struct WS;
+
+// Depth, terrain height and unit normal (world) at contact point cp of body i.
+// The f32 kernels take them from pass 1's f64 chain (pen64): over a
+// heightfield the values pass 1 evaluated in f64 at the point's f64 position,
+// on flat ground the ground height minus the point's f64 height; the depth is
+// kept on the f64 side of the law's threshold (pen_decided), so the f32
+// kernels switch a contact on and off where the f64 oracle does. The f64
+// kernels evaluate them from supw.
+template <class M, class T, int i>
+__device__ __forceinline__ void contact_depth(const WS<M, T>& ws, const Terrain<T>& tr, int cp, const V3<T>& supw,
+                                              T& pen, T& th, V3<T>& nw) {
+  const int k = ground_off<M>(i) + cp;
+  if constexpr (pen64<M, T>() && M::HAS_HF) {
+    // Height and normal in f32 in the cell pass 1 chose in f64: continuous
+    // in the point's position, so the f32 position serves.
+    pen = ws.hf_pen[k];
+    const HfCell c = unpack_cell(ws.hf_cellw[k]);
+    T g[2];
+    const T tx = hf_u(supw.x, T(tr.ox), tr.nx, T(tr.cell)) - T(c.ix);
+    const T ty = hf_u(supw.y, T(tr.oy), tr.ny, T(tr.cell)) - T(c.iy);
+    th = hf_eval(tr, c, tx, ty, g);
+    const V3<T> gv = v3(g[0], g[1], T(1));
+    nw = gv * frsqrt(dot(gv, gv));
+  } else if constexpr (pen64<M, T>()) {
+    pen = pen_decided<M, T>(M::ground_h - ws.cz64[k]);
+    th = T(M::ground_h);
+    nw = v3(T(0), T(0), T(1));
+  } else {
+    V3<double> n64;
+    const double th64 = terrain_at<M, T>(tr, double(supw.x), double(supw.y), n64);
+    pen = T(n64.z * (th64 - double(supw.z)));
+    th = T(th64);
+    nw = to_t<T>(n64);
+  }
+}
+
 // Ground penalty contact of body i (crates/phyz-gpu/cuda/phyz_kernels.cu:804-980,
 // penalty branch 939-965). Rw: body->world rotation, pw: body origin in world,
 // vel: body-frame spatial velocity. Returns the body-frame spatial force. When
 // `write` is set, stores the readback row (touching, deepest penetration,
 // point (x, y, h), summed world force) at out[k * S], k = 8 i .. 8 i + 7.
 template <class M, class T, int i>
-__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const double* cz64,
-                                              const V3<double>& zb64, const Terrain<T>& tr, T* out, int S,
-                                              bool write) {
+__device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const SV<T>& vel, const WS<M, T>& ws,
+                                              const Terrain<T>& tr, T* out, int S, bool write) {
   constexpr int gt = M::gtype[i];
   constexpr int npts = gt == G_BOX ? 8 : 1;
   constexpr double sc = gt == G_BOX ? 0.25 : 1.0;
@@ -817,17 +929,12 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
 #pragma unroll
   for (int cp = 0; cp < npts; cp++) {
     V3<T> sup;
-    if constexpr (pen64<M, T>()) sup = contact_point<M, T, i, double>(cp, zb, zb64);
+    if constexpr (pen64<M, T>()) sup = contact_point<M, T, i, double>(cp, zb, ws.zb64[i]);
     else sup = contact_point<M, T, i>(cp, zb);
     V3<T> supw = pw + mul(Rw, sup);
+    T pen, th;
     V3<T> nw;
-    const T th = terrain_at<M, T>(tr, supw.x, supw.y, nw);
-    T pen;
-    if constexpr (pen64<M, T>()) {
-      pen = T(double(nw.z) * (double(th) - cz64[cp]));
-    } else {
-      pen = nw.z * (th - supw.z);
-    }
+    contact_depth<M, T, i>(ws, tr, cp, supw, pen, th, nw);
     const V3<T> nb = M::HAS_HF ? tmul(Rw, nw) : zb;
     const bool in = pen > T(0);
     V3<T> vpt = vel.l + cross(vel.a, sup);
@@ -880,14 +987,6 @@ __device__ __forceinline__ SV<T> contact_body(const R3<T>& Rw, V3<T> pw, const S
 // With m' = max(m_n / n_active, 1e-9) and c_t = max(m_t, 1e-9) / n_active the
 // reference's update (bias - r_n) / a_nn and -(b_t - a_tt s_t) / a_tt reads
 //   f_n = max((bias - v_n (1 + e)) m' + s_n, 0),  f_t = s_t - b_t c_t.
-template <class M> constexpr int ground_pts(int i) {
-  return M::gtype[i] == G_NONE ? 0 : (M::gtype[i] == G_BOX ? 8 : 1);
-}
-template <class M> constexpr int ground_off(int i) {
-  int s = 0;
-  for (int k = 0; k < i; k++) s += ground_pts<M>(k);
-  return s;
-}
 template <class M, class T> struct GroundPrep {
   static constexpr int N = ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1;
   V3<T> sup[N], nb[N], tu[N];  // body frame; the second tangent is nb x tu (tangent_frame)
@@ -899,8 +998,9 @@ template <class M, class T> struct GroundPrep {
 // Body i's contact geometry; writes the position part of its readback row
 // (touching, deepest penetration, deepest point) when `write`.
 template <class M, class T, int i>
-__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const double* cz64, const V3<double>& zb64,
-                                               const Terrain<T>& tr, GroundPrep<M, T>& gp, T* out, int S, bool write) {
+__device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const WS<M, T>& ws, const Terrain<T>& tr,
+                                               GroundPrep<M, T>& gp, T* out, int S, bool write) {
+  const V3<double>& zb64 = ws.zb64[i];
   constexpr int n = ground_pts<M>(i), o = ground_off<M>(i);
   const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
   const V3<T> zb = v3(Rw.m[6], Rw.m[7], Rw.m[8]);  // world +Z in the body frame
@@ -912,13 +1012,9 @@ __device__ __forceinline__ void ground_prepare(const R3<T>& Rw, V3<T> pw, const 
     if constexpr (pen64<M, T>()) gp.sup[o + cp] = contact_point<M, T, i, double>(cp, zb, zb64);
     else gp.sup[o + cp] = contact_point<M, T, i>(cp, zb);
     supw[cp] = pw + mul(Rw, gp.sup[o + cp]);
+    T th;
     V3<T> nw;
-    const T th = terrain_at<M, T>(tr, supw[cp].x, supw[cp].y, nw);
-    if constexpr (pen64<M, T>()) {
-      pen[cp] = T(double(nw.z) * (double(th) - cz64[cp]));
-    } else {
-      pen[cp] = nw.z * (th - supw[cp].z);
-    }
+    contact_depth<M, T, i>(ws, tr, cp, supw[cp], pen[cp], th, nw);
     gp.in[o + cp] = pen[cp] > T(-M::c_margin);
     gp.nb[o + cp] = M::HAS_HF ? tmul(Rw, nw) : zb;
     nact += gp.in[o + cp] ? 1 : 0;
@@ -998,9 +1094,49 @@ __device__ __forceinline__ SV<T> ground_sweep(const GroundPrep<M, T>& gp, const 
 // body's local +Z face at plane_offset, finite in x and y, against every other
 // collidable body not excluded. Forces land on both bodies (added to f). In
 // impulse mode pslot[i] holds body i's plane impulses.
+// The plane contacts' decisions, made once per step after pass 1 from the
+// f64 chain (f32 kernels; full64): for each body, bits 0-7 say which of its
+// contact points lie within the plane's depth range, bit 8 whether its
+// footprint overlaps the plane's face. The f32 contact law below then
+// switches each contact on and off where the f64 oracle does; the depths and
+// points it applies stay f32 (the law is continuous in them otherwise).
+template <class M, class T>
+__device__ __forceinline__ void plane_decide(const WS<M, T>& ws, int (&mask)[M::NB]) {
+  constexpr int pb = M::PLANE;
+  const V3<double> nw = v3(ws.xb64[pb].z, ws.yb64[pb].z, ws.zb64[pb].z);
+  const V3<double> ppb = v3(ws.px64[pb], ws.py64[pb], ws.pz64[pb]);
+  const V3<double> p0 = ppb + nw * M::plane_offset;
+  const V3<double> c0 = v3(ws.xb64[pb].x, ws.yb64[pb].x, ws.zb64[pb].x);  // the plane body's x and y axes, world
+  const V3<double> c1 = v3(ws.xb64[pb].y, ws.yb64[pb].y, ws.zb64[pb].y);
+  sfor<0, M::NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    mask[i] = 0;
+    if constexpr (i != pb && M::gtype[i] != G_NONE && !M::gskip[i]) {
+      constexpr int npts = M::gtype[i] == G_BOX ? 8 : 1;
+      const V3<double> nbi = ws.xb64[i] * nw.x + ws.yb64[i] * nw.y + ws.zb64[i] * nw.z;
+      double lox = 1e30, loy = 1e30, hix = -1e30, hiy = -1e30;
+      int m = 0;
+#pragma unroll
+      for (int cp = 0; cp < npts; cp++) {
+        const V3<double> sp = contact_point<M, double, i>(cp, nbi);
+        const V3<double> spw = v3(ws.px64[i] + dot(ws.xb64[i], sp), ws.py64[i] + dot(ws.yb64[i], sp),
+                                  ws.pz64[i] + dot(ws.zb64[i], sp));
+        const V3<double> d = spw - ppb;
+        const double rx = dot(c0, d), ry = dot(c1, d);
+        lox = dmin(lox, rx); loy = dmin(loy, ry);
+        hix = dmax(hix, rx); hiy = dmax(hiy, ry);
+        const double pen = -dot(spw - p0, nw);
+        m |= (pen > 0.0 && pen <= M::plane_depth) ? 1 << cp : 0;
+      }
+      const bool over = !(dmax(lox, -M::plane_hx) > dmin(hix, M::plane_hx) || dmax(loy, -M::plane_hy) > dmin(hiy, M::plane_hy));
+      mask[i] = m | (over ? 1 << 8 : 0);
+    }
+  });
+}
+
 template <class M, class T, bool IMP>
 __device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw, const SV<T>* vel, T (*pslot)[24],
-                                               SV<T>* f) {
+                                               SV<T>* f, const int* mask64) {
   constexpr int pb = M::PLANE;
   const double dtc = M::dt > 1e-9 ? M::dt : 1e-9;
   const V3<T> nw = v3(Rw[pb].m[2], Rw[pb].m[5], Rw[pb].m[8]);  // the face normal, world
@@ -1022,16 +1158,22 @@ __device__ __forceinline__ void plane_contacts(const R3<T>* Rw, const V3<T>* Pw,
         lox = dmin(lox, rp.x); loy = dmin(loy, rp.y);
         hix = dmax(hix, rp.x); hiy = dmax(hiy, rp.y);
         const T d = -dot(spw[cp] - p0, nw);
-        cnt += (d > T(0) && d <= T(M::plane_depth)) ? 1 : 0;
+        if constexpr (pen64<M, T>()) cnt += (mask64[i] >> cp) & 1;
+        else cnt += (d > T(0) && d <= T(M::plane_depth)) ? 1 : 0;
       }
       const T olx = dmax(lox, T(-M::plane_hx)), oly = dmax(loy, T(-M::plane_hy));
       const T ohx = dmin(hix, T(M::plane_hx)), ohy = dmin(hiy, T(M::plane_hy));
-      if (!(olx > ohx || oly > ohy)) {
+      bool over;
+      if constexpr (pen64<M, T>()) over = ((mask64[i] >> 8) & 1) != 0;
+      else over = !(olx > ohx || oly > ohy);
+      if (over) {
         const T na = T(cnt > 1 ? cnt : 1);
 #pragma unroll
         for (int cp = 0; cp < npts; cp++) {
           const T pen = -dot(spw[cp] - p0, nw);
-          const bool in = pen > T(0) && pen <= T(M::plane_depth);
+          bool in;
+          if constexpr (pen64<M, T>()) in = ((mask64[i] >> cp) & 1) != 0;
+          else in = pen > T(0) && pen <= T(M::plane_depth);
           V3<T> rpp = tmul(Rw[pb], spw[cp] - Pw[pb]);
           rpp.x = dmin(dmax(rpp.x, olx), ohx);
           rpp.y = dmin(dmax(rpp.y, oly), ohy);
@@ -1113,6 +1255,14 @@ template <class M, class T> struct WS {
   V3<double> zb64[M::NB];  // f64 penetration chain (f32 kernels with contact)
   double pz64[M::NB];
   double cz64[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];  // contact points' world heights
+  // The chain's other two rows and origins (heightfield or body-attached plane):
+  // contact points' world x, y, and the plane's frame, in f64.
+  V3<double> xb64[M::NB], yb64[M::NB];
+  double px64[M::NB], py64[M::NB];
+  // Over a heightfield, each contact point's depth (pen_decided) and terrain
+  // cell (pack_cell), both decided in pass 1 in f64.
+  T hf_pen[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];
+  int hf_cellw[ground_off<M>(M::NB) > 0 ? ground_off<M>(M::NB) : 1];
   T ts[M::NB], tc[M::NB];  // revolute joints' sin and cos of -q (split-lane kernels)
   Sym<T> cI[M::NB];        // a group's summed subtree contributions to trunk body p (groups other than 0)
   SV<T> cP[M::NB];
@@ -1259,14 +1409,40 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
     if constexpr (p < 0) {
       ws.zb64[i] = v3(E64.m[2], E64.m[5], E64.m[8]);
       ws.pz64[i] = r64.z;
+      if constexpr (full64<M, T>()) {
+        ws.xb64[i] = v3(E64.m[0], E64.m[3], E64.m[6]);
+        ws.yb64[i] = v3(E64.m[1], E64.m[4], E64.m[7]);
+        ws.px64[i] = r64.x;
+        ws.py64[i] = r64.y;
+      }
     } else {
       ws.zb64[i] = mul(E64, ws.zb64[p]);
       ws.pz64[i] = ws.pz64[p] + dot(ws.zb64[p], r64);
+      if constexpr (full64<M, T>()) {
+        ws.xb64[i] = mul(E64, ws.xb64[p]);
+        ws.yb64[i] = mul(E64, ws.yb64[p]);
+        ws.px64[i] = ws.px64[p] + dot(ws.xb64[p], r64);
+        ws.py64[i] = ws.py64[p] + dot(ws.yb64[p], r64);
+      }
     }
-    // Only the contact points' heights outlive the body's children.
+    // Only the contact points' world heights (and over a heightfield their
+    // x, y) outlive the body's children.
 #pragma unroll
-    for (int cp = 0; cp < ground_pts<M>(i); cp++)
-      ws.cz64[ground_off<M>(i) + cp] = ws.pz64[i] + dot(ws.zb64[i], contact_point<M, double, i>(cp, ws.zb64[i]));
+    for (int cp = 0; cp < ground_pts<M>(i); cp++) {
+      const int k = ground_off<M>(i) + cp;
+      const V3<double> sp = contact_point<M, double, i>(cp, ws.zb64[i]);
+      const double cz = ws.pz64[i] + dot(ws.zb64[i], sp);
+      if constexpr (M::HAS_HF) {
+        V3<double> n64;
+        HfCell c;
+        const double th =
+            terrain_at<M, T>(tr, ws.px64[i] + dot(ws.xb64[i], sp), ws.py64[i] + dot(ws.yb64[i], sp), n64, &c);
+        ws.hf_pen[k] = pen_decided<M, T>(n64.z * (th - cz));
+        ws.hf_cellw[k] = pack_cell(c);
+      } else {
+        ws.cz64[k] = cz;
+      }
+    }
   } else if constexpr (M::LANES > 1 && M::jtype[i] == J_REV) {
     rev_xf<M, T, i>(ws.ts[i], ws.tc[i], v, X, vj);
   } else {
@@ -1291,8 +1467,7 @@ __device__ __forceinline__ void body_pass1(WS<M, T>& ws, const T* q, const T* v,
   }
   if constexpr (M::gtype[i] != G_NONE) {
     if (do_contact) {
-      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], ws.cz64 + ground_off<M>(i), ws.zb64[i], tr, rows, S,
-                                             write_rows);
+      SV<T> f = contact_body<M, T, i>(ws.Rw[i], ws.Pw[i], ws.vel[i], ws, tr, rows, S, write_rows);
       ws.pA[i] = ws.pA[i] - f;
     }
   }
@@ -1700,7 +1875,9 @@ __device__ __forceinline__ void step_group(T (&q)[M::NQ], T (&v)[M::NV], T (&ctr
     // Body-attached plane, penalty law (one group owns every body here).
     SV<T> fp[NB];
     sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; fp[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))}; });
-    plane_contacts<M, T, false>(ws.Rw, ws.Pw, ws.vel, (T(*)[24]) nullptr, fp);
+    int pmask[NB];
+    if constexpr (pen64<M, T>()) plane_decide<M, T>(ws, pmask);
+    plane_contacts<M, T, false>(ws.Rw, ws.Pw, ws.vel, (T(*)[24]) nullptr, fp, pmask);
     sfor<0, NB>([&](auto I) { constexpr int i = decltype(I)::value; ws.pA[i] = ws.pA[i] - fp[i]; });
   }
   // ── pass 2: own bodies, leaves first ──
@@ -1917,6 +2094,15 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     constexpr int i = decltype(I)::value;
     body_pass1<M, T, i>(ws, q, v, rows, S, false, false, tr);
   });
+  // The contacts' geometry depends on q alone: prepared straight after pass 1,
+  // so the world transforms it reads need not outlive passes 2 and 3.
+  int pmask[NB];
+  if constexpr (M::PLANE >= 0 && pen64<M, T>()) plane_decide<M, T>(ws, pmask);
+  GroundPrep<M, T> gp;
+  sfor<0, NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    if constexpr (M::gtype[i] != G_NONE) ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws, tr, gp, rows, S, write_rows);
+  });
   sfor<0, NB>([&](auto I) {
     constexpr int i = decltype(I)::value;
     if constexpr (HasExt<M>::template at<i>()) ws.pA[i] = ws.pA[i] - ext[i];
@@ -1939,13 +2125,6 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
     }
   });
   sfor<0, NB>([&](auto I) { body_pass3<M, T, decltype(I)::value>(ws, qdd); });
-  GroundPrep<M, T> gp;
-  sfor<0, NB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    if constexpr (M::gtype[i] != G_NONE)
-      ground_prepare<M, T, i>(ws.Rw[i], ws.Pw[i], ws.cz64 + ground_off<M>(i), ws.zb64[i], tr, gp, rows, S,
-                              write_rows);
-  });
   // Each sweep moves qdd by the ABA's response to that sweep's change of the
   // contact forces (the solve is affine in them): qdd and ext carry from one
   // sweep to the next, so neither the step's first qdd nor its first forces
@@ -1999,7 +2178,7 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
         ext[i] = SV<T>{v3(T(0), T(0), T(0)), v3(T(0), T(0), T(0))};
       }
     });
-    if constexpr (M::PLANE >= 0) plane_contacts<M, T, true>(ws.Rw, ws.Pw, vf, impp, ext);
+    if constexpr (M::PLANE >= 0) plane_contacts<M, T, true>(ws.Rw, ws.Pw, vf, impp, ext, pmask);
     sfor<0, NB>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if constexpr (HasExt<M>::template at<i>()) dp[i] = dp[i] - ext[i];
@@ -2079,7 +2258,7 @@ template <class M, class T, int G> __device__ __forceinline__ void run_group(con
   u64 rng = 0;
   if constexpr (M::NNOISE > 0) rng = a.rng[wl];
   T* rows = M::HAS_CONTACT ? (T*)a.contact_rows + wl : nullptr;
-  const Terrain<T> tr{(const T*)a.hf, T(a.hf_ox), T(a.hf_oy), T(a.hf_oz), T(a.hf_cell), a.hf_nx, a.hf_ny};
+  const Terrain<T> tr{(const double*)a.hf, a.hf_ox, a.hf_oy, a.hf_oz, a.hf_cell, a.hf_nx, a.hf_ny};
   const int n = a.nsteps;
   if constexpr (M::HAS_CONTACT && M::CMODE == 1) {
     // Impulse mode: one group (checked on the host); the solver state persists.

@@ -1187,7 +1187,7 @@ struct phz_sim {
   int max_steps = 1000;
   hipStream_t stream = nullptr;
   void *q = nullptr, *v = nullptr, *ctrl = nullptr, *qdd = nullptr, *targets = nullptr, *rows = nullptr;
-  void *ext_buf = nullptr, *imp_buf = nullptr, *hf_buf = nullptr;  // impulse solver state; heightfield nodes (T)
+  void *ext_buf = nullptr, *imp_buf = nullptr, *hf_buf = nullptr;  // impulse solver state; heightfield nodes (f64)
   size_t hf_cap = 0;                                                // node capacity of hf_buf
   uint64_t* rng = nullptr;
   double* staging = nullptr;
@@ -1568,15 +1568,12 @@ bool check_heightfield(phz_sim* s, const double* hf, const double* heights, int&
   return true;
 }
 
+// The nodes stay f64 on the device in every precision: the kernels evaluate
+// the terrain in f64 (see Terrain in phz_device.h).
 bool upload_heightfield(phz_sim* s, const double* heights, size_t n) {
   if (!s->has_device()) return true;
-  const size_t E = s->esize();
-  std::vector<char> buf(n * E);
-  for (size_t k = 0; k < n; k++) {
-    if (s->f64) ((double*)buf.data())[k] = heights[k];
-    else ((float*)buf.data())[k] = (float)heights[k];
-  }
-  if (!s->hip_ok(hipMemcpyAsync(s->hf_buf, buf.data(), n * E, hipMemcpyHostToDevice, s->stream), "upload heightfield"))
+  if (!s->hip_ok(hipMemcpyAsync(s->hf_buf, heights, n * sizeof(double), hipMemcpyHostToDevice, s->stream),
+                 "upload heightfield"))
     return false;
   return s->hip_ok(hipStreamSynchronize(s->stream), "upload heightfield");
 }
@@ -1643,7 +1640,7 @@ int set_contact(phz_sim* s, const ContactSpec& cs, uint32_t* collidable_out) {
     // Node buffer sized to this first field (set_heightfield may shrink, not grow, it).
     const size_t nodes = (size_t)std::max(nx, 1) * std::max(ny, 1);
     if (s->hf_buf) { s->invalidate(); hipFree(s->hf_buf); s->hf_buf = nullptr; }
-    if (!s->alloc(&s->hf_buf, nodes * E, "heightfield alloc")) return 1;
+    if (!s->alloc(&s->hf_buf, nodes * sizeof(double), "heightfield alloc")) return 1;
     s->hf_cap = nx > 0 ? nodes : 0;
     if (nx > 0 && !upload_heightfield(s, cs.heights, nodes)) return 1;
   } else {

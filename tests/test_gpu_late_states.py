@@ -4,9 +4,7 @@ small and the feet rest in stick friction, the regime where f32 rounding of the
 contact geometry is amplified most. Each case rolls the workload forward on
 the device from its seeded states, then holds one more device step of 256
 sampled worlds to the f64 oracle: qdd normwise relative error <= 1e-4, the f32
-bound, in penalty mode; <= 2e-4 in impulse mode (workload 6), whose f32 kernel
-evaluates penetration depths in f32, like the reference's own f32 contact pass,
-which deviates from the f64 law by up to 2e-4 in this mode."""
+bound, in every contact mode (workload 6: heightfield terrain, impulse mode)."""
 import numpy as np
 import pytest
 
@@ -17,7 +15,6 @@ from tests.helpers import late_step_errors
 pytestmark = pytest.mark.gpu
 
 TOL_F32 = 1e-4
-TOL_F32_IMPULSE = 2e-4
 
 
 @pytest.mark.parametrize("cfg,steps", [(3, 1000), (3, 300), (4, 1000), (6, 1000), (7, 1000), (7, 2000), (8, 300),
@@ -37,7 +34,7 @@ def test_f32_late_state_parity(cfg, steps):
     assert finite.size >= n // 2
     idx = finite[np.linspace(0, finite.size - 1, 256).astype(int)]
     e, extra = late_step_errors(w, sim, "f32", idx)
-    tol = TOL_F32_IMPULSE if w.impulse_sweeps > 0 else TOL_F32
+    tol = TOL_F32
     print(f"  qdd rel err max {e.max():.3e} p99 {np.percentile(e, 99):.3e} median {np.median(e):.3e}; "
           f"within 1e-4 {np.mean(e <= TOL_F32):.4f} {extra}", flush=True)
     assert e.max() <= tol, f"world {idx[e.argmax()]}: {e.max():.3e}"
