@@ -297,5 +297,5 @@ def test_merged_f32_plans_multistep_repeat(cfg, nworld, groups):
     dv = np.abs(va - vb).max(axis=1) / np.maximum(1.0, np.abs(vb).max(axis=1))
     print(f"  merged vs one lane after 200 steps: q max {dq.max():.2e} p99 {np.percentile(dq, 99):.2e} "
           f"median {np.median(dq):.2e}; v max {dv.max():.2e} p99 {np.percentile(dv, 99):.2e}", flush=True)
-    assert np.median(dq) <= 1e-5 and np.percentile(dq, 99) <= 1e-3
-    assert np.median(dv) <= 1e-4
+    # Measured: q max 1.0e-6, v max 2.5e-6 (relative) over these cases.
+    assert dq.max() <= 1e-5 and dv.max() <= 1e-5
