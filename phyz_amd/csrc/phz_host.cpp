@@ -169,6 +169,7 @@ struct Features {
   // for the partition plan.
   int wgs = 0, cus = 256;
   bool f64 = false;  // the sim's precision (the planner keeps f64 subtrees one per wave)
+  bool host_only = false;  // a sim without a device (device ordinal -1): code generation only
   // Terms of the CPU model that the device body table has no slots for
   // (joint.rs:27-104, model.rs:18-82): the soft position limit and dry friction
   // of one-DOF joints (one entry per body; empty: none), and actuators (empty:
@@ -219,6 +220,13 @@ struct Plan {
 Plan plan_partition(const ModelD& m, const Features& f) {
   const int nb = m.nb;
   Plan pl;
+  // PHZ_HOST_LIFT_GUARDS=1 lifts the two guards below (f64 plans keep one
+  // subtree per wave; no plan has exactly three waves) on host-only sims,
+  // whose kernels are only generated: the host emulation of the step kernel
+  // (tests/host_emulation.py) builds the guarded plans for the CPU. A device
+  // sim always keeps both guards.
+  const char* lift_env = std::getenv("PHZ_HOST_LIFT_GUARDS");
+  const bool lift_guards = f.host_only && lift_env && lift_env[0] == '1';
   std::vector<int> all(nb);
   for (int i = 0; i < nb; i++) all[i] = i;
   const char* env = std::getenv("PHZ_PARTITION");
@@ -348,7 +356,7 @@ Plan plan_partition(const ModelD& m, const Features& f) {
       for (int k = 0; k < n; k++) g[owner[k]].push_back(k);
       std::vector<std::vector<int>> h;
       for (auto& x : g) if (!x.empty()) h.push_back(x);
-      if (h.size() == 3) return;
+      if (h.size() == 3 && !lift_guards) return;
       std::vector<double> load;
       for (auto& x : h) { double l = 0; for (int k : x) l += pw[k]; load.push_back(l); }
       const double c = cost(load);
@@ -404,9 +412,11 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   std::vector<std::vector<int>> unmerged;
   for (int k : by_weight) unmerged.push_back(parts[k]);
   if (const char* e = std::getenv("PHZ_MAX_GROUPS")) {
-    // Rounded down to 1, 2, 4 or 8, the caps the planner itself tries.
+    // Rounded down to 1, 2, 4 or 8, the caps the planner itself tries (3
+    // stays 3 when the guards are lifted, for the host emulation).
     const int want = std::atoi(e);
-    parts = as_bodies(pack(want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1).first);
+    const int cap = (lift_guards && want == 3) ? 3 : want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
+    parts = as_bodies(pack(cap).first);
   } else {
     std::vector<std::vector<int>> best;
     double best_cost = -1;
@@ -419,7 +429,7 @@ Plan plan_partition(const ModelD& m, const Features& f) {
     }
     parts = as_bodies(best);
   }
-  if (parts.size() == 3) return lane_per_world();  // unreachable: pack(2) holds at most two
+  if (parts.size() == 3 && !lift_guards) return lane_per_world();  // unreachable: pack(2) holds at most two
   if (parts.size() < 2) return lane_per_world();
   // f64: no wave runs two subtrees. Merged f64 plans of the MJCF humanoid (two
   // and three waves) gave NaN or launch-varying results from launches of many
@@ -427,7 +437,7 @@ Plan plan_partition(const ModelD& m, const Features& f) {
   // lane-per-world kernel; their kernels spill several hundred bytes per lane.
   // The unmerged plan (one subtree per wave) is taken instead when it has a
   // wave count the planner uses, else one lane per world.
-  if (f.f64 && parts.size() < unmerged.size()) {
+  if (f.f64 && parts.size() < unmerged.size() && !lift_guards) {
     if (unmerged.size() == 2 || unmerged.size() == 4 || (unmerged.size() > 4 && unmerged.size() <= 8)) {
       parts = unmerged;
     } else {
@@ -1696,6 +1706,7 @@ int phz_sim_create(const double* body_table, uint32_t nb, uint32_t nq, uint32_t 
     s->feat.wgs = s->stride / 64;
     s->feat.cus = std::max(cus, 1);
     s->feat.f64 = s->f64;
+    s->feat.host_only = device_ordinal < 0;
   }
   *out = s.release();
   return 0;

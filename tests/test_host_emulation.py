@@ -1,0 +1,121 @@
+"""The step kernel's generated source, run on the CPU by the workgroup
+emulation of tests/host_emulation.py, for the plans whose device builds gave
+wrong or launch-varying results (the planner refuses them on a device):
+
+  - the MJCF humanoid in f64 with control noise, subtrees merged into two
+    waves (on gfx950: every world NaN within a 50-step launch) and into three
+    (values of order 1e67 from the first step);
+  - the MJCF hand in f64 merged into two waves (one world's NaN bits changed
+    between repeats);
+  - the f64 terrain + impulse ant under the finite-math flags (qdd wrong by
+    1e5 on gfx950, so that kernel is built IEEE).
+
+On the host each runs the same source 50 steps (the impulse case one step
+from a settled contact state) under AddressSanitizer and
+UndefinedBehaviorSanitizer with every automatic variable and every LDS slot
+initialised to NaN and the FP traps armed, under ThreadSanitizer (the waves'
+LDS exchange as a multi-threaded protocol), and at -O3 under the device
+kernels' finite-math flags; each must match the f64 oracle. They do, to
+1e-14: the source holds no out-of-bounds access, read before write, data
+race or finite-math violation that these tools see, so the device failures
+lie in how the source is compiled for gfx950 or run there, and the plans stay
+refused on the device.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle.oracle import Oracle
+from phyz_amd import workloads as W
+from phyz_amd.model import pack_geometries, uniform_frequency_gains
+from phyz_amd.sim import BatchSim, from_workload
+from tests import host_emulation as HE
+from tests.helpers import oracle_for
+
+pytestmark = pytest.mark.skipif(not os.path.exists(HE.CLANG), reason="clang++ (ROCm LLVM) not present")
+
+NOISE = (0xA55, 1, -0.03, 0.03)  # as tests/test_gpu_mjcf.py
+
+
+def mjcf_case(name, groups, prec="f64", n=64):
+    m = W.mjcf_model(name)
+    gains = uniform_frequency_gains(m, 50.0, 1.0)
+    geom, _ = pack_geometries(m, gains=gains)
+    os.environ["PHZ_HOST_LIFT_GUARDS"] = "1"
+    os.environ["PHZ_MAX_GROUPS"] = str(groups)
+    try:
+        s = BatchSim(m, n, prec, device=-1)
+        s.enable_ground_contact_per_body(0.0, 1.0, gains)
+        s.enable_control_noise(*NOISE, list(range(m.nctrl())))
+        src = HE.dump_source(s)
+        block = s.kernel_info()["block"]
+    finally:
+        os.environ.pop("PHZ_HOST_LIFT_GUARDS", None)
+        os.environ.pop("PHZ_MAX_GROUPS", None)
+    orc = Oracle(m, contact=(geom, 0.0, 1.0), noise=(*NOISE, list(range(m.nctrl()))))
+    rng = np.random.default_rng(13)
+    q = np.zeros((n, m.nq))
+    v = rng.normal(size=(n, m.nv)) * 0.1
+    for i, b in enumerate(m.bodies):
+        j, o = b.joint, m.q_offsets[i]
+        if j.ndof() == 1:
+            lo, hi = j.limits if j.limits is not None else (-1.0, 1.0)
+            q[:, o] = rng.uniform(lo + 0.05, hi - 0.05, size=n)
+        elif j.ndof() == 6:
+            q[:, o:o + 3] = rng.normal(size=(n, 3)) * 0.2
+            q[:, o + 3:o + 6] = rng.normal(size=(n, 3)) * 0.05
+    c = rng.uniform(-0.05, 0.05, size=(n, m.nctrl()))
+    return m, src, block, orc, q, v, c
+
+
+def finite_rows(q, v):
+    return np.isfinite(q).all(axis=1) & np.isfinite(v).all(axis=1) & (np.abs(v).max(axis=1) < 1e4)
+
+
+@pytest.mark.parametrize("name,groups,mode", [
+    ("humanoid", 2, "asan"), ("humanoid", 2, "tsan"), ("humanoid", 2, "finite"),
+    ("humanoid", 3, "asan"), ("humanoid", 3, "finite"),
+    ("shadow_hand", 2, "asan"), ("shadow_hand", 2, "tsan"),
+])
+def test_refused_f64_plans_are_correct_on_the_host(name, groups, mode):
+    n, steps = 64, 50
+    m, src, block, orc, q, v, c = mjcf_case(name, groups)
+    assert block == 64 * groups  # the guarded plan itself, subtrees merged
+    exe = HE.build(src, "f64", mode)
+    # The hand's explicit limit law lets a few worlds run away in the oracle
+    # too, legitimately producing inf and NaN: traps only where none do.
+    trap = mode == "asan" and name == "humanoid"
+    qe, ve, _, re, err = HE.run(exe, "f64", groups, q, v, c, orc.rng_states(n), steps, nb=m.nbodies, trap=trap)
+    assert "WARNING: ThreadSanitizer" not in err and "runtime error" not in err, err[-3000:]
+    qo, vo, co = q.copy(), v.copy(), c.copy()
+    rng = orc.rng_states(n)
+    orc.step_batch(qo, vo, co, steps, rng=rng, threads=8)
+    fo, fe = finite_rows(qo, vo), finite_rows(qe, ve)
+    assert np.array_equal(fo, fe) and fo.mean() >= 0.9
+    assert np.array_equal(re[fo], rng[fo])  # the control stream advanced exactly as the oracle's
+    assert np.abs(qe[fo] - qo[fo]).max() <= 1e-12
+    assert np.abs(ve[fo] - vo[fo]).max() <= 1e-12 * max(1.0, np.abs(vo[fo]).max())
+
+
+@pytest.mark.parametrize("mode", ["asan", "finite"])
+def test_f64_impulse_terrain_kernel_is_correct_on_the_host(mode):
+    w = W.config(6)
+    n = 64
+    s = from_workload(w, "f64", nworld=n, device=-1)
+    src = HE.dump_source(s)
+    q, v, c, _ = w.initial_state(n)
+    orc = oracle_for(w)
+    nb = w.model.nbodies
+    e0, s0 = np.zeros((n, nb, 6)), np.zeros((n, nb, 56))
+    orc.step_batch(q, v, c, 300, rng=orc.rng_states(n), threads=8, ext_state=e0, cs_state=s0)  # feet on the terrain
+    exe = HE.build(src, "f64", mode)
+    qe, ve, qdde, _, err = HE.run(exe, "f64", 1, q, v, c, orc.rng_states(n), 1, nb=nb, trap=mode == "asan",
+                                  heightfield=w.heightfield)
+    assert "runtime error" not in err, err[-3000:]
+    e1, s1 = np.zeros((n, nb, 6)), np.zeros((n, nb, 56))
+    want, rows = orc.step_batch(q.copy(), v.copy(), c.copy(), 1, rng=orc.rng_states(n), threads=8, ext_state=e1,
+                                cs_state=s1, want_contacts=True)
+    assert (rows[:, :, 0] > 0).any()  # contacts active in the compared step
+    rel = np.abs(qdde - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-12)
+    assert rel.max() <= 1e-12
