@@ -88,9 +88,10 @@ __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
 // through u^7 (through r^16); the truncations stay below 1e-19 and 3e-18 of
 // the value on |r| <= pi/4. P and Q are evaluated in Estrin's form (pairs,
 // then u^2, then u^4), about half the dependent chain of Horner's form.
-// Used for the Box-Muller angle (in an IEEE build of the chain kernel the
-// library sincos gave one of those sines a sign that varied from launch to
-// launch, its optimised IR correct) and for every f64 joint angle.
+// Used for the f64 quaternion exponential of a free joint (in an IEEE build
+// of the chain kernel the library sincos gave a Box-Muller sine a sign that
+// varied from launch to launch, its optimised IR correct; the revolute
+// angles and the Box-Muller angle now take tab_sincos below).
 __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
   constexpr double M = 6755399441055744.0;  // 1.5 * 2^52
   const double t = fma(x, 0x1.45f306dc9c883p-1, M);
@@ -120,6 +121,103 @@ __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
   const unsigned long long cs = (unsigned long long)((n + 1u) & 2u) << 62;
   *s = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? cr : sr) ^ ss);
   *c = __builtin_bit_cast(double, __builtin_bit_cast(unsigned long long, odd ? sr : cr) ^ cs);
+}
+// sin and cos of an f64 angle from a table in LDS (the f64 kernels' revolute
+// joint angles and Box-Muller angles): x = 2 pi k / 64
+// + r with k = rint(64 x / 2 pi) and r reduced by a two-part 2 pi / 64 (the
+// high part has 25 significant bits, so k times it is exact for |k| < 2^28);
+// sin x = s_k cos r + c_k sin r, cos x = c_k cos r - s_k sin r with (c_k, s_k)
+// the table's exactly rounded cosine and sine of 2 pi k / 64, and on
+// |r| <= pi/64 the Taylor series of sin r through r^7 and of cos r through
+// r^8 (truncation below 4.5e-18 and 2.5e-20). Within about 2 ulp, in about 19
+// VALU instructions, one LDS read and ten constants, against about 30
+// instructions and twenty constants for angle_sincos. At k = 0 the table
+// entry is (1, 0) exactly, so a small angle keeps its relative accuracy.
+// The kernel fills the table once per launch (fill_sincos_table) before any
+// use.
+__shared__ __attribute__((aligned(16))) double phz_sc_tab[128];
+__device__ __forceinline__ void fill_sincos_table(int lane) {
+  static constexpr double k[128] = {
+    0x1.0000000000000p+0, 0x0.0p+0,
+    0x1.fd88da3d12526p-1, 0x1.917a6bc29b42cp-4,
+    0x1.f6297cff75cb0p-1, 0x1.8f8b83c69a60bp-3,
+    0x1.e9f4156c62ddap-1, 0x1.294062ed59f06p-2,
+    0x1.d906bcf328d46p-1, 0x1.87de2a6aea963p-2,
+    0x1.c38b2f180bdb1p-1, 0x1.e2b5d3806f63bp-2,
+    0x1.a9b66290ea1a3p-1, 0x1.1c73b39ae68c8p-1,
+    0x1.8bc806b151741p-1, 0x1.44cf325091dd6p-1,
+    0x1.6a09e667f3bcdp-1, 0x1.6a09e667f3bcdp-1,
+    0x1.44cf325091dd6p-1, 0x1.8bc806b151741p-1,
+    0x1.1c73b39ae68c8p-1, 0x1.a9b66290ea1a3p-1,
+    0x1.e2b5d3806f63bp-2, 0x1.c38b2f180bdb1p-1,
+    0x1.87de2a6aea963p-2, 0x1.d906bcf328d46p-1,
+    0x1.294062ed59f06p-2, 0x1.e9f4156c62ddap-1,
+    0x1.8f8b83c69a60bp-3, 0x1.f6297cff75cb0p-1,
+    0x1.917a6bc29b42cp-4, 0x1.fd88da3d12526p-1,
+    0.0, 0x1.0000000000000p+0,
+    -0x1.917a6bc29b42cp-4, 0x1.fd88da3d12526p-1,
+    -0x1.8f8b83c69a60bp-3, 0x1.f6297cff75cb0p-1,
+    -0x1.294062ed59f06p-2, 0x1.e9f4156c62ddap-1,
+    -0x1.87de2a6aea963p-2, 0x1.d906bcf328d46p-1,
+    -0x1.e2b5d3806f63bp-2, 0x1.c38b2f180bdb1p-1,
+    -0x1.1c73b39ae68c8p-1, 0x1.a9b66290ea1a3p-1,
+    -0x1.44cf325091dd6p-1, 0x1.8bc806b151741p-1,
+    -0x1.6a09e667f3bcdp-1, 0x1.6a09e667f3bcdp-1,
+    -0x1.8bc806b151741p-1, 0x1.44cf325091dd6p-1,
+    -0x1.a9b66290ea1a3p-1, 0x1.1c73b39ae68c8p-1,
+    -0x1.c38b2f180bdb1p-1, 0x1.e2b5d3806f63bp-2,
+    -0x1.d906bcf328d46p-1, 0x1.87de2a6aea963p-2,
+    -0x1.e9f4156c62ddap-1, 0x1.294062ed59f06p-2,
+    -0x1.f6297cff75cb0p-1, 0x1.8f8b83c69a60bp-3,
+    -0x1.fd88da3d12526p-1, 0x1.917a6bc29b42cp-4,
+    -0x1.0000000000000p+0, 0.0,
+    -0x1.fd88da3d12526p-1, -0x1.917a6bc29b42cp-4,
+    -0x1.f6297cff75cb0p-1, -0x1.8f8b83c69a60bp-3,
+    -0x1.e9f4156c62ddap-1, -0x1.294062ed59f06p-2,
+    -0x1.d906bcf328d46p-1, -0x1.87de2a6aea963p-2,
+    -0x1.c38b2f180bdb1p-1, -0x1.e2b5d3806f63bp-2,
+    -0x1.a9b66290ea1a3p-1, -0x1.1c73b39ae68c8p-1,
+    -0x1.8bc806b151741p-1, -0x1.44cf325091dd6p-1,
+    -0x1.6a09e667f3bcdp-1, -0x1.6a09e667f3bcdp-1,
+    -0x1.44cf325091dd6p-1, -0x1.8bc806b151741p-1,
+    -0x1.1c73b39ae68c8p-1, -0x1.a9b66290ea1a3p-1,
+    -0x1.e2b5d3806f63bp-2, -0x1.c38b2f180bdb1p-1,
+    -0x1.87de2a6aea963p-2, -0x1.d906bcf328d46p-1,
+    -0x1.294062ed59f06p-2, -0x1.e9f4156c62ddap-1,
+    -0x1.8f8b83c69a60bp-3, -0x1.f6297cff75cb0p-1,
+    -0x1.917a6bc29b42cp-4, -0x1.fd88da3d12526p-1,
+    0.0, -0x1.0000000000000p+0,
+    0x1.917a6bc29b42cp-4, -0x1.fd88da3d12526p-1,
+    0x1.8f8b83c69a60bp-3, -0x1.f6297cff75cb0p-1,
+    0x1.294062ed59f06p-2, -0x1.e9f4156c62ddap-1,
+    0x1.87de2a6aea963p-2, -0x1.d906bcf328d46p-1,
+    0x1.e2b5d3806f63bp-2, -0x1.c38b2f180bdb1p-1,
+    0x1.1c73b39ae68c8p-1, -0x1.a9b66290ea1a3p-1,
+    0x1.44cf325091dd6p-1, -0x1.8bc806b151741p-1,
+    0x1.6a09e667f3bcdp-1, -0x1.6a09e667f3bcdp-1,
+    0x1.8bc806b151741p-1, -0x1.44cf325091dd6p-1,
+    0x1.a9b66290ea1a3p-1, -0x1.1c73b39ae68c8p-1,
+    0x1.c38b2f180bdb1p-1, -0x1.e2b5d3806f63bp-2,
+    0x1.d906bcf328d46p-1, -0x1.87de2a6aea963p-2,
+    0x1.e9f4156c62ddap-1, -0x1.294062ed59f06p-2,
+    0x1.f6297cff75cb0p-1, -0x1.8f8b83c69a60bp-3,
+    0x1.fd88da3d12526p-1, -0x1.917a6bc29b42cp-4};
+  phz_sc_tab[lane] = k[lane];
+  phz_sc_tab[64 + lane] = k[64 + lane];
+}
+__device__ __forceinline__ void tab_sincos(double x, double* s, double* c) {
+  const double t = x * 0x1.45f306dc9c883p+3;  // 64 / 2 pi
+  const double k = rint(t);
+  const double r = fma(-k, 0x1.110b4611a6263p-30, fma(-k, 0x1.921fb50000000p-4, x));
+  const int i = cvt_sat_i32(k) & 63;  // a diverged world's NaN reads entry 0
+  const double ck = phz_sc_tab[2 * i], sk = phz_sc_tab[2 * i + 1];
+  const double r2 = r * r;
+  const double ps = fma(r2, fma(r2, -1.0 / 5040.0, 1.0 / 120.0), -1.0 / 6.0);
+  const double sr = fma(r * r2, ps, r);
+  const double qc = fma(r2, fma(r2, fma(r2, 1.0 / 40320.0, -1.0 / 720.0), 1.0 / 24.0), -0.5);
+  const double cr = fma(r2, qc, 1.0);
+  *s = fma(sk, cr, ck * sr);
+  *c = fma(ck, cr, -(sk * sr));
 }
 // sin and cos of an f32 angle x: the reduction of the f64 angle_sincos (x is
 // exact in f64), then in f32 the Taylor series of sin r through r^9 and of
@@ -163,7 +261,7 @@ __device__ __forceinline__ void rev_sincos(float xf, float* s, float* c) {
   *s = __builtin_amdgcn_sinf(x);
   *c = __builtin_amdgcn_cosf(x);
 }
-__device__ __forceinline__ void rev_sincos(double x, double* s, double* c) { angle_sincos(x, s, c); }
+__device__ __forceinline__ void rev_sincos(double x, double* s, double* c) { tab_sincos(x, s, c); }
 // ln x for x in [2^-53, 1] (1 - u of the f64 Box-Muller radius), within
 // about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from the hardware
 // frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) / (m + 1),
@@ -211,7 +309,7 @@ __device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
   *c = __builtin_amdgcn_cosf(u);
 }
 __device__ __forceinline__ void turn_sincos(double u, double* s, double* c) {
-  angle_sincos(6.283185307179586 * u, s, c);
+  tab_sincos(6.283185307179586 * u, s, c);
 }
 // sin and cos of a joint angle in f64 for the f32 kernels' penetration chain:
 // the reduction of angle_sincos (exact for |x| < 1.6e6), Taylor series through
@@ -2222,6 +2320,11 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
 // loads the DOFs it owns and the trunk's; it stores only the DOFs it owns
 // (group 0 also stores the trunk's and the RNG state).
 template <class M, class T, int G> __device__ __forceinline__ void run_group(const StepArgs& a, int lane, T* lds) {
+  if constexpr (sizeof(T) == 8) {
+    // The f64 sine / cosine table, before any lane of the workgroup returns.
+    if constexpr (G == 0) fill_sincos_table(lane);
+    __syncthreads();
+  }
   // Split-lane kernels give each world LANES consecutive lanes.
   const int w = (int)(blockIdx.x * 64 + lane) / M::LANES;
   const bool live = w < a.nworld;

@@ -12,7 +12,10 @@ waves as G host threads:
     its own column, lds[slot * 64 + lane]);
   - __syncthreads() is a pthread barrier over the G threads;
   - the workgroup's LDS is one heap array of exactly the kernel's size, so
-    AddressSanitizer bounds every slot access;
+    AddressSanitizer bounds every slot access (the f64 sine table, a
+    namespace-scope __shared__ array that wave 0 fills before a barrier, one
+    entry pair per lane, is a plain global that the emulated lane fills
+    whole);
   - the AMDGPU builtins become their host meanings (v_sin_f32 / v_cos_f32
     take turns, v_rcp / v_rsq are reciprocals, v_cvt_i32 saturates and maps
     NaN to 0).
@@ -50,6 +53,7 @@ PRELUDE = r"""
 #define __global__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
+#define __shared__
 struct EmuDim3 { unsigned x = 0, y = 0, z = 0; };
 thread_local EmuDim3 threadIdx, blockIdx;
 extern "C" void emu_syncthreads();
@@ -177,17 +181,25 @@ FLAGS = {
 }
 
 
-def host_source(device_src: str, prec: str) -> str:
-    """The generated kernel source, rewritten for the host."""
-    s = device_src
+def host_device_code(s: str) -> str:
+    """Device source with its AMDGPU builtins and inline asm given host meanings."""
     s = s.replace("#pragma once", "")
     s = s.replace("__builtin_amdgcn_", "emu_amdgcn_")
     s = s.replace('asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));', "r = emu_cvt_sat(x);")
     s = s.replace('asm("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(x));', "r = emu_cvt_sat(x);")
-    s = s.replace('"+s"', '"+r"').replace('"+v"', '"+x"')
+    return s.replace('"+s"', '"+r"').replace('"+v"', '"+x"')
+
+
+def host_source(device_src: str, prec: str) -> str:
+    """The generated kernel source, rewritten for the host."""
+    s = host_device_code(device_src)
     t = "double" if prec == "f64" else "float"
     s, n = re.subn(r"__shared__\s+" + t + r"\s+lds\[[^;]*\];", f"{t}* lds = ({t}*)emu_lds_base;", s)
     assert n == 1, "the kernel's LDS declaration was not found"
+    # One emulated lane at a time: the filling lane writes the whole table.
+    fill = "phz_sc_tab[lane] = k[lane];\n  phz_sc_tab[64 + lane] = k[64 + lane];"
+    assert fill in s, "the f64 sine table's fill was not found"
+    s = s.replace(fill, "for (int e = 0; e < 128; e++) phz_sc_tab[e] = k[e];")
     assert "asm(" not in s, "an unhandled inline asm block is left in the source"
     return PRELUDE + s + "\n#define EMU_T " + t + "\n" + DRIVER
 

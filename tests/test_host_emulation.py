@@ -119,3 +119,69 @@ def test_f64_impulse_terrain_kernel_is_correct_on_the_host(mode):
     assert (rows[:, :, 0] > 0).any()  # contacts active in the compared step
     rel = np.abs(qdde - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-12)
     assert rel.max() <= 1e-12
+
+
+def test_f64_table_sincos_accuracy():
+    """tab_sincos, the f64 kernels' sine and cosine of a revolute joint angle
+    and of the Box-Muller angle, compiled from the device header for the host,
+    against mpmath at 40 digits: within 2 ulp on joint-angle ranges (4 ulp up
+    to |x| = 3e6, where the reduction's two-part 2 pi / 64 loses a little),
+    exact where the angle is below pi / 128 (the sine is then r itself), and
+    at the table's own nodes and the midpoints between them."""
+    import subprocess
+
+    import mpmath
+    hdr = open(os.path.join(os.path.dirname(HE.HERE), "phyz_amd", "csrc", "phz_device.h")).read()
+    main = r'''
+#include <cstdio>
+#include <vector>
+void* emu_lds_base = nullptr;
+extern "C" void emu_syncthreads() {}
+int main(int argc, char** argv) {
+  for (int lane = 0; lane < 64; lane++) phz::fill_sincos_table(lane);
+  FILE* f = fopen(argv[1], "rb");
+  long n = 0;
+  if (fread(&n, 8, 1, f) != 1) return 3;
+  std::vector<double> x(n), o(2 * n);
+  if (fread(x.data(), 8, n, f) != (size_t)n) return 3;
+  fclose(f);
+  for (long i = 0; i < n; i++) phz::tab_sincos(x[i], &o[2 * i], &o[2 * i + 1]);
+  f = fopen(argv[2], "wb");
+  fwrite(o.data(), 8, 2 * n, f);
+  fclose(f);
+  return 0;
+}
+'''
+    os.makedirs(HE.CACHE, exist_ok=True)
+    cpp, exe = os.path.join(HE.CACHE, "tab_sincos.cpp"), os.path.join(HE.CACHE, f"tab_sincos_{os.getpid()}")
+    with open(cpp, "w") as f:
+        f.write(HE.PRELUDE + HE.host_device_code(hdr) + main)
+    r = subprocess.run([HE.CLANG, "-x", "c++", "-std=c++17", "-O2", "-ffp-contract=off", cpp, "-o", exe],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    rng = np.random.default_rng(1)
+    nodes = np.arange(-320, 321) * (2 * np.pi / 64)
+    near = np.concatenate([rng.uniform(-60, 60, 3000), nodes, np.nextafter(nodes, np.inf),
+                           np.nextafter(nodes, -np.inf), nodes + np.pi / 64, [np.pi, -np.pi, np.pi / 2, 2 * np.pi]])
+    tiny = np.concatenate([np.logspace(-300, np.log10(np.pi / 128) - 1e-9, 300), [0.0]])
+    tiny = np.concatenate([tiny, -tiny])
+    far = rng.uniform(-3e6, 3e6, 500)
+    xs = np.concatenate([near, tiny, far])
+    fin, fout = exe + ".in", exe + ".out"
+    with open(fin, "wb") as f:
+        np.array([len(xs)], np.int64).tofile(f)
+        xs.tofile(f)
+    try:
+        subprocess.run([exe, fin, fout], check=True)
+        o = np.fromfile(fout).reshape(-1, 2)
+    finally:
+        for p in (exe, fin, fout):
+            if os.path.exists(p):
+                os.remove(p)
+    mpmath.mp.dps = 40
+    ref = np.array([[float(mpmath.sin(mpmath.mpf(x))), float(mpmath.cos(mpmath.mpf(x)))] for x in xs])
+    err, ulp = np.abs(o - ref), np.spacing(np.abs(ref))
+    a, b = len(near), len(near) + len(tiny)
+    assert (err[:a] <= 2 * ulp[:a] + 2.0 ** -60).all()
+    assert (err[a:b, 0] == 0).all() and (err[a:b, 1] <= ulp[a:b, 1]).all()
+    assert (err[b:] <= 4 * ulp[b:] + 2.0 ** -60).all()
