@@ -133,10 +133,77 @@ __device__ __forceinline__ void angle_sincos(double x, double* s, double* c) {
 // VALU instructions, one LDS read and ten constants, against about 30
 // instructions and twenty constants for angle_sincos. At k = 0 the table
 // entry is (1, 0) exactly, so a small angle keeps its relative accuracy.
-// The kernel fills the table once per launch (fill_sincos_table) before any
-// use.
+// The kernel fills the table once per launch (fill_tables) before any use.
 __shared__ __attribute__((aligned(16))) double phz_sc_tab[128];
-__device__ __forceinline__ void fill_sincos_table(int lane) {
+// The table of tab_log below: (invc, logc) for each of its 64 intervals.
+__shared__ __attribute__((aligned(16))) double phz_log_tab[128];
+// Both tables, entry pair `lane` of each, from the 64 lanes of one wave.
+__device__ __forceinline__ void fill_tables(int lane) {
+  static constexpr double lg[128] = {
+    0x1.702e05c0b8170p+0, -0x1.741d876c67bb1p-2,
+    0x1.6c16c16c16c17p+0, -0x1.68ac83e9c6a15p-2,
+    0x1.6816816816817p+0, -0x1.5d5bddf595f31p-2,
+    0x1.642c8590b2164p+0, -0x1.522ae0738a3d7p-2,
+    0x1.6058160581606p+0, -0x1.4718dc271c41cp-2,
+    0x1.5c9882b931057p+0, -0x1.3c25277333183p-2,
+    0x1.58ed2308158edp+0, -0x1.314f1e1d35ce3p-2,
+    0x1.5555555555555p+0, -0x1.269621134db91p-2,
+    0x1.51d07eae2f815p+0, -0x1.1bf99635a6b95p-2,
+    0x1.4e5e0a72f0539p+0, -0x1.1178e8227e47ap-2,
+    0x1.4afd6a052bf5bp+0, -0x1.07138604d5864p-2,
+    0x1.47ae147ae147bp+0, -0x1.f991c6cb3b37ap-3,
+    0x1.446f86562d9fbp+0, -0x1.e530effe71013p-3,
+    0x1.4141414141414p+0, -0x1.d1037f2655e7bp-3,
+    0x1.3e22cbce4a902p+0, -0x1.bd087383bd8aap-3,
+    0x1.3b13b13b13b14p+0, -0x1.a93ed3c8ad9e5p-3,
+    0x1.3813813813814p+0, -0x1.95a5adcf70182p-3,
+    0x1.3521cfb2b78c1p+0, -0x1.823c16551a3c0p-3,
+    0x1.323e34a2b10bfp+0, -0x1.6f0128b756ab9p-3,
+    0x1.2f684bda12f68p+0, -0x1.5bf406b543db0p-3,
+    0x1.2c9fb4d812ca0p+0, -0x1.4913d8333b563p-3,
+    0x1.29e4129e4129ep+0, -0x1.365fcb0159014p-3,
+    0x1.27350b8812735p+0, -0x1.23d712a49c201p-3,
+    0x1.2492492492492p+0, -0x1.1178e8227e47ap-3,
+    0x1.21fb78121fb78p+0, -0x1.fe89139dbd565p-4,
+    0x1.1f7047dc11f70p+0, -0x1.da7276384469ep-4,
+    0x1.1cf06ada2811dp+0, -0x1.b6ac88dad5b1dp-4,
+    0x1.1a7b9611a7b96p+0, -0x1.9335e5d594988p-4,
+    0x1.1811811811812p+0, -0x1.700d30aeac0e8p-4,
+    0x1.15b1e5f75270dp+0, -0x1.4d3115d207eacp-4,
+    0x1.135c81135c811p+0, -0x1.2aa04a44717a1p-4,
+    0x1.1111111111111p+0, -0x1.08598b59e3a06p-4,
+    0x1.0ecf56be69c90p+0, -0x1.ccb73cdddb2d0p-5,
+    0x1.0c9714fbcda3bp+0, -0x1.894aa149fb34bp-5,
+    0x1.0a6810a6810a7p+0, -0x1.466aed42de3f9p-5,
+    0x1.0842108421084p+0, -0x1.0415d89e74440p-5,
+    0x1.0624dd2f1a9fcp+0, -0x1.8492528c8cac5p-6,
+    0x1.0410410410410p+0, -0x1.0205658935837p-6,
+    0x1.0204081020408p+0, -0x1.010157588de69p-7,
+    0x1.0000000000000p+0, 0x0.0p+0,
+    0x1.f81f81f81f820p-1, 0x1.fc0a8b0fc03c4p-7,
+    0x1.f07c1f07c1f08p-1, 0x1.f829b0e7832f8p-6,
+    0x1.e9131abf0b767p-1, 0x1.77458f632dcffp-5,
+    0x1.e1e1e1e1e1e1ep-1, 0x1.f0a30c01162a8p-5,
+    0x1.dae6076b981dbp-1, 0x1.341d7961bd1d0p-4,
+    0x1.d41d41d41d41dp-1, 0x1.6f0d28ae56b4ep-4,
+    0x1.cd85689039b0bp-1, 0x1.a926d3a4ad562p-4,
+    0x1.c71c71c71c71cp-1, 0x1.e27076e2af2eap-4,
+    0x1.c0e070381c0e0p-1, 0x1.0d77e7cd08e5bp-3,
+    0x1.bacf914c1bad0p-1, 0x1.29552f81ff521p-3,
+    0x1.b4e81b4e81b4fp-1, 0x1.44d2b6ccb7d1cp-3,
+    0x1.af286bca1af28p-1, 0x1.5ff3070a793d6p-3,
+    0x1.a98ef606a63bep-1, 0x1.7ab890210d907p-3,
+    0x1.a41a41a41a41ap-1, 0x1.9525a9cf456b6p-3,
+    0x1.9ec8e951033d9p-1, 0x1.af3c94e80bff3p-3,
+    0x1.999999999999ap-1, 0x1.c8ff7c79a9a20p-3,
+    0x1.948b0fcd6e9e0p-1, 0x1.e27076e2af2e8p-3,
+    0x1.8f9c18f9c18fap-1, 0x1.fb9186d5e3e29p-3,
+    0x1.8acb90f6bf3aap-1, 0x1.0a324e27390e2p-2,
+    0x1.8618618618618p-1, 0x1.1675cababa60fp-2,
+    0x1.8181818181818p-1, 0x1.22941fbcf7966p-2,
+    0x1.7d05f417d05f4p-1, 0x1.2e8e2bae11d31p-2,
+    0x1.78a4c8178a4c8p-1, 0x1.3a64c556945eap-2,
+    0x1.745d1745d1746p-1, 0x1.4618bc21c5ec2p-2};
   static constexpr double k[128] = {
     0x1.0000000000000p+0, 0x0.0p+0,
     0x1.fd88da3d12526p-1, 0x1.917a6bc29b42cp-4,
@@ -204,12 +271,10 @@ __device__ __forceinline__ void fill_sincos_table(int lane) {
     0x1.fd88da3d12526p-1, -0x1.917a6bc29b42cp-4};
   phz_sc_tab[lane] = k[lane];
   phz_sc_tab[64 + lane] = k[64 + lane];
+  phz_log_tab[lane] = lg[lane];
+  phz_log_tab[64 + lane] = lg[64 + lane];
 }
-__device__ __forceinline__ void tab_sincos(double x, double* s, double* c) {
-  const double t = x * 0x1.45f306dc9c883p+3;  // 64 / 2 pi
-  const double k = rint(t);
-  const double r = fma(-k, 0x1.110b4611a6263p-30, fma(-k, 0x1.921fb50000000p-4, x));
-  const int i = cvt_sat_i32(k) & 63;  // a diverged world's NaN reads entry 0
+__device__ __forceinline__ void tab_sincos_at(double r, int i, double* s, double* c) {
   const double ck = phz_sc_tab[2 * i], sk = phz_sc_tab[2 * i + 1];
   const double r2 = r * r;
   const double ps = fma(r2, fma(r2, -1.0 / 5040.0, 1.0 / 120.0), -1.0 / 6.0);
@@ -218,6 +283,12 @@ __device__ __forceinline__ void tab_sincos(double x, double* s, double* c) {
   const double cr = fma(r2, qc, 1.0);
   *s = fma(sk, cr, ck * sr);
   *c = fma(ck, cr, -(sk * sr));
+}
+__device__ __forceinline__ void tab_sincos(double x, double* s, double* c) {
+  const double t = x * 0x1.45f306dc9c883p+3;  // 64 / 2 pi
+  const double k = rint(t);
+  const double r = fma(-k, 0x1.110b4611a6263p-30, fma(-k, 0x1.921fb50000000p-4, x));
+  tab_sincos_at(r, cvt_sat_i32(k) & 63, s, c);  // a diverged world's NaN reads entry 0
 }
 // sin and cos of an f32 angle x: the reduction of the f64 angle_sincos (x is
 // exact in f64), then in f32 the Taylor series of sin r through r^9 and of
@@ -262,13 +333,14 @@ __device__ __forceinline__ void rev_sincos(float xf, float* s, float* c) {
   *c = __builtin_amdgcn_cosf(x);
 }
 __device__ __forceinline__ void rev_sincos(double x, double* s, double* c) { tab_sincos(x, s, c); }
-// ln x for x in [2^-53, 1] (1 - u of the f64 Box-Muller radius), within
-// about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from the hardware
-// frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) / (m + 1),
-// |s| <= 0.1716, z = s^2, and P(z) = sum_j z^j / (2j + 3) through z^8 (the
-// first omitted term is below 3e-17 of ln m), in Estrin's form; 1 / (m + 1)
-// is the hardware reciprocal refined by two Newton steps; ln 2 is split so
-// that e * ln2_hi is exact. About a third of the library log's instructions.
+// ln x for a normal x in (0, 1] (the policy kernel's Box-Muller ln u1, u1 >=
+// 1e-300), within about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from
+// the hardware frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) /
+// (m + 1), |s| <= 0.1716, z = s^2, and P(z) = sum_j z^j / (2j + 3) through
+// z^8 (the first omitted term is below 3e-17 of ln m), in Estrin's form;
+// 1 / (m + 1) is the hardware reciprocal refined by two Newton steps; ln 2 is
+// split so that e * ln2_hi is exact. About a third of the library log's
+// instructions.
 __device__ __forceinline__ double bm_log(double x) {
   double m = __builtin_amdgcn_frexp_mant(x);  // [0.5, 1)
   int e = __builtin_amdgcn_frexp_exp(x);
@@ -292,24 +364,66 @@ __device__ __forceinline__ double bm_log(double x) {
   const double fe = (double)e;
   return fma(fe, 0x1.62e42fefa3800p-1, fma(fe, 0x1.ef35793c76730p-45, lnm));
 }
-// The Box-Muller radius sqrt(-2 ln(1 - u)) of a uniform u in [0, 1). f32: the
+// ln x for a normal x > 0 from the LDS table phz_log_tab (Tang's method),
+// within about 1 ulp: the step kernels' f64 Box-Muller ln(1 - u). From x's
+// high word h by integer arithmetic alone: t = h - 0x3FE62000, k = t >> 20
+// (arithmetic) and z = x / 2^k, so that z lies in [OFF, 2 OFF), OFF =
+// 0x1.62p-1 (about 0.691); bits 14..19 of t pick one of 64 intervals of z,
+// 2^-7 wide below 1 and 2^-6 above. The table holds for each interval invc,
+// the double nearest 1 / (its midpoint), and logc, the double nearest
+// -ln invc; the interval around 1, [1 - 2^-8, 1 + 2^-7), has invc = 1 and
+// logc = 0 exactly, so that x near 1 keeps its relative accuracy. Then
+// r = z invc - 1 by one fma (|r| <= 2^-7, rounded once), ln x = k ln2 + logc
+// + log1p r, log1p r through r^8 in Estrin's form (truncation below 2^-59
+// of r). About 20 VALU instructions and one LDS read, against about 33 for
+// bm_log.
+__device__ __forceinline__ double tab_log(double x) {
+  const u64 b = __builtin_bit_cast(u64, x);
+  const unsigned h = (unsigned)(b >> 32);
+  const int t = (int)(h - 0x3FE62000u);
+  const int k = t >> 20;
+  const int i = (t >> 14) & 63;
+  const unsigned zh = h - ((unsigned)t & 0xFFF00000u);
+  const double z = __builtin_bit_cast(double, ((u64)zh << 32) | (b & 0xFFFFFFFFull));
+  const double invc = phz_log_tab[2 * i], logc = phz_log_tab[2 * i + 1];
+  const double r = fma(z, invc, -1.0);
+  const double r2 = r * r;
+  const double r4 = r2 * r2;
+  const double a = fma(r, 1.0 / 3.0, -0.5);
+  const double bq = fma(r, 1.0 / 5.0, -0.25);
+  const double c = fma(r2, -0.125, fma(r, 1.0 / 7.0, -1.0 / 6.0));
+  const double p = fma(r2, fma(r4, c, fma(r2, bq, a)), r);
+  const double fk = (double)k;
+  return fma(fk, 0x1.62e42fefa3800p-1, logc) + fma(fk, 0x1.ef35793c76730p-45, p);
+}
+// sqrt y (f64) for y = 0 or a normal y >= 2^-1000: the hardware v_rsq_f64
+// estimate of 1 / sqrt y, one Goldschmidt step for g ~ sqrt y and h ~
+// 1 / (2 sqrt y), then two corrections g += (y - g^2) h, each residual one
+// fma; correctly rounded but for rare near-ties. The library routine adds a
+// rescaling for tiny and huge y and a class test for 0 and inf; here y = 0
+// takes the estimate of 2^-1000 and comes out 0 exactly (g = 0 * a).
+__device__ __forceinline__ double nr_sqrt(double y) {
+  const double a = __builtin_amdgcn_rsq(fmax(y, 0x1p-1000));
+  double g = y * a, h = 0.5 * a;
+  const double e = fma(-g, h, 0.5);
+  g = fma(g, e, g);
+  h = fma(h, e, h);
+  g = fma(fma(-g, g, y), h, g);
+  return fma(fma(-g, g, y), h, g);
+}
+// The f32 Box-Muller radius sqrt(-2 ln(1 - u)) of a uniform u in [0, 1): the
 // hardware log2 and square root (1 - u >= 2^-24, never denormal), a few ulp
-// from the correctly rounded value, for the synthetic control stream; f64:
-// bm_log (about 2 ulp) and the correctly rounded square root, as the oracle
-// replays that stream to 1e-13.
+// from the correctly rounded value, for the synthetic control stream. The
+// f64 radius is box_muller(u64&, double*, ...) below.
 __device__ __forceinline__ float bm_radius(float u) {
   return __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(1.0f - u));
 }
-__device__ __forceinline__ double bm_radius(double u) { return sqrt(-2.0 * bm_log(1.0 - u)); }
-// sin and cos of the Box-Muller angle 2 pi u for a uniform u in [0, 1): u is
-// the angle in turns, which the hardware v_sin_f32 / v_cos_f32 take as they
-// are (1.25e-7 absolute at most, see angle_sincos(float)); f64 as angle_sincos.
+// sin and cos of the f32 Box-Muller angle 2 pi u for a uniform u in [0, 1): u
+// is the angle in turns, which the hardware v_sin_f32 / v_cos_f32 take as they
+// are (1.25e-7 absolute at most, see angle_sincos(float)).
 __device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
   *s = __builtin_amdgcn_sinf(u);
   *c = __builtin_amdgcn_cosf(u);
-}
-__device__ __forceinline__ void turn_sincos(double u, double* s, double* c) {
-  tab_sincos(6.283185307179586 * u, s, c);
 }
 // sin and cos of a joint angle in f64 for the f32 kernels' penetration chain:
 // the reduction of angle_sincos (exact for |x| < 1.6e6), Taylor series through
@@ -351,20 +465,41 @@ __device__ __forceinline__ float datan2(float y, float x) { return atan2f(y, x);
 // Reciprocal on the ABA and penalty-contact paths. f32: the hardware
 // v_rcp_f32 (within 1 ulp) in place of the correctly rounded division's
 // eleven-instruction expansion; the f32 kernels' per-step bound is 1e-4 and
-// one ulp is 6e-8. f64: the correctly rounded division. The impulse solve and
-// the heightfield cell lookup keep their correctly rounded f32 divisions.
+// one ulp is 6e-8. f64: the hardware v_rcp_f64 estimate refined by two Newton
+// steps r += r (1 - x r), within about 1 ulp for a normal x, five
+// instructions against the correctly rounded division's eleven (its scaling
+// for extreme exponents and final fixup); the f64 bound is 1e-10 per step and
+// one ulp 1.1e-16. The impulse solve and the heightfield cell lookup keep
+// their correctly rounded divisions.
 __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
-__device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
-// a / b: f32 through the hardware reciprocal (about 2 ulp), f64 correctly rounded.
+__device__ __forceinline__ double frcp(double x) {
+  double r = __builtin_amdgcn_rcp(x);
+  r = fma(fma(-x, r, 1.0), r, r);
+  return fma(fma(-x, r, 1.0), r, r);
+}
+// a / b: f32 through the hardware reciprocal (about 2 ulp); f64 q = a frcp(b)
+// and one residual correction q += (a - b q) frcp(b) (about 1 ulp).
 __device__ __forceinline__ float fdiv(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
-__device__ __forceinline__ double fdiv(double a, double b) { return a / b; }
+__device__ __forceinline__ double fdiv(double a, double b) {
+  const double r = frcp(b);
+  const double q = a * r;
+  return fma(fma(-b, q, a), r, q);
+}
 // Square root on the penalty-contact path: f32 the hardware v_sqrt_f32 (within
-// 1 ulp, no correction sequence), f64 the correctly rounded one.
+// 1 ulp, no correction sequence), f64 nr_sqrt (0 or a normal x >= 2^-1000; a
+// smaller positive x gives a result below 2^-499 rather than its root).
 __device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
-__device__ __forceinline__ double fsqrt(double x) { return sqrt(x); }
-// 1 / sqrt(x): f32 the hardware v_rsq_f32 (about 1 ulp), f64 correctly rounded steps.
+__device__ __forceinline__ double fsqrt(double x) { return nr_sqrt(x); }
+// 1 / sqrt(x): f32 the hardware v_rsq_f32 (about 1 ulp); f64 the hardware
+// v_rsq_f64 estimate refined by two Newton steps y += y (1/2 - (x/2) y^2)
+// (about 2 ulp, x normal).
 __device__ __forceinline__ float frsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
-__device__ __forceinline__ double frsqrt(double x) { return 1.0 / sqrt(x); }
+__device__ __forceinline__ double frsqrt(double x) {
+  const double h = 0.5 * x;
+  double y = __builtin_amdgcn_rsq(x);
+  y = fma(y, fma(-(h * y), y, 0.5), y);
+  return fma(y, fma(-(h * y), y, 0.5), y);
+}
 // The friction-loss argument qd / 1e-3: f32 multiplies by 1e3 (within an ulp
 // of the quotient), f64 divides as the oracle does.
 __device__ __forceinline__ float per_milli(float x) { return x * 1e3f; }
@@ -645,9 +780,36 @@ __device__ __forceinline__ u64 xorshift64(u64& s) {
   s = x;
   return x;
 }
-// Uniform on [0, 1): 53 bits on the f64 path, 24 bits on the f32 path (both exact).
-__device__ __forceinline__ double uniform01(u64& s, double) { return (double)(xorshift64(s) >> 11) * 0x1.0p-53; }
+// Uniform on [0, 1): 53 bits on the f64 path, 24 bits on the f32 path (both
+// exact). f64: (x >> 11) 2^-53 = hi 2^-32 + (lo >> 11) 2^-53 for the 32-bit
+// words hi, lo of x, one fma of two exact conversions, the sum exact.
+__device__ __forceinline__ double uniform01(u64& s, double) {
+  const u64 x = xorshift64(s);
+  return fma((double)(unsigned)(x >> 32), 0x1p-32, (double)((unsigned)x >> 11) * 0x1p-53);
+}
 __device__ __forceinline__ float uniform01(u64& s, float) { return (float)(unsigned)(xorshift64(s) >> 40) * 0x1.0p-24f; }
+// One Box-Muller pair from two uniforms u1, u2 (drawn in that order): the
+// radius sqrt(-2 ln(1 - u1)) and the sine and cosine of 2 pi u2. f64: 1 - u1
+// is formed exactly from the words of the draw (1 - (lo >> 11) 2^-53 is exact,
+// and so is the fma that takes hi 2^-32 from it), ln by tab_log, sqrt by
+// nr_sqrt; the angle is reduced in turns, where it is exact: t = 64 u2 (no
+// rounding), k = rint(t), and r = (t - k) 2 pi / 64 (t - k exact, one
+// rounding in the product), then tab_sincos_at.
+__device__ __forceinline__ void box_muller(u64& s, float* r, float* sn, float* cs) {
+  const float u1 = uniform01(s, 0.0f);
+  const float u2 = uniform01(s, 0.0f);
+  *r = bm_radius(u1);
+  turn_sincos(u2, sn, cs);
+}
+__device__ __forceinline__ void box_muller(u64& s, double* r, double* sn, double* cs) {
+  const u64 x1 = xorshift64(s);
+  const u64 x2 = xorshift64(s);
+  const double om = fma(-(double)(unsigned)(x1 >> 32), 0x1p-32, fma(-(double)((unsigned)x1 >> 11), 0x1p-53, 1.0));
+  *r = nr_sqrt(-2.0 * tab_log(om));
+  const double t = fma((double)(unsigned)(x2 >> 32), 0x1p-26, (double)((unsigned)x2 >> 11) * 0x1p-47);
+  const double k = rint(t);
+  tab_sincos_at((t - k) * 0x1.921fb54442d18p-4, cvt_sat_i32(k) & 63, sn, cs);
+}
 
 // ── kernel arguments ─────────────────────────────────────────────────────────
 // Structure-of-arrays state: element (j, w) at j * stride + w.
@@ -1850,12 +2012,9 @@ __device__ __forceinline__ void apply_controls(const T (&q)[M::NQ], const T (&v)
         constexpr int k = 2 * decltype(K)::value;
         constexpr bool mine0 = M::ctrl_owner[M::noise_dof[k]] == G;
         constexpr bool mine1 = k + 1 < M::NNOISE && M::ctrl_owner[M::noise_dof[k + 1 < M::NNOISE ? k + 1 : k]] == G;
-        T u1 = uniform01(rng, T(0));
-        T u2 = uniform01(rng, T(0));
+        T r, sn, cs;
+        box_muller(rng, &r, &sn, &cs);  // the pair's radius and angle
         if constexpr (mine0 || mine1) {
-          T r = bm_radius(u1);
-          T sn, cs;
-          turn_sincos(u2, &sn, &cs);
           if constexpr (mine0) ctrl[M::noise_dof[k]] = T(M::noise_a) + T(M::noise_b) * (r * cs);
           if constexpr (mine1) ctrl[M::noise_dof[k + 1]] = T(M::noise_a) + T(M::noise_b) * (r * sn);
         }
@@ -1888,11 +2047,8 @@ template <class M, class T> __device__ __forceinline__ void draw_shared_noise(u6
   } else {
     sfor<0, (M::NNOISE + 1) / 2>([&](auto K) {
       constexpr int k = 2 * decltype(K)::value;
-      T u1 = uniform01(rng, T(0));
-      T u2 = uniform01(rng, T(0));
-      T r = bm_radius(u1);
-      T sn, cs;
-      turn_sincos(u2, &sn, &cs);
+      T r, sn, cs;
+      box_muller(rng, &r, &sn, &cs);
       lds_put(lds, M::slot_noise + k, lane, T(M::noise_a) + T(M::noise_b) * (r * cs));
       if constexpr (k + 1 < M::NNOISE) lds_put(lds, M::slot_noise + k + 1, lane, T(M::noise_a) + T(M::noise_b) * (r * sn));
     });
@@ -2321,8 +2477,8 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
 // (group 0 also stores the trunk's and the RNG state).
 template <class M, class T, int G> __device__ __forceinline__ void run_group(const StepArgs& a, int lane, T* lds) {
   if constexpr (sizeof(T) == 8) {
-    // The f64 sine / cosine table, before any lane of the workgroup returns.
-    if constexpr (G == 0) fill_sincos_table(lane);
+    // The f64 sine / cosine and log tables, before any lane of the workgroup returns.
+    if constexpr (G == 0) fill_tables(lane);
     __syncthreads();
   }
   // Split-lane kernels give each world LANES consecutive lanes.

@@ -1111,7 +1111,7 @@ std::string gen_obs_source(const ModelD& m, const PolicyD* p, bool f64) {
     << arr1(naux, [&](int k) { return num(aux.empty() ? 0.0 : aux[k]); }) << ";\n};\n";
   s += o.str();
   s += "extern \"C\" __global__ void __launch_bounds__(64) phz_obs(phz::ObsArgs a) {\n";
-  if (f64) s += "  phz::fill_sincos_table(threadIdx.x);\n  __syncthreads();\n";  // f64 FK's joint sines and cosines
+  if (f64) s += "  phz::fill_tables(threadIdx.x);\n  __syncthreads();\n";  // f64 FK's joint sines and cosines
   s += "  const int w = blockIdx.x * 64 + threadIdx.x;\n";
   s += "  if (w < a.nworld) phz::obs_world<Model, Obs, " + T + ">(a, w);\n}\n";
   return s;

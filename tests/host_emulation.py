@@ -12,9 +12,9 @@ waves as G host threads:
     its own column, lds[slot * 64 + lane]);
   - __syncthreads() is a pthread barrier over the G threads;
   - the workgroup's LDS is one heap array of exactly the kernel's size, so
-    AddressSanitizer bounds every slot access (the f64 sine table, a
-    namespace-scope __shared__ array that wave 0 fills before a barrier, one
-    entry pair per lane, is a plain global that the emulated lane fills
+    AddressSanitizer bounds every slot access (the f64 sine and log tables,
+    namespace-scope __shared__ arrays that wave 0 fills before a barrier, one
+    entry pair per lane, are plain globals that the emulated lane fills
     whole);
   - the AMDGPU builtins become their host meanings (v_sin_f32 / v_cos_f32
     take turns, v_rcp / v_rsq are reciprocals, v_cvt_i32 saturates and maps
@@ -62,6 +62,7 @@ extern void* emu_lds_base;
 static inline float emu_amdgcn_rcpf(float x) { return 1.0f / x; }
 static inline double emu_amdgcn_rcp(double x) { return 1.0 / x; }
 static inline float emu_amdgcn_rsqf(float x) { return 1.0f / std::sqrt(x); }
+static inline double emu_amdgcn_rsq(double x) { return 1.0 / std::sqrt(x); }
 static inline float emu_amdgcn_sqrtf(float x) { return std::sqrt(x); }
 static inline float emu_amdgcn_sinf(float t) { return (float)std::sin(6.283185307179586 * (double)t); }
 static inline float emu_amdgcn_cosf(float t) { return (float)std::cos(6.283185307179586 * (double)t); }
@@ -197,9 +198,10 @@ def host_source(device_src: str, prec: str) -> str:
     s, n = re.subn(r"__shared__\s+" + t + r"\s+lds\[[^;]*\];", f"{t}* lds = ({t}*)emu_lds_base;", s)
     assert n == 1, "the kernel's LDS declaration was not found"
     # One emulated lane at a time: the filling lane writes the whole table.
-    fill = "phz_sc_tab[lane] = k[lane];\n  phz_sc_tab[64 + lane] = k[64 + lane];"
-    assert fill in s, "the f64 sine table's fill was not found"
-    s = s.replace(fill, "for (int e = 0; e < 128; e++) phz_sc_tab[e] = k[e];")
+    fill = ("phz_sc_tab[lane] = k[lane];\n  phz_sc_tab[64 + lane] = k[64 + lane];\n"
+            "  phz_log_tab[lane] = lg[lane];\n  phz_log_tab[64 + lane] = lg[64 + lane];")
+    assert fill in s, "the f64 tables' fill was not found"
+    s = s.replace(fill, "for (int e = 0; e < 128; e++) { phz_sc_tab[e] = k[e]; phz_log_tab[e] = lg[e]; }")
     assert "asm(" not in s, "an unhandled inline asm block is left in the source"
     return PRELUDE + s + "\n#define EMU_T " + t + "\n" + DRIVER
 

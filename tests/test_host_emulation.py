@@ -121,16 +121,11 @@ def test_f64_impulse_terrain_kernel_is_correct_on_the_host(mode):
     assert rel.max() <= 1e-12
 
 
-def test_f64_table_sincos_accuracy():
-    """tab_sincos, the f64 kernels' sine and cosine of a revolute joint angle
-    and of the Box-Muller angle, compiled from the device header for the host,
-    against mpmath at 40 digits: within 2 ulp on joint-angle ranges (4 ulp up
-    to |x| = 3e6, where the reduction's two-part 2 pi / 64 loses a little),
-    exact where the angle is below pi / 128 (the sine is then r itself), and
-    at the table's own nodes and the midpoints between them."""
+def device_math(call: str, words: np.ndarray, nout: int) -> np.ndarray:
+    """Run a device-header function on the host: `call` is a C++ statement
+    that reads in[i] (a double x = X(i) or a 64-bit word W(i)) and writes
+    o[nout * i + j]; the tables filled as a wave fills them."""
     import subprocess
-
-    import mpmath
     hdr = open(os.path.join(os.path.dirname(HE.HERE), "phyz_amd", "csrc", "phz_device.h")).read()
     main = r'''
 #include <cstdio>
@@ -138,27 +133,50 @@ def test_f64_table_sincos_accuracy():
 void* emu_lds_base = nullptr;
 extern "C" void emu_syncthreads() {}
 int main(int argc, char** argv) {
-  for (int lane = 0; lane < 64; lane++) phz::fill_sincos_table(lane);
+  for (int lane = 0; lane < 64; lane++) phz::fill_tables(lane);
   FILE* f = fopen(argv[1], "rb");
   long n = 0;
   if (fread(&n, 8, 1, f) != 1) return 3;
-  std::vector<double> x(n), o(2 * n);
-  if (fread(x.data(), 8, n, f) != (size_t)n) return 3;
+  std::vector<unsigned long long> in(n);
+  std::vector<double> o(NOUT * n);
+  if (fread(in.data(), 8, n, f) != (size_t)n) return 3;
   fclose(f);
-  for (long i = 0; i < n; i++) phz::tab_sincos(x[i], &o[2 * i], &o[2 * i + 1]);
+  for (long i = 0; i < n; i++) { CALL; }
   f = fopen(argv[2], "wb");
-  fwrite(o.data(), 8, 2 * n, f);
+  fwrite(o.data(), 8, NOUT * n, f);
   fclose(f);
   return 0;
 }
-'''
+'''.replace("NOUT", str(nout)).replace("CALL", call)
+    prelude = HE.PRELUDE + "#define X(i) __builtin_bit_cast(double, in[i])\n#define W(i) in[i]\n"
     os.makedirs(HE.CACHE, exist_ok=True)
-    cpp, exe = os.path.join(HE.CACHE, "tab_sincos.cpp"), os.path.join(HE.CACHE, f"tab_sincos_{os.getpid()}")
-    with open(cpp, "w") as f:
-        f.write(HE.PRELUDE + HE.host_device_code(hdr) + main)
-    r = subprocess.run([HE.CLANG, "-x", "c++", "-std=c++17", "-O2", "-ffp-contract=off", cpp, "-o", exe],
-                       capture_output=True, text=True)
-    assert r.returncode == 0, r.stderr[-3000:]
+    exe = os.path.join(HE.CACHE, f"device_math_{os.getpid()}")
+    with open(exe + ".cpp", "w") as f:
+        f.write(prelude + HE.host_device_code(hdr) + main)
+    fin, fout = exe + ".in", exe + ".out"
+    try:
+        r = subprocess.run([HE.CLANG, "-x", "c++", "-std=c++20", "-O2", "-ffp-contract=off", exe + ".cpp", "-o", exe],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-3000:]
+        with open(fin, "wb") as f:
+            np.array([len(words)], np.int64).tofile(f)
+            np.ascontiguousarray(words).view(np.uint64).tofile(f)
+        subprocess.run([exe, fin, fout], check=True)
+        return np.fromfile(fout).reshape(-1, nout)
+    finally:
+        for q in (exe, exe + ".cpp", fin, fout):
+            if os.path.exists(q):
+                os.remove(q)
+
+
+def test_f64_table_sincos_accuracy():
+    """tab_sincos, the f64 kernels' sine and cosine of a revolute joint angle
+    and of the Box-Muller angle, compiled from the device header for the host,
+    against mpmath at 40 digits: within 2 ulp on joint-angle ranges (4 ulp up
+    to |x| = 3e6, where the reduction's two-part 2 pi / 64 loses a little),
+    exact where the angle is below pi / 128 (the sine is then r itself), and
+    at the table's own nodes and the midpoints between them."""
+    import mpmath
     rng = np.random.default_rng(1)
     nodes = np.arange(-320, 321) * (2 * np.pi / 64)
     near = np.concatenate([rng.uniform(-60, 60, 3000), nodes, np.nextafter(nodes, np.inf),
@@ -167,17 +185,7 @@ int main(int argc, char** argv) {
     tiny = np.concatenate([tiny, -tiny])
     far = rng.uniform(-3e6, 3e6, 500)
     xs = np.concatenate([near, tiny, far])
-    fin, fout = exe + ".in", exe + ".out"
-    with open(fin, "wb") as f:
-        np.array([len(xs)], np.int64).tofile(f)
-        xs.tofile(f)
-    try:
-        subprocess.run([exe, fin, fout], check=True)
-        o = np.fromfile(fout).reshape(-1, 2)
-    finally:
-        for p in (exe, fin, fout):
-            if os.path.exists(p):
-                os.remove(p)
+    o = device_math("phz::tab_sincos(X(i), &o[2 * i], &o[2 * i + 1])", xs, 2)
     mpmath.mp.dps = 40
     ref = np.array([[float(mpmath.sin(mpmath.mpf(x))), float(mpmath.cos(mpmath.mpf(x)))] for x in xs])
     err, ulp = np.abs(o - ref), np.spacing(np.abs(ref))
@@ -185,3 +193,59 @@ int main(int argc, char** argv) {
     assert (err[:a] <= 2 * ulp[:a] + 2.0 ** -60).all()
     assert (err[a:b, 0] == 0).all() and (err[a:b, 1] <= ulp[a:b, 1]).all()
     assert (err[b:] <= 4 * ulp[b:] + 2.0 ** -60).all()
+
+
+def test_f64_table_log_sqrt_and_box_muller_accuracy():
+    """The f64 Box-Muller pieces compiled from the device header for the host,
+    against mpmath at 40 digits: tab_log within 1 ulp over 1 - u for uniform u,
+    x just below 1 (1 - k 2^-53), the powers of two the radius meets, the
+    table's interval boundaries and their neighbours, and normal x from 1e-300
+    to 1e300, exactly 0 at 1; nr_sqrt (with the host's exact reciprocal square
+    root for the hardware estimate, so this pins the refinement, not the
+    estimate) correctly rounded on [0, 80] and over the normal range; and
+    box_muller(double) from 64-bit states: the state advanced by exactly two
+    xorshift64 draws, the radius within 1 ulp of sqrt(-2 ln(1 - u1)) and the
+    sine and cosine within 2 ulp of those of 2 pi u2."""
+    import struct
+
+    import mpmath
+    mpmath.mp.dps = 40
+    rng = np.random.default_rng(3)
+    bounds = []
+    for i in range(65):
+        b = struct.unpack("<d", struct.pack("<Q", (0x3FE62000 + i * 2 ** 14) << 32))[0]
+        bounds += [b, np.nextafter(b, 0), np.nextafter(b, 2)]
+    xs = np.concatenate([1 - rng.random(2000), 1 - np.arange(0, 200) * 2.0 ** -53, 2.0 ** -np.arange(0, 54), bounds,
+                         np.exp(rng.uniform(-690, 690, 1000)), [1e-300]])
+    got = device_math("o[i] = phz::tab_log(X(i))", xs, 1)[:, 0]
+    ref = np.array([float(mpmath.log(mpmath.mpf(x))) for x in xs])
+    assert got[xs == 1.0].tolist() == [0.0] * int((xs == 1.0).sum())
+    nz = ref != 0
+    assert (np.abs(got - ref)[nz] <= np.spacing(np.abs(ref))[nz]).all()
+
+    ys = np.concatenate([rng.uniform(0, 80, 2000), [0.0, 2.0 ** -52, 2.0 ** -1000, 1.0, 2.0, 4.0],
+                         np.exp(rng.uniform(-690, 690, 1000))])
+    assert np.array_equal(device_math("o[i] = phz::nr_sqrt(X(i))", ys, 1)[:, 0], np.sqrt(ys))
+
+    st = rng.integers(1, 2 ** 63, 1500, dtype=np.int64).astype(np.uint64)
+    got = device_math("{ unsigned long long s = W(i); phz::box_muller(s, &o[4 * i], &o[4 * i + 1], &o[4 * i + 2]);"
+                      " o[4 * i + 3] = __builtin_bit_cast(double, s); }", st, 4)
+    mask = (1 << 64) - 1
+
+    def xorshift(x):
+        x ^= (x << 13) & mask
+        x ^= x >> 7
+        return x ^ ((x << 17) & mask)
+
+    ref, nxt = [], []
+    for s0 in st:
+        x1 = xorshift(int(s0))
+        x2 = xorshift(x1)
+        u1, u2 = mpmath.mpf(x1 >> 11) / 2 ** 53, mpmath.mpf(x2 >> 11) / 2 ** 53
+        ref.append([float(mpmath.sqrt(-2 * mpmath.log(1 - u1))), float(mpmath.sin(2 * mpmath.pi * u2)),
+                    float(mpmath.cos(2 * mpmath.pi * u2))])
+        nxt.append(x2)
+    ref = np.array(ref)
+    assert np.array_equal(got[:, 3].view(np.uint64), np.array(nxt, dtype=np.uint64))
+    err, ulp = np.abs(got[:, :3] - ref), np.spacing(np.abs(ref))
+    assert (err[:, 0] <= ulp[:, 0]).all() and (err[:, 1:] <= 2 * ulp[:, 1:]).all()
