@@ -1812,8 +1812,11 @@ __device__ __forceinline__ void body_solve(WS<M, T>& ws, const T* q, const T* v,
       T dj = D[j][j];
 #pragma unroll
       for (int k = 0; k < j; k++) dj = dj - ws.Lm[i][j][k] * E[j][k];
-      ws.ok[i] = ws.ok[i] && !(dabs(dj) < T(1e-20));
-      ws.Dinv[i][j] = frcp(dabs(dj) < T(1e-20) ? T(1) : dj);
+      // piv_ok: the host has bounded every pivot of this joint away from the
+      // test, so ok stays true at compile time and the parent updates guarded
+      // by it need no branch.
+      if constexpr (!M::piv_ok[i]) ws.ok[i] = ws.ok[i] && !(dabs(dj) < T(1e-20));
+      ws.Dinv[i][j] = frcp(!M::piv_ok[i] && dabs(dj) < T(1e-20) ? T(1) : dj);
 #pragma unroll
       for (int r = j + 1; r < nd; r++) {
         T e = D[r][j];

@@ -472,6 +472,89 @@ int lanes_per_world(const ModelD& m, const Features& f, const Plan& pl) {
   return L;
 }
 
+// Whether body i's joint-space inertia D = S^T I_A S + (armature + dt
+// damping) 1 can never give an LDL pivot below the singular test's 1e-20
+// (aba.rs:210 skips such a body), for any configuration: I_A is the body's
+// own spatial inertia plus its children's articulated inertias, which are
+// positive semidefinite, so every pivot of D is at least the least pivot
+// bound of D0 = S^T I_i S + (armature + dt damping) 1, and D0 - tau 1 >= 0
+// (a Cholesky factorisation that succeeds) bounds every pivot by tau. tau
+// adds to 1e-20 a rounding margin of 1e3 unit roundoffs times the trace of
+// an upper bound of the subtree's composite inertia about the joint
+// (sum of tr Ic_j + m_j (3 + 2 R_j^2), R_j the joint-to-COM distance along
+// the fixed link offsets). A slide or free joint inside the subtree leaves
+// R unbounded: no bound then. With the bound the kernel drops the test and
+// the branch around the parent update.
+bool pivots_bounded(const ModelD& m, int i, bool f64) {
+  const int nb = m.nb;
+  // Distance bound from body i's joint to each descendant's frame origin.
+  std::vector<double> reach(nb, -1.0);
+  reach[i] = 0.0;
+  double trace = 0.0;
+  for (int j = i; j < nb; j++) {
+    if (j != i) {
+      const int pj = m.b[j].parent;
+      if (pj < 0 || reach[pj] < 0.0) continue;
+      if (m.b[j].jtype == 1 || m.b[j].jtype == 4) return false;
+      const double* t = m.b[j].ptj_pos;
+      reach[j] = reach[pj] + std::sqrt(t[0] * t[0] + t[1] * t[1] + t[2] * t[2]);
+    }
+    const BodyD& b = m.b[j];
+    const double rc = reach[j] + std::sqrt(b.com[0] * b.com[0] + b.com[1] * b.com[1] + b.com[2] * b.com[2]);
+    trace += b.inertia[0] + b.inertia[1] + b.inertia[2] + b.mass * (3.0 + 2.0 * rc * rc);
+  }
+  const double eps = f64 ? 0x1p-53 : 0x1p-24;
+  const double tau = 1e-20 + 1e3 * eps * trace;
+  const BodyD& b = m.b[i];
+  const double cx = b.com[0], cy = b.com[1], cz = b.com[2], mm = b.mass;
+  const double c2 = cx * cx + cy * cy + cz * cz;
+  const double Ic[9] = {b.inertia[0], b.inertia[3], b.inertia[4], b.inertia[3], b.inertia[1],
+                        b.inertia[5], b.inertia[4], b.inertia[5], b.inertia[2]};
+  const double c[3] = {cx, cy, cz};
+  double Is[6][6] = {};  // spatial inertia at the body frame, angular rows first
+  for (int r = 0; r < 3; r++)
+    for (int k = 0; k < 3; k++) Is[r][k] = Ic[r * 3 + k] + mm * ((r == k ? c2 : 0.0) - c[r] * c[k]);
+  const double X[9] = {0, -cz, cy, cz, 0, -cx, -cy, cx, 0};  // [c]x
+  for (int r = 0; r < 3; r++)
+    for (int k = 0; k < 3; k++) {
+      Is[r][3 + k] = mm * X[r * 3 + k];
+      Is[3 + k][r] = mm * X[r * 3 + k];
+    }
+  for (int r = 0; r < 3; r++) Is[3 + r][3 + r] = mm;
+  int nd = 0;
+  double S[6][6] = {};  // columns of the motion subspace
+  if (b.jtype == 0 || b.jtype == 1) {
+    for (int k = 0; k < 3; k++) S[(b.jtype == 0 ? 0 : 3) + k][0] = b.axis[k];
+    nd = 1;
+  } else if (b.jtype == 3) {
+    for (int k = 0; k < 3; k++) S[k][k] = 1.0;
+    nd = 3;
+  } else if (b.jtype == 4) {
+    for (int k = 0; k < 6; k++) S[k][k] = 1.0;
+    nd = 6;
+  } else {
+    return true;  // a fixed joint has no pivots
+  }
+  double D[6][6];
+  for (int r = 0; r < nd; r++)
+    for (int k = 0; k < nd; k++) {
+      double acc = 0.0;
+      for (int a = 0; a < 6; a++)
+        for (int e = 0; e < 6; e++) acc += S[a][r] * Is[a][e] * S[e][k];
+      D[r][k] = acc + (r == k ? b.armature + m.dt * b.damping - tau : 0.0);
+    }
+  for (int k = 0; k < nd; k++) {  // Cholesky of D0 - tau 1
+    for (int t = 0; t < k; t++) D[k][k] -= D[k][t] * D[k][t];
+    if (!(D[k][k] > 0.0)) return false;
+    D[k][k] = std::sqrt(D[k][k]);
+    for (int r = k + 1; r < nd; r++) {
+      for (int t = 0; t < k; t++) D[r][k] -= D[r][t] * D[k][t];
+      D[r][k] /= D[k][k];
+    }
+  }
+  return true;
+}
+
 std::string gen_model(const ModelD& m, const Features& f) {
   const int nb = m.nb;
   // Rigid spatial inertia [[Ic + m cx cx^T, m cx], [m cx^T, m 1]] as symmetric blocks.
@@ -689,6 +772,11 @@ std::string gen_model(const ModelD& m, const Features& f) {
       if (b.axis[c] != 0.0) { nz++; k = c; }
     return nz == 1 && std::fabs(b.axis[k]) == 1.0 ? k : -1;
   });
+  // Not for an f64 kernel of several waves: the MJCF humanoid's four-wave
+  // f64 kernel without the branch returned non-finite worlds on gfx950 where
+  // its host emulation (ASan, TSan, finite-math -O3) and the oracle agree.
+  const bool multi_f64 = f.f64 && pl.groups.size() > 1;
+  bb("piv_ok", [&](int i) { return !multi_f64 && pivots_bounded(m, i, f.f64); });
   db("mass", [&](int i) { return m.b[i].mass; });
   d2("com", 3, [&](int i, int k) { return m.b[i].com[k]; });
   d2("inA", 6, [&](int i, int k) { return A[i * 6 + k]; });
