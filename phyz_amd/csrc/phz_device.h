@@ -426,33 +426,10 @@ __device__ __forceinline__ void turn_sincos(float u, float* s, float* c) {
   *c = __builtin_amdgcn_cosf(u);
 }
 // sin and cos of a joint angle in f64 for the f32 kernels' penetration chain:
-// the reduction of angle_sincos (exact for |x| < 1.6e6), Taylor series through
-// r^13 and r^14, truncation below 3e-14 on |r| <= pi/4.
-__device__ __forceinline__ void joint_sincos64(double x, double* s, double* c) {
-  const double k = rint(x * 0x1.45f306dc9c883p-1);
-  const double r = (x - k * 0x1.921fb54400000p+0) - k * 0x1.0b4611a626331p-34;
-  const double r2 = r * r;
-  double ps = 1.0 / 6227020800.0;  // 1/13!
-  ps = fma(ps, -r2, 1.0 / 39916800.0);
-  ps = fma(ps, -r2, 1.0 / 362880.0);
-  ps = fma(ps, -r2, 1.0 / 5040.0);
-  ps = fma(ps, -r2, 1.0 / 120.0);
-  ps = fma(ps, -r2, 1.0 / 6.0);
-  const double sr = fma(-r * r2, ps, r);
-  double pc = 1.0 / 87178291200.0;  // 1/14!
-  pc = fma(pc, -r2, 1.0 / 479001600.0);
-  pc = fma(pc, -r2, 1.0 / 3628800.0);
-  pc = fma(pc, -r2, 1.0 / 40320.0);
-  pc = fma(pc, -r2, 1.0 / 720.0);
-  pc = fma(pc, -r2, 1.0 / 24.0);
-  pc = fma(pc, -r2, 0.5);
-  const double cr = fma(-r2, pc, 1.0);
-  const int q = cvt_sat_i32(k) & 3;  // a diverged world's NaN selects quadrant 0
-  const double a = (q & 1) ? cr : sr;
-  const double b = (q & 1) ? sr : cr;
-  *s = (q & 2) ? -a : a;
-  *c = ((q + 1) & 2) ? -b : b;
-}
+// tab_sincos from the LDS table, which those kernels fill as the f64 kernels
+// do (within 2 ulp; the Taylor form through r^13 it replaced truncated at
+// 3e-14 and took about 35 VALU instructions and thirteen constants).
+__device__ __forceinline__ void joint_sincos64(double x, double* s, double* c) { tab_sincos(x, s, c); }
 __device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double dlog(double x) { return log(x); }
 __device__ __forceinline__ float dlog(float x) { return logf(x); }
@@ -2479,8 +2456,9 @@ __device__ __forceinline__ void step_impulse(T (&q)[M::NQ], T (&v)[M::NV], T (&c
 // loads the DOFs it owns and the trunk's; it stores only the DOFs it owns
 // (group 0 also stores the trunk's and the RNG state).
 template <class M, class T, int G> __device__ __forceinline__ void run_group(const StepArgs& a, int lane, T* lds) {
-  if constexpr (sizeof(T) == 8) {
-    // The f64 sine / cosine and log tables, before any lane of the workgroup returns.
+  if constexpr (sizeof(T) == 8 || pen64<M, T>()) {
+    // The f64 sine / cosine and log tables (f64 kernels, and the f32 contact
+    // kernels' f64 penetration chain), before any lane of the workgroup returns.
     if constexpr (G == 0) fill_tables(lane);
     __syncthreads();
   }
