@@ -212,19 +212,24 @@ struct PolicyArgs {
 };
 
 // KernelRng::uniform / normal (policy_pipeline.rs:441-456): 53-bit uniform,
-// Box–Muller on two uniforms, cosine branch, in double. ln u1 is bm_log (u1 >=
-// 1e-300, a normal number; within about 2 ulp of the library log) and the
-// cosine the step kernels' closed-form angle_sincos: about a third of the
-// library routines' instructions, and these 37 normals per world and control
-// step are the part of the policy kernel that does not overlap its MFMAs.
-__device__ __forceinline__ double policy_uniform(u64& s) { return (double)(xorshift64(s) >> 11) * 0x1.0p-53; }
+// Box-Muller on two uniforms, cosine branch, in double: sqrt(-2 ln u1) cos(2 pi
+// u2) with u1 >= 1e-300. The uniforms come from the draws' 32-bit words in one
+// exact fma each; ln is tab_log and the root nr_sqrt (the step kernels' f64
+// Box-Muller, within 1 ulp each); the cosine is taken in turns, where the
+// reduction is exact (t = 64 u2, k = rint(t), r = (t - k) 2 pi / 64) and the
+// LDS table gives cos(2 pi k / 64), within 2 ulp of the cosine of the exact
+// angle. These 37 normals per world and control step are the part of the
+// policy kernel that does not overlap its MFMAs; the kernel fills the tables
+// at its start.
 __device__ __forceinline__ double policy_normal(u64& s) {
-  double u1 = policy_uniform(s);
-  const double u2 = policy_uniform(s);
-  if (u1 < 1e-300) u1 = 1e-300;
+  const u64 x1 = xorshift64(s);
+  const u64 x2 = xorshift64(s);
+  const double u1 = fma((double)(unsigned)(x1 >> 32), 0x1p-32, (double)((unsigned)x1 >> 11) * 0x1p-53);
+  const double t = fma((double)(unsigned)(x2 >> 32), 0x1p-26, (double)((unsigned)x2 >> 11) * 0x1p-47);
+  const double k = rint(t);
   double sn, cs;
-  angle_sincos(6.283185307179586476925286766559 * u2, &sn, &cs);
-  return sqrt(-2.0 * bm_log(u1)) * cs;
+  tab_sincos_at((t - k) * 0x1.921fb54442d18p-4, cvt_sat_i32(k) & 63, &sn, &cs);
+  return nr_sqrt(-2.0 * tab_log(fmax(u1, 1e-300))) * cs;
 }
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {

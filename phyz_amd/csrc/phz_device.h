@@ -333,39 +333,9 @@ __device__ __forceinline__ void rev_sincos(float xf, float* s, float* c) {
   *c = __builtin_amdgcn_cosf(x);
 }
 __device__ __forceinline__ void rev_sincos(double x, double* s, double* c) { tab_sincos(x, s, c); }
-// ln x for a normal x in (0, 1] (the policy kernel's Box-Muller ln u1, u1 >=
-// 1e-300), within about 2 ulp: x = 2^e m with m in [sqrt(1/2), sqrt(2)) from
-// the hardware frexp; ln m = 2 atanh s = 2 s (1 + z P(z)) with s = (m - 1) /
-// (m + 1), |s| <= 0.1716, z = s^2, and P(z) = sum_j z^j / (2j + 3) through
-// z^8 (the first omitted term is below 3e-17 of ln m), in Estrin's form;
-// 1 / (m + 1) is the hardware reciprocal refined by two Newton steps; ln 2 is
-// split so that e * ln2_hi is exact. About a third of the library log's
-// instructions.
-__device__ __forceinline__ double bm_log(double x) {
-  double m = __builtin_amdgcn_frexp_mant(x);  // [0.5, 1)
-  int e = __builtin_amdgcn_frexp_exp(x);
-  const bool low = m < 0x1.6a09e667f3bcdp-1;
-  m = low ? 2.0 * m : m;
-  e = low ? e - 1 : e;
-  const double d = m + 1.0;
-  double r = __builtin_amdgcn_rcp(d);
-  r = fma(fma(-d, r, 1.0), r, r);
-  r = fma(fma(-d, r, 1.0), r, r);
-  const double s = (m - 1.0) * r;
-  const double z = s * s;
-  const double z2 = z * z;
-  const double z4 = z2 * z2;
-  const double p01 = fma(z, 1.0 / 5.0, 1.0 / 3.0);
-  const double p23 = fma(z, 1.0 / 9.0, 1.0 / 7.0);
-  const double p45 = fma(z, 1.0 / 13.0, 1.0 / 11.0);
-  const double p67 = fma(z, 1.0 / 17.0, 1.0 / 15.0);
-  const double p = fma(z4, fma(z4, 1.0 / 19.0, fma(z2, p67, p45)), fma(z2, p23, p01));
-  const double lnm = 2.0 * fma(s * z, p, s);
-  const double fe = (double)e;
-  return fma(fe, 0x1.62e42fefa3800p-1, fma(fe, 0x1.ef35793c76730p-45, lnm));
-}
 // ln x for a normal x > 0 from the LDS table phz_log_tab (Tang's method),
-// within about 1 ulp: the step kernels' f64 Box-Muller ln(1 - u). From x's
+// within about 1 ulp: the f64 Box-Muller logarithms (the step kernels'
+// ln(1 - u), the policy kernel's ln u1). From x's
 // high word h by integer arithmetic alone: t = h - 0x3FE62000, k = t >> 20
 // (arithmetic) and z = x / 2^k, so that z lies in [OFF, 2 OFF), OFF =
 // 0x1.62p-1 (about 0.691); bits 14..19 of t pick one of 64 intervals of z,
@@ -375,8 +345,8 @@ __device__ __forceinline__ double bm_log(double x) {
 // logc = 0 exactly, so that x near 1 keeps its relative accuracy. Then
 // r = z invc - 1 by one fma (|r| <= 2^-7, rounded once), ln x = k ln2 + logc
 // + log1p r, log1p r through r^8 in Estrin's form (truncation below 2^-59
-// of r). About 20 VALU instructions and one LDS read, against about 33 for
-// bm_log.
+// of r). About 20 VALU instructions and one LDS read, where an atanh series
+// on [sqrt(1/2), sqrt(2)) takes about 33 and the library log about 90.
 __device__ __forceinline__ double tab_log(double x) {
   const u64 b = __builtin_bit_cast(u64, x);
   const unsigned h = (unsigned)(b >> 32);

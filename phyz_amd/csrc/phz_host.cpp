@@ -1228,6 +1228,7 @@ std::string gen_policy_source(const PolicyD& p, int npd, bool f64) {
   s += o.str();
   s += "extern \"C\" __global__ void __launch_bounds__(64) phz_policy(phz::PolicyArgs a) {\n";
   s += "  __shared__ float lds[Pol::LDS];\n";
+  s += "  phz::fill_tables(threadIdx.x);\n  __syncthreads();\n";  // the normals' f64 log, sine and cosine tables
   s += "  phz::policy_wave<Pol, " + T + ">(a, lds);\n}\n";
   return s;
 }
