@@ -318,7 +318,10 @@ typedef double double4_t __attribute__((ext_vector_type(4)));
 // inputs past O and I read clamped in-range values and are not stored. Every
 // sum is an f64 sum in an order fixed by the hardware, so a tile's partials
 // are reproducible. The bias sums use four lanes per output: rows p, p + 4,
-// ... for lane p, combined by a fixed butterfly.
+// ... for lane p, combined by a fixed butterfly. The partials are stored
+// non-temporally: each is written once here and read once by ppo_adam,
+// mostly on another XCD, so holding them in this XCD's L2 only slowed the
+// stores (31 -> 25 us per tile launch at the timing shape).
 __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O, const float* __restrict__ X,
                            uint32_t ldx, uint32_t I, uint32_t R, double* __restrict__ Gw, double* __restrict__ Gb) {
   const uint32_t wave = threadIdx.x / 64u, lane = threadIdx.x % 64u;
@@ -352,7 +355,7 @@ __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const uint32_t o = o0 + lr + 4u * v, i = i0 + lc;
-        if (o < O && i < I) Gw[(size_t)o * I + i] = acc[v];
+        if (o < O && i < I) __builtin_nontemporal_store(acc[v], &Gw[(size_t)o * I + i]);
       }
     }
   for (uint32_t t = threadIdx.x; t < 4u * ((O + 15u) & ~15u); t += kTileThreads) {
@@ -362,7 +365,7 @@ __device__ void dense_grad(const float* __restrict__ D, uint32_t ldd, uint32_t O
       for (uint32_t r = p; r < R; r += 4u) acc += (double)D[r * ldd + o];
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
-    if (p == 0 && o < O) Gb[o] = acc;
+    if (p == 0 && o < O) __builtin_nontemporal_store(acc, &Gb[o]);
   }
 }
 
