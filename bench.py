@@ -494,28 +494,33 @@ def control_parity(cl, sim, q, v):
     return {"worlds_checked": len(idx), **{k: float(f"{e:.3g}") for k, e in err.items()}}, orc
 
 
-def control_cpu_baseline(cl, orc, nworld: int = 512, n_control: int = 32):
-    """The oracle's rollout (observe + policy per world in Python, then the f64
-    physics steps threaded over worlds) on a bounded sample."""
+def control_cpu_baseline(cl, orc, nworld: int = 4096, n_control: int = 16):
+    """The oracle's rollout on a bounded sample: per control step the f64 FK on
+    all host threads, the observation ops and the policy batched over worlds in
+    numpy (oracle/policy_ref.py's batched forms), then the f64 physics steps
+    threaded over worlds."""
     from oracle import policy_ref as PR
     threads, _ = host_threads()
     m = cl.base.model
     q, v, c, _ = cl.base.initial_state(nworld)
     base = cl.base_targets(nworld)
-    rngs = [PR.KernelRng.for_world(cl.seed, w) for w in range(nworld)]
-    zs = np.zeros((nworld, cl.spec.n_out()))
+    rng = PR.BatchRng.for_worlds(cl.seed, range(nworld))
+    z = np.zeros((nworld, cl.spec.n_out()))
     tg = np.zeros((nworld, len(cl.pd)))
+    t_pol = 0.0
     t0 = time.perf_counter()
     for _ in range(n_control):
-        for w in range(nworld):
-            o = np.array(PR.observe_reference(m, orc, q[w], v[w], cl.spec.obs))
-            PR.policy_reference(cl.spec, cl.weights, cl.std, rngs[w], o, zs[w], base[w], tg[w])
+        ta = time.perf_counter()
+        obs = PR.observe_batch(m, orc, q, v, cl.spec.obs, threads)
+        PR.policy_batch(cl.spec, cl.weights, cl.std, rng, obs, z, base, tg)
+        t_pol += time.perf_counter() - ta
         orc.step_batch(q, v, c, cl.control_every, targets=tg, threads=threads)
     dt = time.perf_counter() - t0
     return {"value": round(nworld * n_control * cl.control_every / dt, 1), "unit": "world-steps/s", "cores": threads,
             "kind": "port", "sample": f"{nworld} worlds x {n_control} control steps x {cl.control_every} physics steps, "
-                                      f"f64 oracle (observation and policy per world in one Python thread, C++ physics "
-                                      f"on {threads} threads), {dt:.1f} s",
+                                      f"f64 oracle (FK and physics in C++ on {threads} threads, observation and policy "
+                                      f"batched over worlds in numpy), {dt:.1f} s of which observe+policy "
+                                      f"{t_pol:.1f} s",
             "control_steps_per_s": round(nworld * n_control / dt, 1)}
 
 

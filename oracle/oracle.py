@@ -51,6 +51,7 @@ def lib():
         L.orc_crba.argtypes = [C.c_void_p, dp, dp]
         L.orc_generalized_forces.argtypes = [C.c_void_p, dp, dp, dp, dp]
         L.orc_fk.argtypes = [C.c_void_p, dp, dp, dp]
+        L.orc_fk_batch.argtypes = [C.c_void_p, C.c_int, dp, dp, dp, C.c_int]
         L.orc_contact.argtypes = [C.c_void_p, dp, dp, dp, dp]
         L.orc_integrate.argtypes = [C.c_void_p, dp, dp, dp]
         L.orc_world_seed.restype = C.c_uint64
@@ -193,6 +194,14 @@ class Oracle:
     def fk(self, q, v):
         out = np.zeros((self.nb, 18))
         lib().orc_fk(self._h, _d(np.ascontiguousarray(q, dtype=np.float64)), _d(np.ascontiguousarray(v, dtype=np.float64)), _d(out))
+        return out
+
+    def fk_batch(self, q, v, threads=1):
+        """fk over world-major states: [nworld][nb][18]."""
+        q = np.ascontiguousarray(q, dtype=np.float64)
+        v = np.ascontiguousarray(v, dtype=np.float64)
+        out = np.zeros((q.shape[0], self.nb, 18))
+        lib().orc_fk_batch(self._h, q.shape[0], _d(q), _d(v), _d(out), int(threads))
         return out
 
     def contact(self, q, v):

@@ -184,6 +184,27 @@ int orc_fk(orc_model* o, const double* q, const double* v, double* out) {
   }
   return 0;
 }
+// orc_fk over nworld world-major states (out: [nworld][nb][18]), worlds split
+// over `threads` threads (0: all hardware threads).
+int orc_fk_batch(orc_model* o, int nworld, const double* q, const double* v, double* out, int threads) {
+  const Model& m = o->m;
+  if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+  threads = std::min(threads, std::max(1, nworld));
+  auto work = [&](int w0, int w1) {
+    for (int w = w0; w < w1; w++)
+      orc_fk(o, q + (size_t)w * m.nq, v + (size_t)w * m.nv, out + (size_t)w * m.nb * 18);
+  };
+  if (threads == 1) { work(0, nworld); return 0; }
+  std::vector<std::thread> pool;
+  int chunk = (nworld + threads - 1) / threads;
+  for (int t = 0; t < threads; t++) {
+    int w0 = t * chunk, w1 = std::min(nworld, w0 + chunk);
+    if (w0 >= w1) break;
+    pool.emplace_back(work, w0, w1);
+  }
+  for (auto& th : pool) th.join();
+  return 0;
+}
 int orc_contact(orc_model* o, const double* q, const double* v, double* ext_out, double* rows_out) {
   if (!o->m.contact) return 1;
   std::vector<FK<double>> fk(o->m.nb);

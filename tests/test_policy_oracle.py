@@ -188,3 +188,66 @@ def test_heading_frame_is_yaw_invariant():
     r1 = PR.observe_reference(m, orc, q1, np.zeros(m.nv), ops)
     np.testing.assert_allclose(r0[:3], r1[:3], atol=1e-12)
     assert abs(r0[3] - r1[3]) > 1e-6
+
+
+def test_batched_forms_follow_the_per_world_functions():
+    """The world-batched observation, RNG and policy (the control-loop CPU
+    baseline's forms) against the per-world functions, world by world, over
+    three control steps of the ant control workload with its PD physics in
+    between: RNG states bit for bit, everything else to 1e-12 (the batched
+    products and numpy's log/cos round differently)."""
+    from phyz_amd import workloads as W
+    from phyz_amd.model import pack_geometries, pack_pd_dofs
+    cl = W.control_loop(hidden=32)
+    m = cl.base.model
+    g, _ = pack_geometries(m, cl.base.contact.stiffness, cl.base.contact.damping)
+    orc = Oracle(m, contact=(g, cl.base.contact.ground_height, cl.base.contact.friction), pd=pack_pd_dofs(cl.pd))
+    nw = 12
+    q, v, c, _ = cl.base.initial_state(nw)
+    rng = np.random.default_rng(5)
+    q[:, 6:] += rng.uniform(-0.3, 0.3, size=(nw, m.nq - 6))
+    v += rng.uniform(-0.5, 0.5, size=v.shape)
+    base = cl.base_targets(nw)
+    # Every op kind, including the world-frame COM entry, a constant and an empty support.
+    feet = [(2 + 2 * k, [0.0, 0.0, 0.0]) for k in range(4)]
+    extra = [P.Const(0.25), P.BodyPos(0, 2), P.BodyPos(3, 1), P.ComOverSupport(feet, None, 2),
+             P.ComOverSupport(feet, 0, 2), P.ComOverSupport([], 0, 0), P.BodyYawError(0, 3.0)]
+    ops = list(cl.spec.obs) + extra
+    rows_b = PR.kinematics_rows_batch(orc, q, v, threads=3)
+    ob = PR.observe_batch(m, orc, q, v, ops, threads=2)
+    for w in range(nw):
+        np.testing.assert_array_equal(rows_b[w], PR.kinematics_rows(orc, q[w], v[w]))
+        np.testing.assert_allclose(ob[w], PR.observe_reference(m, orc, q[w], v[w], ops), rtol=0, atol=1e-12)
+    rngs = [PR.KernelRng.for_world(cl.seed, w) for w in range(nw)]
+    brng = PR.BatchRng.for_worlds(cl.seed, range(nw))
+    z1, zb = np.zeros((nw, cl.spec.n_out())), np.zeros((nw, cl.spec.n_out()))
+    t1, tb = np.zeros((nw, len(cl.pd))), np.zeros((nw, len(cl.pd)))
+    qb, vb, cb = q.copy(), v.copy(), c.copy()
+    for step in range(3):
+        obs_b = PR.observe_batch(m, orc, qb, vb, cl.spec.obs, threads=2)
+        act_b, lp_b = PR.policy_batch(cl.spec, cl.weights, cl.std, brng, obs_b, zb, base, tb)
+        for w in range(nw):
+            o = np.array(PR.observe_reference(m, orc, q[w], v[w], cl.spec.obs))
+            a, lp = PR.policy_reference(cl.spec, cl.weights, cl.std, rngs[w], o, z1[w], base[w], t1[w])
+            assert int(brng.state[w]) == rngs[w].state, (step, w)
+            np.testing.assert_allclose(obs_b[w], o, rtol=0, atol=1e-12)
+            np.testing.assert_allclose(act_b[w], a, rtol=0, atol=1e-12)
+            assert lp_b[w] == pytest.approx(lp, abs=1e-11)
+        np.testing.assert_allclose(zb, z1, rtol=0, atol=1e-12)
+        np.testing.assert_allclose(tb, t1, rtol=0, atol=1e-12)
+        orc.step_batch(q, v, c, cl.control_every, targets=t1, threads=1)
+        orc.step_batch(qb, vb, cb, cl.control_every, targets=tb, threads=4)
+        np.testing.assert_allclose(qb, q, rtol=0, atol=1e-9)
+    # The states really moved and the policy acted on them.
+    assert np.abs(t1 - base).max() > 1e-3
+
+
+def test_batch_rng_draws_match_kernel_rng():
+    """BatchRng's u64 words, uniforms and normals against KernelRng per world."""
+    worlds = [0, 1, 7, 1000, 123456]
+    b = PR.BatchRng.for_worlds(42, worlds)
+    ks = [PR.KernelRng.for_world(42, w) for w in worlds]
+    for _ in range(5):
+        assert [int(x) for x in b.next_u64()] == [k.next_u64() for k in ks]
+        np.testing.assert_array_equal(b.uniform(), [k.uniform() for k in ks])
+        np.testing.assert_allclose(b.normal(), [k.normal() for k in ks], rtol=1e-15, atol=1e-15)
