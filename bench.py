@@ -494,7 +494,7 @@ def control_parity(cl, sim, q, v):
     return {"worlds_checked": len(idx), **{k: float(f"{e:.3g}") for k, e in err.items()}}, orc
 
 
-def control_cpu_baseline(cl, orc, nworld: int = 4096, n_control: int = 16):
+def control_cpu_baseline(cl, orc, nworld: int = 8192, n_control: int = 32):
     """The oracle's rollout on a bounded sample: per control step the f64 FK on
     all host threads, the observation ops and the policy batched over worlds in
     numpy (oracle/policy_ref.py's batched forms), then the f64 physics steps
