@@ -396,7 +396,10 @@ __device__ inline float clampf(float x, float lo, float hi) { return x < lo ? lo
 // One workgroup per (tile of R minibatch rows, network); MODE as above.
 template <int MODE>
 __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
-  if (*a.skip) return;
+  // The stop flag is read here and tested once the tile's first loads are in
+  // flight, so its round trip overlaps theirs; a stopped minibatch's loads
+  // stay in bounds (its index list was validated) and it stores nothing.
+  const int stopped = *a.skip;
   extern __shared__ __align__(16) float lds[];
   const int net = blockIdx.y;
   const Dims d = a.dims[net];
@@ -497,6 +500,7 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
     q0 = q;
     ch0 = ch;
   }
+  if (stopped) return;  // uniform over the workgroup, before its first barrier
   if (net == 0 && threadIdx.x < d.n_out) {
     const float sd = expf(sdv);
     SD[threadIdx.x] = sd;
@@ -705,11 +709,10 @@ __device__ void brake(const AdamArgs& a) {
 // a fixed tree; a fixed xor butterfly gives all four the same total, and the
 // first applies the step.
 __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
-  if (*a.skip) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
-    return;
-  }
-  if (blockIdx.x == 0) brake(a);
+  // The stop flag is tested once the partial sums' loads are in flight (as
+  // in ppo_tiles); a stopped minibatch's tiles stored nothing, so what they
+  // read is never used.
+  const int stopped = *a.skip;
   const uint32_t gt = blockIdx.x * kAdamThreads + threadIdx.x;
   const uint32_t t = gt / kAdamLanes, sub = gt % kAdamLanes;
   const bool valid = t < a.n_param[0] + a.n_param[1];
@@ -731,6 +734,11 @@ __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
     for (uint32_t j = 0; j < kChains; j++)
       if (k + j * kAdamLanes < a.tiles) gc[j] += part[(size_t)(k + j * kAdamLanes) * np];
   }
+  if (stopped) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
+    return;
+  }
+  if (blockIdx.x == 0) brake(a);
   double g = ((gc[0] + gc[1]) + (gc[2] + gc[3])) + ((gc[4] + gc[5]) + (gc[6] + gc[7]));
   for (int off = 1; off < kAdamLanes; off <<= 1) g += __shfl_xor(g, off, 64);
   if (!valid || sub != 0) return;
