@@ -455,21 +455,37 @@ Plan plan_partition(const ModelD& m, const Features& f) {
 
 // Lanes per world of the step kernel. A launch of few worlds leaves most SIMDs
 // idle (4096 worlds are 64 waves on 1024 SIMDs), and a one-lane kernel then
-// runs at the latency of its own instruction stream: such launches give each
-// world 2 or 4 lanes that split the revolute joints' sincos (see
-// trig_prepass in phz_device.h) when the split waves still fit one per SIMD.
-// Contact, partitioned plans and trees with fewer than two revolute joints
-// keep one lane. PHZ_LANES=1 turns the split off.
+// runs at the latency of its own instruction stream: such launches can give
+// each world 2 or 4 lanes that split the revolute joints' sincos (see
+// trig_prepass in phz_device.h). Every lane still runs the rest of the step,
+// so the split pays only where the sincos is a large share of it. Measured on
+// MI355X (event time per 200- or 100-step span against PHZ_LANES=1):
+//  - two revolute joints (the double pendulum, 2 lanes): 7-15% faster at
+//    1024-32768 worlds in f64 and in f32, where the split waves fit one per
+//    SIMD;
+//  - chain7 (4 lanes): f32, whose sincos is the hardware's, 6-17% slower at
+//    every size from 1024 to 16384 worlds; f64 (table sincos) 4-6% faster up
+//    to 4096 worlds (one split wave per CU), even at 8192, 9% slower at 16384.
+// So 2 lanes go wherever the split waves fit one per SIMD, 4 lanes only to f64
+// kernels whose split waves fit one per CU. Contact, partitioned plans and
+// trees with fewer than two revolute joints keep one lane. PHZ_LANES=1 turns
+// the split off; PHZ_LANES=2 or 4 (any value above 1) splits wherever the
+// model allows it, whatever the size and precision (tests, tuning).
 int lanes_per_world(const ModelD& m, const Features& f, const Plan& pl) {
-  if (const char* e = std::getenv("PHZ_LANES"))
+  bool forced = false;
+  if (const char* e = std::getenv("PHZ_LANES")) {
     if (std::atoi(e) <= 1) return 1;
+    forced = true;
+  }
   if (pl.mode != 0 || pl.groups.size() != 1 || f.contact) return 1;
   int nrev = 0;
   for (int i = 0; i < m.nb; i++) nrev += m.b[i].jtype == 0;
   if (nrev < 2) return 1;
   const int L = nrev == 2 ? 2 : 4;
-  if ((long)std::max(f.wgs, 1) * L > 4L * std::max(f.cus, 1)) return 1;
-  return L;
+  if (forced) return L;
+  const long waves = (long)std::max(f.wgs, 1) * L, cus = std::max(f.cus, 1);
+  if (L == 2) return waves <= 4 * cus ? 2 : 1;
+  return f.f64 && waves <= cus ? 4 : 1;
 }
 
 // Whether body i's joint-space inertia D = S^T I_A S + (armature + dt

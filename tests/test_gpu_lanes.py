@@ -1,10 +1,13 @@
 """Split-lane step kernels (small launches give each world 2 or 4 lanes that
 share its revolute joints' sincos) against the one-lane kernel of the same
-size (PHZ_LANES=1). The two compilations may fuse a product into a different
-fma, so they agree to rounding, not bit for bit: f64 rollouts within 1e-9, and
-one step's accelerations from a late state within 1e-12 (f64) and 1e-5 (f32)
-relative. The oracle comparisons of configs 1 and 2 at 200 and 256 worlds
-(test_gpu_parity.py, test_gpu_divergence.py) run split-lane kernels."""
+size (PHZ_LANES=1). The split kernel is forced (PHZ_LANES=2 or 4) so that the
+f32 four-lane kernel, which the library itself does not choose, stays covered.
+The two compilations may fuse a product into a different fma, so they agree
+to rounding, not bit for bit: f64 rollouts within 1e-9, and one step's
+accelerations from a late state within 1e-12 (f64) and 1e-5 (f32) relative.
+The oracle comparisons of configs 1 and 2 at 200 and 256 worlds
+(test_gpu_parity.py, test_gpu_divergence.py) run split-lane kernels in f64
+and, for config 1, in f32."""
 import os
 
 import numpy as np
@@ -17,9 +20,8 @@ from tests.helpers import as_precision, rel_err_rows
 pytestmark = pytest.mark.gpu
 
 
-def _sim(w, prec, n, lanes_off):
-    if lanes_off:
-        os.environ["PHZ_LANES"] = "1"
+def _sim(w, prec, n, lanes):
+    os.environ["PHZ_LANES"] = str(lanes)
     try:
         sim = from_workload(w, prec, nworld=n)
         sim.compile()
@@ -33,7 +35,7 @@ def _sim(w, prec, n, lanes_off):
 def test_split_lanes_match_one_lane(cfg, n, lanes, prec):
     w = W.config(cfg)
     steps = 500 if cfg == 1 else 200
-    split, one = _sim(w, prec, n, False), _sim(w, prec, n, True)
+    split, one = _sim(w, prec, n, lanes), _sim(w, prec, n, 1)
     assert (split.kernel_info()["lanes_per_world"], one.kernel_info()["lanes_per_world"]) == (lanes, 1)
     q, v, c, tg = w.initial_state(n)
     q, v, c = (as_precision(a, prec) for a in (q, v, c))

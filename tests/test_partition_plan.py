@@ -114,21 +114,33 @@ def test_f64_never_merges_subtrees(index, block, monkeypatch):
     assert s64.kernel_info()["block"] == block
 
 
-@pytest.mark.parametrize("index,nworld,lanes", [
-    (1, 4096, 2),     # double pendulum, 64 workgroups: two lanes per world
-    (2, 1024, 4),     # chain7 at 1024 worlds: four lanes
-    (2, 65536, 1),    # chain7 at 65536 worlds fills the SIMDs already
-    (3, 1024, 1),     # contact keeps one lane
+@pytest.mark.parametrize("index,nworld,prec,lanes", [
+    (1, 4096, "f64", 2),     # double pendulum, 64 workgroups: two lanes per world
+    (1, 4096, "f32", 2),     # in f32 too
+    (1, 32768, "f64", 2),    # 1024 split waves: one per SIMD
+    (1, 65536, "f64", 1),    # beyond one per SIMD
+    (2, 1024, "f64", 4),     # chain7 at 1024 worlds: four lanes
+    (2, 4096, "f64", 4),     # 256 split waves: one per CU
+    (2, 8192, "f64", 1),     # 512 split waves: one lane
+    (2, 1024, "f32", 1),     # f32 chain7 never splits (hardware sincos)
+    (2, 65536, "f64", 1),    # chain7 at 65536 worlds fills the SIMDs already
+    (3, 1024, "f64", 1),     # contact keeps one lane
 ])
-def test_lanes_per_world(index, nworld, lanes, monkeypatch):
-    """Small launches split each world's revolute-joint sincos over 2 or 4
-    lanes when the split waves still fit one per SIMD; PHZ_LANES=1 turns the
-    split off."""
+def test_lanes_per_world(index, nworld, prec, lanes, monkeypatch):
+    """Small launches split each world's revolute-joint sincos over 2 lanes
+    (two revolute joints) while the split waves fit one per SIMD, and over 4
+    lanes only in f64 while they fit one per CU (the measured rule in
+    lanes_per_world); PHZ_LANES=1 turns the split off, and PHZ_LANES=4 forces
+    it wherever the model allows it."""
     monkeypatch.delenv("PHZ_LANES", raising=False)
-    s = from_workload(W.config(index), "f64", nworld=nworld, device=-1)
+    s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
     s.compile()
     assert s.kernel_info()["lanes_per_world"] == lanes
     monkeypatch.setenv("PHZ_LANES", "1")
-    s = from_workload(W.config(index), "f64", nworld=nworld, device=-1)
+    s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
     s.compile()
     assert s.kernel_info()["lanes_per_world"] == 1
+    monkeypatch.setenv("PHZ_LANES", "4")
+    s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
+    s.compile()
+    assert s.kernel_info()["lanes_per_world"] == {1: 2, 2: 4, 3: 1}[index]
