@@ -180,9 +180,12 @@ int phz_compile(phz_sim* sim);
  * execution time from the first start to the last end, without the dispatch
  * around them. */
 int phz_time_step_many(phz_sim* sim, uint32_t n, uint32_t reps, double* ms_per_rep);
-/* Kernel resource use of the compiled step kernel: [0] VGPRs per lane (arch),
- * [1] AGPRs, [2] SGPRs, [3] private (scratch) bytes per lane, [4] block size,
- * [5] max steps per launch. */
+/* Kernel resource use of the compiled step kernel that a launch of [5] steps
+ * runs: [0] VGPRs per lane (arch), [1] AGPRs, [2] SGPRs, [3] private
+ * (scratch) bytes per lane, [4] block size, [5] max steps per launch. A large
+ * launch of a kernel above 256 registers may run a second build of the same
+ * arithmetic for two resident waves per SIMD (spilling to scratch) in its
+ * launches of 16 steps or more; shorter launches run the one-wave build. */
 int phz_kernel_info(phz_sim* sim, int64_t* info);
 /* Lanes per world of the compiled step kernel: 1, or 2 or 4 when a small
  * launch splits each world's revolute-joint sincos over several lanes; -1 on

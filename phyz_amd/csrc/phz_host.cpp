@@ -57,6 +57,11 @@ constexpr int kBodyStride = PHZ_BODY_STRIDE;
 constexpr int kGeomStride = PHZ_GEOM_STRIDE;
 constexpr int kPdStride = PHZ_PD_DOF_STRIDE;
 constexpr int kMaxBodies = PHZ_MAX_BODIES;
+// Launches of at least this many steps run the two-waves-per-SIMD build of the
+// step kernel where there is one (phz_sim::two_waves_pay): it saves about 1.4
+// us per step at 131072 ant worlds and costs about 14 us more per launch, so
+// it breaks even near 10 steps.
+constexpr int kTwoWaveMinSteps = 16;
 
 thread_local std::string g_create_error;
 
@@ -862,7 +867,10 @@ std::string gen_model(const ModelD& m, const Features& f) {
 }
 
 // One workgroup = NG waves over the same 64 worlds; wave g runs group g.
-std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups, int* lanes) {
+// two_waves: ask the compiler for two resident waves per SIMD (at most 256
+// registers per lane, spilling what does not fit).
+std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroups, int* lanes,
+                       bool two_waves = false) {
   const Plan pl = plan_partition(m, f);
   const int ng = (int)pl.groups.size();
   *ngroups = ng;
@@ -871,7 +879,8 @@ std::string gen_source(const ModelD& m, const Features& f, bool f64, int* ngroup
   std::string s = kDeviceSrc;
   s += "\n// ---- model-specialised instantiation ----\n";
   s += gen_model(m, f);
-  s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(64 * ng) + ") phz_step(phz::StepArgs a) {\n";
+  s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(64 * ng) + ")" +
+       (two_waves ? " __attribute__((amdgpu_waves_per_eu(2, 2)))" : "") + " phz_step(phz::StepArgs a) {\n";
   s += "  __shared__ " + T + " lds[(Model::NSLOT > 0 ? Model::NSLOT : 1) * 64];\n";
   s += "  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n";
   s += "  const int lane = threadIdx.x & 63;\n";
@@ -1314,6 +1323,11 @@ struct phz_sim {
   std::shared_ptr<CodeObject> code;
   hipModule_t module = nullptr;
   hipFunction_t fn = nullptr;
+  // The same kernel built for two resident waves per SIMD (two_waves_pay),
+  // for launches of at least kTwoWaveMinSteps steps; null where it does not pay.
+  std::shared_ptr<CodeObject> code2;
+  hipModule_t module2 = nullptr;
+  hipFunction_t fn2 = nullptr;
   bool graphs = true;
   hipGraphExec_t gexec = nullptr;
   uint32_t graph_steps = 0;
@@ -1359,7 +1373,9 @@ struct phz_sim {
     if (stream) hipStreamSynchronize(stream);  // nothing in flight uses the modules unloaded below
     drop_graph();
     if (module) { hipModuleUnload(module); module = nullptr; fn = nullptr; }
+    if (module2) { hipModuleUnload(module2); module2 = nullptr; fn2 = nullptr; }
     code.reset();
+    code2.reset();
     epoch++;
     ctl_epoch++;
   }
@@ -1410,15 +1426,53 @@ struct phz_sim {
     if (f64 && feat.cmode == 1) {
       code = compile_source(src, Build::Ieee, e);
     } else {
-      code = compile_source(src, Build::Reassoc, e);
-      if (code && remark_value(code->log, "ScratchSize [bytes/lane]:") > 0) code = compile_source(src, Build::Finite, e);
+      Build b = Build::Reassoc;
+      code = compile_source(src, b, e);
+      if (code && remark_value(code->log, "ScratchSize [bytes/lane]:") > 0) {
+        b = Build::Finite;
+        code = compile_source(src, b, e);
+      }
+      if (code && ng == 1 && two_waves_pay(code->log)) {
+        // The same build (the same arithmetic: a launch gives the same bits
+        // whichever of the two runs it), kept while its spills stay small.
+        int ng2 = 1, lanes2 = 1;
+        std::string e2;
+        auto c2 = compile_source(gen_source(model, feat, f64, &ng2, &lanes2, true), b, e2);
+        const int64_t sc = c2 ? remark_value(c2->log, "ScratchSize [bytes/lane]:") : -1;
+        if (sc >= 0 && sc <= (f64 ? 128 : 512)) code2 = c2;
+      }
     }
     if (!code) { err = e; return false; }
     return true;
   }
+  // Whether the one-wave-per-world-group kernel compiled to `log` gets a
+  // second build for two resident waves per SIMD: it holds more than 256
+  // registers (one wave per SIMD), and the launch has more waves than the
+  // device has SIMDs, so that at one per SIMD they run in rounds with nothing
+  // to cover a wave's latencies. The rebuild spills registers to scratch and
+  // pays a fixed cost per launch (about 14 us more at 131072 ant worlds), so
+  // launches of fewer than kTwoWaveMinSteps steps keep the one-wave kernel.
+  // Measured on MI355X (ms per 1000 steps, one launch): the ant at 131072
+  // worlds 9.03 -> 7.22 (404 B of spills per lane), at 98304 9.16 -> 7.59, at
+  // 262144 18.02 -> 14.22, but 4.54 -> 4.94 at 65536 (one wave per SIMD either
+  // way); the MJCF ant 16.30 -> 16.54 (960 B, not taken); chain7 f64 at 131072
+  // 6.51 -> 8.46 (284 B of 8-byte spills, not taken). Per launch at 131072
+  // ant worlds: 1 step 21.2 -> 33.8 us, 5 steps 62.2 -> 65.6, 20 steps 210.6
+  // -> 191.2. PHZ_TWO_WAVES=0 keeps one wave per SIMD.
+  bool two_waves_pay(const std::string& log) const {
+    if (const char* e = std::getenv("PHZ_TWO_WAVES"))
+      if (e[0] == '0') return false;
+    const int64_t regs = remark_value(log, "VGPRs:") + std::max<int64_t>(remark_value(log, "AGPRs:"), 0);
+    const long waves = (long)std::max(feat.wgs, 1) * lanes;
+    return regs > 256 && waves > 4L * std::max(feat.cus, 1);
+  }
   bool load_kernel() {
     if (fn) return true;
     if (!compile()) return false;
+    if (code2) {
+      if (!hip_ok(hipModuleLoadData(&module2, code2->code.data()), "hipModuleLoadData")) return false;
+      if (!hip_ok(hipModuleGetFunction(&fn2, module2, "phz_step"), "hipModuleGetFunction")) return false;
+    }
     if (!hip_ok(hipModuleLoadData(&module, code->code.data()), "hipModuleLoadData")) return false;
     return hip_ok(hipModuleGetFunction(&fn, module, "phz_step"), "hipModuleGetFunction");
   }
@@ -1430,6 +1484,7 @@ struct phz_sim {
                stride,  nsteps,  feat.contact ? 1 : 0};
     void* params[] = {&a};
     const unsigned grid = (unsigned)(((long)nworld * lanes + 63) / 64);
+    hipFunction_t fn = fn2 && nsteps >= kTwoWaveMinSteps ? fn2 : this->fn;
     if (start || stop) {
       // hipExtModuleLaunchKernel takes the grid in work-items (32 bits);
       // beyond that the events bracket the launch on the stream instead.
@@ -1622,6 +1677,7 @@ struct phz_sim {
       if (stream) hipStreamSynchronize(stream);
       drop_graph();
       if (module) hipModuleUnload(module);
+      if (module2) hipModuleUnload(module2);
       obs_k.reset();
       pol_k.reset();
       free_policy_buffers();
@@ -2297,7 +2353,7 @@ int phz_lanes_per_world(phz_sim* s) {
 int phz_kernel_info(phz_sim* s, int64_t* info) {
   if (!s || !info) return 1;
   if (!s->compile()) return 1;
-  const std::string& log = s->code->log;
+  const std::string& log = (s->code2 ? s->code2 : s->code)->log;
   info[0] = remark_value(log, "VGPRs:");
   info[1] = remark_value(log, "AGPRs:");
   info[2] = remark_value(log, "SGPRs:");
