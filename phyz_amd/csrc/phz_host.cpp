@@ -1433,13 +1433,32 @@ struct phz_sim {
         code = compile_source(src, b, e);
       }
       if (code && ng == 1 && two_waves_pay(code->log)) {
-        // The same build (the same arithmetic: a launch gives the same bits
-        // whichever of the two runs it), kept while its spills stay small.
+        // The same build as the one-wave kernel (the same arithmetic: a launch
+        // gives the same bits whichever of the two runs it), kept while its
+        // spills stay small: 512 bytes per lane reassociated, 768 in order,
+        // 128 in f64. An f32 kernel whose reassociated rebuild spills more
+        // takes the in-order build for both kernels when that rebuild fits.
         int ng2 = 1, lanes2 = 1;
+        const std::string src2 = gen_source(model, feat, f64, &ng2, &lanes2, true);
+        auto spills = [](const std::shared_ptr<CodeObject>& c) {
+          return c ? remark_value(c->log, "ScratchSize [bytes/lane]:") : (int64_t)-1;
+        };
+        auto fits = [&](const std::shared_ptr<CodeObject>& c, Build bb) {
+          const int64_t sc = spills(c);
+          return sc >= 0 && sc <= (f64 ? 128 : bb == Build::Reassoc ? 512 : 768);
+        };
         std::string e2;
-        auto c2 = compile_source(gen_source(model, feat, f64, &ng2, &lanes2, true), b, e2);
-        const int64_t sc = c2 ? remark_value(c2->log, "ScratchSize [bytes/lane]:") : -1;
-        if (sc >= 0 && sc <= (f64 ? 128 : 512)) code2 = c2;
+        auto c2 = compile_source(src2, b, e2);
+        if (fits(c2, b)) {
+          code2 = c2;
+        } else if (!f64 && b == Build::Reassoc) {
+          auto c2f = compile_source(src2, Build::Finite, e2);
+          auto c1f = fits(c2f, Build::Finite) ? compile_source(src, Build::Finite, e2) : nullptr;
+          if (c1f && spills(c1f) == 0) {
+            code = c1f;
+            code2 = c2f;
+          }
+        }
       }
     }
     if (!code) { err = e; return false; }
@@ -1455,10 +1474,13 @@ struct phz_sim {
   // Measured on MI355X (ms per 1000 steps, one launch): the ant at 131072
   // worlds 9.03 -> 7.22 (404 B of spills per lane), at 98304 9.16 -> 7.59, at
   // 262144 18.02 -> 14.22, but 4.54 -> 4.94 at 65536 (one wave per SIMD either
-  // way); the MJCF ant 16.30 -> 16.54 (960 B, not taken); chain7 f64 at 131072
-  // 6.51 -> 8.46 (284 B of 8-byte spills, not taken). Per launch at 131072
-  // ant worlds: 1 step 21.2 -> 33.8 us, 5 steps 62.2 -> 65.6, 20 steps 210.6
-  // -> 191.2. PHZ_TWO_WAVES=0 keeps one wave per SIMD.
+  // way); the MJCF ant reassociated 16.30 -> 16.54 (960 B, not taken), in
+  // order 17.39 -> 12.91 (612 B: both kernels in order, its 1- and 5-step
+  // launches 6% slower than the reassociated one-wave kernel); chain7 f64 at
+  // 131072 6.51 -> 8.46 (284 B of 8-byte spills, not taken). Per launch at
+  // 131072 ant worlds: 1 step 21.2 -> 33.8 us, 5 steps 62.2 -> 65.6, 20 steps
+  // 210.6 -> 191.2. PHZ_TWO_WAVES=0 keeps one wave per SIMD (and the
+  // reassociated build).
   bool two_waves_pay(const std::string& log) const {
     if (const char* e = std::getenv("PHZ_TWO_WAVES"))
       if (e[0] == '0') return false;

@@ -1,11 +1,14 @@
 """The two-waves-per-SIMD build of a step kernel (a one-wave-per-world-group
-kernel above 256 registers, in a launch with more waves than SIMDs: the ant at
-131072 worlds) runs launches of 16 steps or more; shorter launches run the
-one-wave build. Both are the same build of the same source, so the rebuild
-only spills registers and changes no arithmetic: a span gives the same bits
-however it is split into launches, and the same bits as the one-wave kernel
-alone (PHZ_TWO_WAVES=0). From the late state the two-wave launches reach, one
-more step meets the f32 oracle bound of 1e-4 on 256 sampled worlds."""
+kernel above 256 registers, in a launch with more waves than SIMDs: the ant
+and the MJCF ant at 131072 worlds) runs launches of 16 steps or more; shorter
+launches run the one-wave build. Both are the same build of the same source,
+so the rebuild only spills registers and changes no arithmetic: a span gives
+the same bits however it is split into launches. The ant's pair is its
+reassociated build, so it also matches the one-wave kernel alone
+(PHZ_TWO_WAVES=0) bit for bit; the MJCF ant's pair is the in-order build,
+which PHZ_TWO_WAVES=0 replaces by the reassociated one. From the late state
+the two-wave launches reach, one more step meets the f32 oracle bound of 1e-4
+on 256 sampled worlds."""
 import os
 
 import numpy as np
@@ -29,10 +32,11 @@ def _sim(w, n, one_wave):
     return sim
 
 
-def test_two_wave_build_same_bits_and_oracle():
-    w = W.config(3)
+@pytest.mark.parametrize("cfg,same_as_one_wave", [(3, True), (7, False)])
+def test_two_wave_build_same_bits_and_oracle(cfg, same_as_one_wave):
+    w = W.config(cfg)
     n, steps = 131072, 320
-    print(f"ant f32: {n} worlds, {steps} steps as one launch, as 20 launches of 16 and as 64 of 5", flush=True)
+    print(f"{w.name} f32: {n} worlds, {steps} steps as one launch, as 20 launches of 16 and as 64 of 5", flush=True)
     two, one = _sim(w, n, False), _sim(w, n, True)
     i2, i1 = two.kernel_info(), one.kernel_info()
     assert i2["vgpr"] + max(i2["agpr"], 0) <= 256 and i2["scratch_bytes"] > 0
@@ -50,6 +54,12 @@ def test_two_wave_build_same_bits_and_oracle():
         qg, vg = sim.readback_states()
         outs.append((qg, vg, sim.readback_rng()))
     for k, name in ((1, "16-step launches"), (2, "5-step launches"), (3, "one-wave kernel")):
+        if k == 3 and not same_as_one_wave:
+            # Another build (rounding differs): the same random stream, and the worlds stay finite.
+            assert np.array_equal(outs[k][2], outs[0][2]), name
+            ok = np.isfinite(outs[0][0]).all(axis=1) & np.isfinite(outs[k][0]).all(axis=1)
+            assert ok.mean() > 0.99
+            continue
         assert np.array_equal(outs[k][0], outs[0][0], equal_nan=True), name
         assert np.array_equal(outs[k][1], outs[0][1], equal_nan=True), name
         assert np.array_equal(outs[k][2], outs[0][2]), name

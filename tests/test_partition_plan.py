@@ -150,7 +150,8 @@ def test_lanes_per_world(index, nworld, prec, lanes, monkeypatch):
     (3, 131072, "f32", True),    # ant: 2048 waves over 1024 SIMDs, 356 registers
     (3, 262144, "f32", True),
     (3, 65536, "f32", False),    # one wave per SIMD either way
-    (7, 131072, "f32", False),   # MJCF ant: its two-wave build spills 960 bytes per lane
+    (7, 131072, "f32", True),    # MJCF ant: both kernels in order (reassociated: 960 bytes of spills)
+    (7, 65536, "f32", False),
     (2, 131072, "f64", False),   # chain7 f64: 284 bytes of 8-byte spills
     (2, 65536, "f64", False),
     (2, 262144, "f32", False),   # chain7 f32 already fits two waves per SIMD
@@ -160,7 +161,8 @@ def test_two_waves_per_simd(index, nworld, prec, two, monkeypatch):
     """A one-wave-per-world-group kernel above 256 registers gets a second
     build of the same arithmetic for two resident waves per SIMD (run by
     launches of 16 steps or more) when the launch has more waves than SIMDs
-    and the rebuild spills at most 512 bytes per lane (f32; 128 for f64);
+    and the rebuild spills at most 512 bytes per lane (f32 reassociated; 768
+    in order, which then builds both kernels in order; 128 for f64);
     kernel_info reports the kernel of a full launch. PHZ_TWO_WAVES=0 keeps
     one wave per SIMD."""
     monkeypatch.delenv("PHZ_TWO_WAVES", raising=False)
@@ -169,7 +171,7 @@ def test_two_waves_per_simd(index, nworld, prec, two, monkeypatch):
     info = s.kernel_info()
     assert (info["vgpr"] + max(info["agpr"], 0) <= 256 and info["scratch_bytes"] > 0) == two
     if two:
-        assert info["scratch_bytes"] <= 512
+        assert info["scratch_bytes"] <= 768
         monkeypatch.setenv("PHZ_TWO_WAVES", "0")
         s = from_workload(W.config(index), prec, nworld=nworld, device=-1)
         s.compile()
