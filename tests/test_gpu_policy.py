@@ -335,3 +335,35 @@ def test_nan_world_stays_in_its_world():
     assert np.array_equal(res[0][0][:, keep], res[1][0][:, keep])
     assert np.array_equal(res[0][1][:, keep], res[1][1][:, keep])
     assert np.isnan(res[1][1][0, 17]).any()
+
+
+def test_two_wave_policy_kernel_same_bits():
+    """At 131072 worlds (4096 policy waves over 1024 SIMDs) the policy kernel
+    is built for two resident waves per SIMD; the same build of the same
+    source, so a rollout's observations, actions, log-probs, targets and
+    states equal the one-wave kernel's (PHZ_TWO_WAVES=0) bit for bit."""
+    import os
+    from phyz_amd import workloads as W
+    from phyz_amd.sim import from_control_loop
+    cl = W.control_loop()
+    n = 131072
+    outs, infos = [], []
+    for one_wave in (False, True):
+        if one_wave:
+            os.environ["PHZ_TWO_WAVES"] = "0"
+        try:
+            sim = from_control_loop(cl, "f32", nworld=n)
+            q, v, _, _ = cl.base.initial_state(n)
+            sim.load_states(q, v)
+            sim.seed_policy(cl.seed)
+            infos.append(sim.control_kernel_info("policy"))
+            sim.rollout(0, 3, cl.control_every, True)
+        finally:
+            os.environ.pop("PHZ_TWO_WAVES", None)
+        outs.append(sim.readback_policy_history(0, 3) + sim.readback_state_history(0, 3) + (sim.readback_targets(),))
+        sim.close()
+    print(f"policy kernels: {infos}", flush=True)
+    assert infos[0]["scratch_bytes"] > 0 and infos[0]["vgpr"] + max(infos[0]["agpr"], 0) <= 256
+    assert infos[1]["scratch_bytes"] == 0 and infos[1]["vgpr"] + infos[1]["agpr"] > 256
+    for x, y in zip(outs[0], outs[1]):
+        assert np.array_equal(x, y, equal_nan=True)

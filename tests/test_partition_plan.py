@@ -177,3 +177,19 @@ def test_two_waves_per_simd(index, nworld, prec, two, monkeypatch):
         s.compile()
         one = s.kernel_info()
         assert one["vgpr"] + one["agpr"] > 256 and one["scratch_bytes"] == 0
+
+
+@pytest.mark.parametrize("nworld,two", [(131072, True), (32768, False)])
+def test_two_wave_policy_kernel(nworld, two, monkeypatch):
+    """The control loop's policy kernel (about 370 registers at hidden 256) is
+    built for two resident waves per SIMD when the launch has more waves than
+    SIMDs (131072 worlds: 4096 waves of 32 worlds), spilling at most 512 bytes
+    per lane; PHZ_TWO_WAVES=0 keeps one."""
+    from phyz_amd.sim import from_control_loop
+    monkeypatch.delenv("PHZ_TWO_WAVES", raising=False)
+    info = from_control_loop(W.control_loop(), "f32", nworld=nworld, device=-1).control_kernel_info("policy")
+    assert (info["scratch_bytes"] > 0) == two
+    assert info["scratch_bytes"] <= 512
+    monkeypatch.setenv("PHZ_TWO_WAVES", "0")
+    info = from_control_loop(W.control_loop(), "f32", nworld=nworld, device=-1).control_kernel_info("policy")
+    assert info["scratch_bytes"] == 0 and info["vgpr"] + info["agpr"] > 256
