@@ -796,8 +796,11 @@ std::string gen_model(const ModelD& m, const Features& f) {
   // Not for an f64 kernel of several waves: the MJCF humanoid's four-wave
   // f64 kernel without the branch returned non-finite worlds on gfx950 where
   // its host emulation (ASan, TSan, finite-math -O3) and the oracle agree.
-  // PHZ_PIVOT_BOUND=0 keeps the test everywhere (tuning, tests).
-  const bool multi_f64 = f.f64 && pl.groups.size() > 1;
+  // PHZ_PIVOT_BOUND=0 keeps the test everywhere (tuning, tests). A host-only
+  // sim with PHZ_HOST_LIFT_PIVOT=1 generates the refused kernel (for the host
+  // emulation, as PHZ_HOST_LIFT_GUARDS does for the refused plans).
+  const char* lift_env = std::getenv("PHZ_HOST_LIFT_PIVOT");
+  const bool multi_f64 = f.f64 && pl.groups.size() > 1 && !(f.host_only && lift_env && lift_env[0] == '1');
   const char* pb_env = std::getenv("PHZ_PIVOT_BOUND");
   const bool pb_off = pb_env && pb_env[0] == '0';
   bb("piv_ok", [&](int i) { return !multi_f64 && !pb_off && pivots_bounded(m, i, f.f64); });

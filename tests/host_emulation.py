@@ -20,6 +20,10 @@ waves as G host threads:
     take turns, v_rcp / v_rsq are reciprocals, v_cvt_i32 saturates and maps
     NaN to 0).
 
+build_device_ir runs, through the same driver, the device compiler's own
+optimised IR of the source (compiled for gfx950, rewritten for x86-64): the
+IR that reaches the AMDGPU back end, checked against the oracle.
+
 Builds: "asan" (AddressSanitizer + UndefinedBehaviorSanitizer, every
 automatic variable initialised to a NaN pattern so that a read before a
 write poisons the result, and the FP traps for invalid operations and
@@ -280,3 +284,118 @@ def run(exe: str, prec: str, waves: int, q: np.ndarray, v: np.ndarray, ctrl: np.
     qddo = arr[n1 + n2:].reshape(nv, stride)[:, :nworld].T.astype(np.float64)
     ro = np.frombuffer(raw[(n1 + 2 * n2) * np.dtype(dt).itemsize:], dtype=np.uint64)[:nworld]
     return qo, vo, qddo, ro, p.stderr
+
+
+# ── The device compiler's own optimised IR, run on the host ─────────────────
+# The step source compiled for gfx950 to LLVM IR (the optimisation pipeline's
+# output under the library's flags, before the AMDGPU back end), rewritten for
+# x86-64 and linked into the driver above. It tells whether a device failure
+# is already in the IR the AMDGPU pipeline produced: if this run matches the
+# oracle, every IR pass (SROA, instcombine, the target-aware ones) kept the
+# source's meaning, and the difference arises in the back end or on the device.
+# The rewrite: address spaces dropped (every pointer is a plain host pointer;
+# the kernel argument block is passed by pointer), the f64 tables made plain
+# globals that the driver fills, and the few AMDGPU intrinsics and inline asm
+# statements of the step kernel given host meanings (work-item ids, uniform
+# reads, the barrier, v_rcp/v_rsq as exact reciprocals, the saturating
+# conversions; the empty asm statements that pin a value in a register stay
+# empty asm statements on x86 registers).
+X86_LAYOUT = 'e-m:e-p270:32:32-p271:32:32-p272:64:64-i64:64-i128:128-f80:128-n8:16:32:64-S128'
+DEVICE_IR_FLAGS = {
+    "finite": ["-O3", "-ffinite-math-only", "-fno-signed-zeros"],
+    "reassoc": ["-O3", "-ffinite-math-only", "-fno-signed-zeros", "-DPHZ_REASSOC=1"],
+    "ieee": ["-O3", "-fno-signed-zeros"],
+}
+IR_INTRINSICS = (("llvm.amdgcn.workitem.id.x", "irx_tid"), ("llvm.amdgcn.workgroup.id.x", "irx_bid"),
+                 ("llvm.amdgcn.readfirstlane.i32", "irx_rfl"), ("llvm.amdgcn.s.barrier", "irx_barrier"),
+                 ("llvm.amdgcn.rcp.f64", "irx_rcp"), ("llvm.amdgcn.rsq.f64", "irx_rsq"))
+IR_SHIMS = r"""
+extern "C" void phz_step_ir(const void*);
+extern "C" double irx_sc_tab[128], irx_log_tab[128];
+extern "C" unsigned irx_tid() { return threadIdx.x; }
+extern "C" unsigned irx_bid() { return blockIdx.x; }
+extern "C" int irx_rfl(int x) { return x; }
+extern "C" void irx_barrier() { emu_syncthreads(); }
+extern "C" double irx_rcp(double x) { return 1.0 / x; }
+extern "C" double irx_rsq(double x) { return 1.0 / std::sqrt(x); }
+extern "C" int irx_cvt_f64(double x) { return emu_cvt_sat(x); }
+extern "C" int irx_cvt_f32(float x) { return emu_cvt_sat(x); }
+"""
+
+
+def device_ir_for_host(ir: str) -> str:
+    """gfx950 IR of the step kernel rewritten for x86-64 (see above)."""
+    out = []
+    for line in ir.split("\n"):
+        if line.startswith("target datalayout"):
+            line = f'target datalayout = "{X86_LAYOUT}"'
+        elif line.startswith("target triple"):
+            line = 'target triple = "x86_64-unknown-linux-gnu"'
+        elif line.startswith(("@__hip_cuid", "@llvm.compiler.used", "!llvm.module.flags")):
+            continue
+        elif line.startswith("attributes #"):
+            line = re.sub(r"= \{.*\}", "= { nounwind }", line)
+        out.append(line)
+    ir = "\n".join(out)
+    ir = re.sub(r" addrspace\(\d\)", "", ir)
+    ir = re.sub(r"(%[\w.]+) = addrspacecast ptr (%[\w.]+) to ptr", r"\1 = getelementptr i8, ptr \2, i64 0", ir)
+    assert "addrspacecast" not in ir, "an address-space cast the rewrite does not handle"
+    ir = ir.replace("amdgpu_kernel ", "")
+    ir = re.sub(r"byref\([^)]*\) ", "", ir)
+    ir = re.sub(r'syncscope\("[a-z-]*"\) ', "", ir)
+    ir = ir.replace("@phz_step(", "@phz_step_ir(")
+    for name, host in (("_ZN3phz10phz_sc_tabE", "irx_sc_tab"), ("_ZN3phz11phz_log_tabE", "irx_log_tab")):
+        ir = re.sub(rf"@{name} = [^\n]*global \[128 x double\] undef", f"@{host} = global [128 x double] zeroinitializer", ir)
+        ir = ir.replace("@" + name, "@" + host)
+    for dev, host in IR_INTRINSICS:
+        ir = ir.replace("@" + dev + "(", "@" + host + "(")
+    left = set(re.findall(r"@llvm\.amdgcn\.[\w.]+", ir))
+    assert not left, f"AMDGPU intrinsics without a host meaning: {left}"
+    ir = re.sub(r"!amdgpu\.[\w.]+ !\d+", "", ir)
+    ir = ir.replace('asm "v_cvt_i32_f64 $0, $1", "=v,v"(', "@irx_cvt_f64(")
+    ir = ir.replace('asm "v_cvt_i32_f32 $0, $1", "=v,v"(', "@irx_cvt_f32(")
+    ir = re.sub(r'(double|float) asm sideeffect "", "=v,0"', r'\1 asm sideeffect "", "=x,0"', ir)
+    ir = re.sub(r'(i32|i64) asm sideeffect "", "=v,0"', r'\1 asm sideeffect "", "=r,0"', ir)
+    ir = ir.replace('asm sideeffect "", "=s,=s,0,1"', 'asm sideeffect "", "=r,=r,0,1"')
+    ir = ir.replace('asm sideeffect "", "=s,=s,=s,0,1,2"', 'asm sideeffect "", "=r,=r,=r,0,1,2"')
+    assert not re.search(r'"=[vs]', ir), "an inline asm statement the rewrite does not handle"
+    return ir + "\ndeclare i32 @irx_cvt_f64(double)\ndeclare i32 @irx_cvt_f32(float)\n"
+
+
+def build_device_ir(device_src: str, prec: str, build: str) -> str:
+    """Compile `device_src` for gfx950 to optimised IR under the library's
+    `build` flags (finite, reassoc, ieee), run it on the host through the
+    driver; returns the executable's path (cached by content)."""
+    key = hashlib.sha1((device_src + prec + build + " ".join(DEVICE_IR_FLAGS[build])).encode()).hexdigest()[:16]
+    os.makedirs(CACHE, exist_ok=True)
+    base = os.path.join(CACHE, f"ir_{key}_{build}")
+    exe = base + ".exe"
+    if os.path.exists(exe):
+        return exe
+    with open(base + ".hip", "w") as f:
+        f.write(device_src)
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "-std=c++17", *DEVICE_IR_FLAGS[build],
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                        "-emit-llvm", base + ".hip", "-o", base + ".ll"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"device IR build failed:\n{r.stderr[-4000:]}")
+    with open(base + "_x86.ll", "w") as f:
+        f.write(device_ir_for_host(open(base + ".ll").read()))
+    r = subprocess.run([CLANG, "-O0", "-c", base + "_x86.ll", "-o", base + ".o"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host codegen of the device IR failed:\n{r.stderr[-4000:]}")
+    drv = host_source(device_src, prec)
+    drv = drv.replace("  phz_step(j->a);", "  phz_step_ir(&j->a);")
+    drv = drv.replace("struct EmuJob {", IR_SHIMS + "struct EmuJob {")
+    drv = drv.replace("int main(int argc, char** argv) {", "int main(int argc, char** argv) {\n"
+                      "  phz::fill_tables(0);\n"
+                      "  memcpy(irx_sc_tab, phz::phz_sc_tab, sizeof(irx_sc_tab));\n"
+                      "  memcpy(irx_log_tab, phz::phz_log_tab, sizeof(irx_log_tab));")
+    with open(base + "_drv.cpp", "w") as f:
+        f.write(drv)
+    r = subprocess.run([CLANG, "-x", "c++", "-std=c++17", "-O1", base + "_drv.cpp", "-x", "none", base + ".o",
+                        "-o", exe + ".tmp", "-lpthread"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"driver build failed:\n{r.stderr[-4000:]}")
+    os.replace(exe + ".tmp", exe)
+    return exe

@@ -22,6 +22,7 @@ lie in how the source is compiled for gfx950 or run there, and the plans stay
 refused on the device.
 """
 import os
+import re
 
 import numpy as np
 import pytest
@@ -38,12 +39,14 @@ pytestmark = pytest.mark.skipif(not os.path.exists(HE.CLANG), reason="clang++ (R
 NOISE = (0xA55, 1, -0.03, 0.03)  # as tests/test_gpu_mjcf.py
 
 
-def mjcf_case(name, groups, prec="f64", n=64):
+def mjcf_case(name, groups, prec="f64", n=64, lift_pivot=False):
     m = W.mjcf_model(name)
     gains = uniform_frequency_gains(m, 50.0, 1.0)
     geom, _ = pack_geometries(m, gains=gains)
     os.environ["PHZ_HOST_LIFT_GUARDS"] = "1"
     os.environ["PHZ_MAX_GROUPS"] = str(groups)
+    if lift_pivot:
+        os.environ["PHZ_HOST_LIFT_PIVOT"] = "1"
     try:
         s = BatchSim(m, n, prec, device=-1)
         s.enable_ground_contact_per_body(0.0, 1.0, gains)
@@ -53,6 +56,7 @@ def mjcf_case(name, groups, prec="f64", n=64):
     finally:
         os.environ.pop("PHZ_HOST_LIFT_GUARDS", None)
         os.environ.pop("PHZ_MAX_GROUPS", None)
+        os.environ.pop("PHZ_HOST_LIFT_PIVOT", None)
     orc = Oracle(m, contact=(geom, 0.0, 1.0), noise=(*NOISE, list(range(m.nctrl()))))
     rng = np.random.default_rng(13)
     q = np.zeros((n, m.nq))
@@ -119,6 +123,60 @@ def test_f64_impulse_terrain_kernel_is_correct_on_the_host(mode):
     assert (rows[:, :, 0] > 0).any()  # contacts active in the compared step
     rel = np.abs(qdde - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-12)
     assert rel.max() <= 1e-12
+
+
+@pytest.mark.parametrize("build", ["finite", "reassoc"])
+def test_f64_impulse_device_ir_is_correct_on_the_host(build):
+    """The device compiler's own optimised IR of the f64 terrain + impulse
+    kernel under the finite-math flags (the build whose accelerations were
+    wrong by 1e5 on gfx950; the library builds this kernel IEEE), run on the
+    host from settled contact states: it matches the oracle, so the IR passes
+    kept the source's meaning."""
+    w = W.config(6)
+    n = 64
+    s = from_workload(w, "f64", nworld=n, device=-1)
+    src = HE.dump_source(s)
+    q, v, c, _ = w.initial_state(n)
+    orc = oracle_for(w)
+    nb = w.model.nbodies
+    e0, s0 = np.zeros((n, nb, 6)), np.zeros((n, nb, 56))
+    orc.step_batch(q, v, c, 300, rng=orc.rng_states(n), threads=8, ext_state=e0, cs_state=s0)
+    exe = HE.build_device_ir(src, "f64", build)
+    _, _, qdde, _, err = HE.run(exe, "f64", 1, q, v, c, orc.rng_states(n), 1, nb=nb, trap=False,
+                                heightfield=w.heightfield)
+    e1, s1 = np.zeros((n, nb, 6)), np.zeros((n, nb, 56))
+    want, rows = orc.step_batch(q.copy(), v.copy(), c.copy(), 1, rng=orc.rng_states(n), threads=8, ext_state=e1,
+                                cs_state=s1, want_contacts=True)
+    assert (rows[:, :, 0] > 0).any()
+    rel = np.abs(qdde - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-12)
+    assert rel.max() <= 1e-12, err[-2000:]
+
+
+@pytest.mark.parametrize("name,groups,build", [("humanoid", 2, "finite"), ("humanoid", 2, "reassoc"),
+                                               ("humanoid", 3, "reassoc"), ("humanoid", 4, "reassoc"),
+                                               ("humanoid", 4, "finite")])
+def test_refused_f64_plans_device_ir_on_the_host(name, groups, build):
+    """The refused f64 kernels from the device compiler's own optimised IR, run
+    on the host: the MJCF humanoid merged into 2 and 3 waves (NaN or
+    launch-varying values from multi-step launches on gfx950) and its 4-wave
+    plan with the static pivot bound (non-finite worlds on gfx950), 50 steps
+    each against the oracle: the same finite worlds, the same control stream,
+    states within 1e-12. What went wrong on the device is not in this IR."""
+    n, steps = 64, 50
+    m, src, block, orc, q, v, c = mjcf_case(name, groups, lift_pivot=groups == 4)
+    assert block == 64 * groups
+    if groups == 4:
+        assert re.search(r"piv_ok\[\d+\] = \{true(, true)*\}", src)  # the bound's kernel, every body bounded
+    exe = HE.build_device_ir(src, "f64", build)
+    qe, ve, _, re_, err = HE.run(exe, "f64", groups, q, v, c, orc.rng_states(n), steps, nb=m.nbodies, trap=False)
+    qo, vo, co = q.copy(), v.copy(), c.copy()
+    rng = orc.rng_states(n)
+    orc.step_batch(qo, vo, co, steps, rng=rng, threads=8)
+    fo, fe = finite_rows(qo, vo), finite_rows(qe, ve)
+    assert np.array_equal(fo, fe) and fo.mean() >= 0.9, err[-2000:]
+    assert np.array_equal(re_[fo], rng[fo])
+    assert np.abs(qe[fo] - qo[fo]).max() <= 1e-12
+    assert np.abs(ve[fo] - vo[fo]).max() <= 1e-12 * max(1.0, np.abs(vo[fo]).max())
 
 
 def device_math(call: str, words: np.ndarray, nout: int) -> np.ndarray:
