@@ -221,15 +221,53 @@ struct PolicyArgs {
 // angle. These 37 normals per world and control step are the part of the
 // policy kernel that does not overlap its MFMAs; the kernel fills the tables
 // at its start.
-__device__ __forceinline__ double policy_normal(u64& s) {
+__device__ __forceinline__ void policy_uniforms(u64& s, double& u1, double& t) {
   const u64 x1 = xorshift64(s);
   const u64 x2 = xorshift64(s);
-  const double u1 = fma((double)(unsigned)(x1 >> 32), 0x1p-32, (double)((unsigned)x1 >> 11) * 0x1p-53);
-  const double t = fma((double)(unsigned)(x2 >> 32), 0x1p-26, (double)((unsigned)x2 >> 11) * 0x1p-47);
+  u1 = fma((double)(unsigned)(x1 >> 32), 0x1p-32, (double)((unsigned)x1 >> 11) * 0x1p-53);
+  t = fma((double)(unsigned)(x2 >> 32), 0x1p-26, (double)((unsigned)x2 >> 11) * 0x1p-47);
+}
+__device__ __forceinline__ double policy_transform(double u1, double t) {
   const double k = rint(t);
   double sn, cs;
   tab_sincos_at((t - k) * 0x1.921fb54442d18p-4, cvt_sat_i32(k) & 63, &sn, &cs);
   return nr_sqrt(-2.0 * tab_log(fmax(u1, 1e-300))) * cs;
+}
+__device__ __forceinline__ double policy_normal(u64& s) {
+  double u1, t;
+  policy_uniforms(s, u1, t);
+  return policy_transform(u1, t);
+}
+
+// A double from lane `lane ^ 32`, the other half of the wave (ds_bpermute,
+// which every lane of the wave executes).
+__device__ __forceinline__ double from_other_half(double v, int lane) {
+  const u64 b = __builtin_bit_cast(u64, v);
+  const int addr = (lane ^ 32) << 2;
+  const unsigned lo = (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)(unsigned)b);
+  const unsigned hi = (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)(unsigned)(b >> 32));
+  return __builtin_bit_cast(double, ((u64)hi << 32) | lo);
+}
+
+// The next N normals of the stream in lanes 0..31 (one world each; lanes
+// 32..63 own none), the same values as N calls of policy_normal there. The
+// world's lane draws every pair of uniforms in order; the transforms, the
+// costly part, run two at a time: normal 2j in the world's lane and normal
+// 2j + 1 in lane + 32, whose uniforms and result cross the wave's halves.
+// Lanes 32..63 advance a stream of their own that nothing reads. Every lane
+// of the wave calls it, outside any branch.
+template <int N> __device__ __forceinline__ void policy_normals_paired(u64& s, int lane, double (&n)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; j += 2) {
+    double u1a, ta, u1b = 0.5, tb = 0.0;
+    policy_uniforms(s, u1a, ta);
+    if (j + 1 < N) policy_uniforms(s, u1b, tb);
+    const double pu = from_other_half(u1b, lane), pt = from_other_half(tb, lane);
+    const bool upper = lane >= 32;
+    const double r = policy_transform(upper ? pu : u1a, upper ? pt : ta);
+    n[j] = r;
+    if (j + 1 < N) n[j + 1] = from_other_half(r, lane);
+  }
 }
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
@@ -303,6 +341,13 @@ __device__ __forceinline__ void mfma_layer(const f32x4* __restrict__ w, int lane
 // worlds. For the next layer, k-step s of input block kb uses register s of
 // the previous output tile, i.e. lane j + 16 g supplies neuron 16 kb + 4 g + s
 // of world j; the host lays W out to match (phz_host.cpp, policy_fragments).
+// Inputs with observation noise, the prologue's normals per world.
+template <class P> constexpr int noised_inputs() {
+  int c = 0;
+  for (int i = 0; i < P::NI; i++) c += P::noise[i] != 0.0 ? 1 : 0;
+  return c;
+}
+
 template <class P, class T> __device__ __forceinline__ void policy_wave(const PolicyArgs& a, float* lds) {
   constexpr int NI = P::NI, NO = P::NO, CB = P::CB, NHB = P::NHB, NOB = P::NOB, KU = P::KU, NPD = P::NPD;
   constexpr int WPW = 16 * CB;     // worlds per wave
@@ -317,7 +362,30 @@ template <class P, class T> __device__ __forceinline__ void policy_wave(const Po
 
   // Prologue: world w0 + lane reads its observation row, adds input noise in
   // index order (the noised value is what the history keeps), stages x in LDS.
-  if (lane < WPW) {
+  if constexpr (WPW == 32) {
+    // Half the lanes own a world: the normals' transforms are paired across
+    // the wave's halves (policy_normals_paired).
+    constexpr int NN = noised_inputs<P>();
+    if (own) rs = a.rng[my];
+    float x[16 * KU];
+#pragma unroll
+    for (int i = 0; i < 16 * KU; i++) x[i] = (i < NI && own) ? a.obs[(size_t)i * S + my] : 0.0f;
+    if constexpr (NN > 0) {
+      double nz[NN];
+      policy_normals_paired<NN>(rs, lane, nz);
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+        if (P::noise[i] != 0.0) {
+          x[i] += float(P::noise[i]) * (float)nz[c++];
+          if (own) a.obs[(size_t)i * S + my] = x[i];
+        }
+    }
+    if (lane < WPW) {
+#pragma unroll
+      for (int i = 0; i < 16 * KU; i++) lds[lane * XS + i] = x[i];
+    }
+  } else if (lane < WPW) {
     if (own) rs = a.rng[my];
 #pragma unroll
     for (int i = 0; i < 16 * KU; i++) {
@@ -362,7 +430,10 @@ template <class P, class T> __device__ __forceinline__ void policy_wave(const Po
 
   // Epilogue (policy_reference, policy_pipeline.rs:488-520): every servo gets
   // its base target, then each action k: AR(1) noise, sample, log-prob, the
-  // clamped action onto its slot's base.
+  // clamped action onto its slot's base. With half the lanes owning a world
+  // the actions' normals are drawn first, paired across the halves.
+  double na[NO];
+  if constexpr (WPW == 32) policy_normals_paired<NO>(rs, lane, na);
   if (own) {
     const T* base = (const T*)a.base;
     T* tgt = (T*)a.targets;
@@ -375,7 +446,7 @@ template <class P, class T> __device__ __forceinline__ void policy_wave(const Po
 #pragma unroll
     for (int k = 0; k < NO; k++) {
       const float mk = lds[lane * MS + k];
-      const float zk = rho * a.z[(size_t)k * S + my] + keep * (float)policy_normal(rs);
+      const float zk = rho * a.z[(size_t)k * S + my] + keep * (float)(WPW == 32 ? na[k] : policy_normal(rs));
       a.z[(size_t)k * S + my] = zk;
       const float sd = a.stdv[k];
       const float act = mk + sd * zk;
