@@ -676,11 +676,18 @@ struct AdamArgs {
 // Wave 0 of workgroup 0: the four statistic columns summed over the tiles
 // (lane l takes tiles l, l + 64, ..., then a fixed butterfly across lanes),
 // rounded to f32 as the reference's reduce_stats output is, into the running
-// sums; then the brake, which decides whether the next minibatch runs.
-__device__ void brake(const AdamArgs& a) {
+// sums; then the brake, which decides whether the next minibatch runs. The
+// first two tiles of each lane come preloaded (`pre`, loaded at kernel entry
+// beside the gradient partials); the rest are read here, in the same order.
+constexpr uint32_t kStatPre = 2;
+__device__ void brake(const AdamArgs& a, const double (&pre)[kStatPre][4]) {
   const uint32_t lane = threadIdx.x;
   double s[4] = {0.0, 0.0, 0.0, 0.0};
-  for (uint32_t k = lane; k < a.tiles; k += 64)
+#pragma unroll
+  for (uint32_t r = 0; r < kStatPre; r++)
+    if (lane + 64u * r < a.tiles)
+      for (int c = 0; c < 4; c++) s[c] += pre[r][c];
+  for (uint32_t k = lane + 64u * kStatPre; k < a.tiles; k += 64)
     for (int c = 0; c < 4; c++) s[c] += a.stats_part[(size_t)k * 4 + c];
   for (int c = 0; c < 4; c++)
     for (int off = 32; off > 0; off >>= 1) s[c] += __shfl_xor(s[c], off, 64);
@@ -705,14 +712,29 @@ __device__ void brake(const AdamArgs& a) {
 
 // tang's ModuleAdam step, elementwise (phyz_train.cu:268-288), on the sum of
 // the tile partials. Four lanes share a parameter: lane s sums tiles s, s + 4,
-// ... in eight interleaved chains (eight loads in flight per lane), added as
-// a fixed tree; a fixed xor butterfly gives all four the same total, and the
-// first applies the step.
-__global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
+// ... in eight interleaved chains, chain j taking tiles s + 4j, s + 4j + 32,
+// ..., added as a fixed tree; a fixed xor butterfly gives all four the same
+// total, and the first applies the step. Each lane issues the loads of up to
+// four rounds of its chains (32 partials, 128 tiles) before the first add, so
+// a minibatch of up to 128 tiles per network costs one memory round trip; the
+// grid holds about one wave per SIMD, so the kernel asks for the registers of
+// two resident waves, not the compiler's default of five (which kept only 22
+// of the 32 loads in flight).
+__global__ void __launch_bounds__(kAdamThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) ppo_adam(AdamArgs a) {
   // The stop flag is tested once the partial sums' loads are in flight (as
   // in ppo_tiles); a stopped minibatch's tiles stored nothing, so what they
   // read is never used.
   const int stopped = *a.skip;
+  // Loaded for every lane at a clamped, in-range tile (tiles >= 1); the brake
+  // adds only those of tiles that exist.
+  double pre[kStatPre][4];
+#pragma unroll
+  for (uint32_t r = 0; r < kStatPre; r++) {
+    const uint32_t k = threadIdx.x + 64u * r;
+    const double* sp = a.stats_part + (size_t)(k < a.tiles ? k : 0u) * 4;
+#pragma unroll
+    for (int c = 0; c < 4; c++) pre[r][c] = sp[c];
+  }
   const uint32_t gt = blockIdx.x * kAdamThreads + threadIdx.x;
   const uint32_t t = gt / kAdamLanes, sub = gt % kAdamLanes;
   const bool valid = t < a.n_param[0] + a.n_param[1];
@@ -720,12 +742,23 @@ __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
   const uint32_t q = valid ? (net == 0 ? t : t - a.n_param[0]) : 0u;
   const uint32_t np = a.n_param[net];
   const double* part = a.part[net] + q;
-  constexpr uint32_t kChains = 8;
+  constexpr uint32_t kChains = 8, kRounds = 4;
   double gc[kChains];
 #pragma unroll
   for (uint32_t j = 0; j < kChains; j++) gc[j] = 0.0;
   if (valid) {
     uint32_t k = sub;
+    for (; k + (kRounds * kChains - 1) * kAdamLanes < a.tiles; k += kRounds * kChains * kAdamLanes) {
+      double x[kRounds][kChains];
+#pragma unroll
+      for (uint32_t r = 0; r < kRounds; r++)
+#pragma unroll
+        for (uint32_t j = 0; j < kChains; j++) x[r][j] = part[(size_t)(k + (r * kChains + j) * kAdamLanes) * np];
+#pragma unroll
+      for (uint32_t r = 0; r < kRounds; r++)
+#pragma unroll
+        for (uint32_t j = 0; j < kChains; j++) gc[j] += x[r][j];
+    }
     for (; k + (kChains - 1) * kAdamLanes < a.tiles; k += kChains * kAdamLanes) {
 #pragma unroll
       for (uint32_t j = 0; j < kChains; j++) gc[j] += part[(size_t)(k + j * kAdamLanes) * np];
@@ -738,7 +771,7 @@ __global__ void __launch_bounds__(kAdamThreads) ppo_adam(AdamArgs a) {
     if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
     return;
   }
-  if (blockIdx.x == 0) brake(a);
+  if (blockIdx.x == 0) brake(a, pre);
   double g = ((gc[0] + gc[1]) + (gc[2] + gc[3])) + ((gc[4] + gc[5]) + (gc[6] + gc[7]));
   for (int off = 1; off < kAdamLanes; off <<= 1) g += __shfl_xor(g, off, 64);
   if (!valid || sub != 0) return;
