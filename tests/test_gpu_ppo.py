@@ -138,6 +138,7 @@ def delta_errors(before, want, got):
 @pytest.mark.gpu
 @pytest.mark.parametrize("a_in,c_in,h,act,n,mb", [
     (55, 67, 64, 22, 16384, 4096),   # the reference's timing shape (examples/cuda_train.rs), 4 minibatches
+    (55, 67, 64, 22, 10000, 5000),   # 157 tiles per minibatch: Adam's loads past its first 128 tiles
     (40, 40, 256, 8, 1000, 300),     # widest hidden layer, ragged minibatches: weights read from HBM
     (128, 96, 128, 8, 2000, 500),    # too wide to stage every matrix: one layer at a time through LDS
     (2000, 24, 32, 6, 256, 96),      # inputs so wide that a 16-row tile needs more than 64 KiB of LDS
