@@ -70,6 +70,10 @@ struct Dims {
 };
 
 __host__ __device__ inline uint32_t pad4(uint32_t x) { return (x + 3u) & ~3u; }
+// A tile's row of f64 gradient partials, padded to whole 128-byte lines: the
+// Adam kernel's wave reads 16 consecutive parameters of a row at once, one
+// line when rows start on line boundaries (two when they do not).
+__host__ __device__ inline uint32_t part_stride(uint32_t n_param) { return (n_param + 15u) & ~15u; }
 // LDS row stride of a row of k values, in floats: k rounded up to whole
 // 16-column blocks (the matrix-core loops read 16 columns per step, so the
 // padding must exist and hold zeros), then the first value = 20 (mod 32)
@@ -162,7 +166,7 @@ struct TileArgs {
   const float* w[2];      // row-major f32 mirrors
   const float* wt[2];     // transposed f32 mirrors of the weight matrices
   const float* img[2];    // padded weight images (WImg)
-  double* part[2];        // [tile][n_param] f64 partial gradients
+  double* part[2];        // [tile][part_stride(n_param)] f64 partial gradients
   Dims dims[2];
   uint32_t n_param[2];
   const uint32_t* idx;    // this minibatch's sample indices
@@ -422,7 +426,7 @@ __global__ void __launch_bounds__(kTileThreads) ppo_tiles(TileArgs a) {
   float* WB = lds + L.WB;
   const float* w = a.w[net];
   const float* wt = a.wt[net];
-  double* part = a.part[net] + (size_t)blockIdx.x * a.n_param[net];
+  double* part = a.part[net] + (size_t)blockIdx.x * part_stride(a.n_param[net]);
   const float* x = a.x[net];
   const float* img = a.img[net];
   // A forward layer's weights for the matrix-core loop: the LDS copy
@@ -678,9 +682,10 @@ struct AdamArgs {
 // rounded to f32 as the reference's reduce_stats output is, into the running
 // sums; then the brake, which decides whether the next minibatch runs. The
 // first two tiles of each lane come preloaded (`pre`, loaded at kernel entry
-// beside the gradient partials); the rest are read here, in the same order.
+// beside the gradient partials), and so does the update's state (`s0`); the
+// rest of the tiles are read here, in the same order.
 constexpr uint32_t kStatPre = 2;
-__device__ void brake(const AdamArgs& a, const double (&pre)[kStatPre][4]) {
+__device__ void brake(const AdamArgs& a, const double (&pre)[kStatPre][4], const UpdateState& s0) {
   const uint32_t lane = threadIdx.x;
   double s[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -696,14 +701,16 @@ __device__ void brake(const AdamArgs& a, const double (&pre)[kStatPre][4]) {
   const double ploss = (double)(float)s[0], kl_sum = (double)(float)s[1];
   const double k3_sum = (double)(float)s[2], vloss = (double)(float)s[3];
   const double b = (double)a.b;
-  st->policy_acc += ploss / b;
-  st->value_acc += vloss / b;
-  st->kl_acc += kl_sum;
-  st->kl_rows += a.b;
-  const double rows = (double)(st->kl_rows > 0 ? st->kl_rows : 1);
-  const double reading = (a.kl_mode == PHZ_KL_CUMULATIVE ? fabs(st->kl_acc / rows) : k3_sum / b) / a.kl_scale;
-  st->brake_acc += reading;
-  st->batches += 1;
+  const double kl_acc = s0.kl_acc + kl_sum;
+  const uint64_t kl_rows = s0.kl_rows + a.b;
+  st->policy_acc = s0.policy_acc + ploss / b;
+  st->value_acc = s0.value_acc + vloss / b;
+  st->kl_acc = kl_acc;
+  st->kl_rows = kl_rows;
+  const double rows = (double)(kl_rows > 0 ? kl_rows : 1);
+  const double reading = (a.kl_mode == PHZ_KL_CUMULATIVE ? fabs(kl_acc / rows) : k3_sum / b) / a.kl_scale;
+  st->brake_acc = s0.brake_acc + reading;
+  st->batches = s0.batches + 1;
   if (reading > a.target_kl) {
     st->stopped = 1;
     a.skip[1] = 1;
@@ -737,11 +744,22 @@ __global__ void __launch_bounds__(kAdamThreads) __attribute__((amdgpu_waves_per_
   }
   const uint32_t gt = blockIdx.x * kAdamThreads + threadIdx.x;
   const uint32_t t = gt / kAdamLanes, sub = gt % kAdamLanes;
-  const bool valid = t < a.n_param[0] + a.n_param[1];
-  const int net = valid && t >= a.n_param[0] ? 1 : 0;
-  const uint32_t q = valid ? (net == 0 ? t : t - a.n_param[0]) : 0u;
-  const uint32_t np = a.n_param[net];
+  // Parameter slots: the actor's padded to a multiple of 16, then the
+  // critic's, so that every wave's 16 parameters lie in one network and start
+  // on a 128-byte line of each partial row.
+  const uint32_t lead = part_stride(a.n_param[0]);
+  const int net = t >= lead ? 1 : 0;
+  const uint32_t qt = net == 0 ? t : t - lead;
+  const bool valid = qt < a.n_param[net];
+  const uint32_t q = valid ? qt : 0u;
+  const uint32_t np = part_stride(a.n_param[net]);
   const double* part = a.part[net] + q;
+  // The parameter's master weight and Adam moments, loaded beside the partials
+  // (the four lanes of a parameter read the same words; lanes past the last
+  // parameter read slot 0 and store nothing), and the update's state for the
+  // brake (every workgroup reads the same 48 bytes; workgroup 0 uses them).
+  const double p0 = a.p[net][q], m0 = a.m[net][q], v0 = a.v[net][q];
+  const UpdateState s0 = *a.st;
   constexpr uint32_t kChains = 8, kRounds = 4;
   double gc[kChains];
 #pragma unroll
@@ -771,17 +789,17 @@ __global__ void __launch_bounds__(kAdamThreads) __attribute__((amdgpu_waves_per_
     if (blockIdx.x == 0 && threadIdx.x == 0) a.skip[1] = 1;  // a stopped update stays stopped
     return;
   }
-  if (blockIdx.x == 0) brake(a, pre);
+  if (blockIdx.x == 0) brake(a, pre, s0);
   double g = ((gc[0] + gc[1]) + (gc[2] + gc[3])) + ((gc[4] + gc[5]) + (gc[6] + gc[7]));
   for (int off = 1; off < kAdamLanes; off <<= 1) g += __shfl_xor(g, off, 64);
   if (!valid || sub != 0) return;
   const double gr = (double)(float)g;
-  double x = a.p[net][q];
+  double x = p0;
   const double lr = a.lr[net];
   if (a.wd[net] > 0.0) x = x * (1.0 - lr * a.wd[net]);
   const double b1 = a.beta1[net], b2 = a.beta2[net];
-  const double mt = b1 * a.m[net][q] + (1.0 - b1) * gr;
-  const double vt = b2 * a.v[net][q] + (1.0 - b2) * gr * gr;
+  const double mt = b1 * m0 + (1.0 - b1) * gr;
+  const double vt = b2 * v0 + (1.0 - b2) * gr * gr;
   a.m[net][q] = mt;
   a.v[net][q] = vt;
   const double m_hat = mt / a.bc1[net];
@@ -1080,7 +1098,7 @@ int phz_train_create(phz_net_dims actor, phz_net_dims critic, uint64_t capacity,
          t->alloc(&t->img[n], WImg(t->dims[n]).size, "alloc weights") &&
          t->alloc(&t->p[n], np, "alloc master weights") && t->alloc(&t->m[n], np, "alloc Adam moments") &&
          t->alloc(&t->v[n], np, "alloc Adam moments") &&
-         t->alloc(&t->part[n], (size_t)t->max_tiles * np, "alloc gradient partials") &&
+         t->alloc(&t->part[n], (size_t)t->max_tiles * part_stride(np), "alloc gradient partials") &&
          t->alloc(&t->obs[n], capacity * t->dims[n].n_in, "alloc batch");
   }
   ok = ok && t->alloc(&t->act, capacity * actor.n_out, "alloc batch") && t->alloc(&t->logp_old, capacity, "alloc batch") &&
@@ -1272,7 +1290,7 @@ int run_update(phz_train* t, const uint32_t* const* order, const uint64_t* order
   aa.kl_scale = cfg->kl_scale;
   aa.target_kl = cfg->target_kl;
   aa.st = t->state;
-  const uint32_t n_all = t->n_param[0] + t->n_param[1];
+  const uint32_t n_all = part_stride(t->n_param[0]) + t->n_param[1];  // ppo_adam's parameter slots
   auto tiles_kernel = t->mode == STAGE_ALL ? ppo_tiles<STAGE_ALL>
                       : t->mode == STAGE_LAYER ? ppo_tiles<STAGE_LAYER> : ppo_tiles<STAGE_NONE>;
   uint64_t j = 0;  // minibatch counter within this update
